@@ -1,0 +1,111 @@
+/*
+ * torchmatch_amd.h -- C ABI of the MI355X (gfx950) solver library
+ * libtorchmatch_amd.so.
+ *
+ * Plain pointers and sizes only: every tensor argument is a device pointer
+ * to contiguous row-major data, every size is an element count, and every
+ * call is stream-ordered on the hipStream_t it is given (0 = null stream).
+ * Nothing here allocates, frees or synchronises unless its comment says so.
+ * Return values are TM_* codes below; kernels never raise.
+ *
+ * Reference interfaces replaced (paths relative to the torchmatch
+ * repository root):
+ *   tm_jv_dense_batch_f32   sources/torchmatch/assignment/cuda/dispatch.cu:137-177
+ *                           (jonker_dense_batch_cuda) together with
+ *                           assignment/cuda/cuda_common.cuh:215-284
+ *                           (compute_inf_sentinel, rewrite_inf_to_sentinel);
+ *                           results follow the CPU op
+ *                           assignment/cpu/ops.cpp:176-289 bit for bit.
+ *   tm_sinkhorn_f32         sources/torchmatch/transport/matrix/_log_sinkhorn.py:136-221
+ *                           (log_sinkhorn_plan) and
+ *                           transport/matrix/_unbalanced_sinkhorn.py:30-103
+ *                           (unbalanced_sinkhorn_plan).
+ */
+#ifndef TORCHMATCH_AMD_H
+#define TORCHMATCH_AMD_H
+
+#include <hip/hip_runtime_api.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Return codes. */
+enum {
+    TM_OK = 0,
+    TM_ERR_INVALID_ARGUMENT = 1, /* negative size, null pointer, bad scalar */
+    TM_ERR_UNSUPPORTED_SHAPE = 2,/* shape beyond what the kernels handle */
+    TM_ERR_WORKSPACE = 3,        /* workspace missing or too small */
+    TM_ERR_LAUNCH = 4,           /* a kernel launch failed (hipGetLastError) */
+    TM_ERR_NAN = 5,              /* input holds NaN (reported by tm_jv_check_status) */
+    TM_ERR_NEG_INF = 6,          /* input holds -inf (reported by tm_jv_check_status) */
+    TM_ERR_HIP = 7,              /* a HIP runtime call failed */
+    TM_ERR_INTERNAL = 8          /* a kernel's iteration guard tripped (a bug) */
+};
+
+/* Status word bits written by tm_jv_dense_batch_f32 into *d_status. */
+enum {
+    TM_JV_FLAG_NAN = 1u,
+    TM_JV_FLAG_NEG_INF = 2u,
+    TM_JV_FLAG_POS_INF = 4u,
+    TM_JV_FLAG_ANY_FINITE = 8u
+};
+
+/* ---- batched Jonker-Volgenant (assignment::jonker_dense_batch) -------- */
+
+/* Largest K = max(N, M) tm_jv_dense_batch_f32 accepts. */
+int32_t tm_jv_max_k(void);
+
+/* Device workspace tm_jv_dense_batch_f32 needs for a (B, N, M) batch. */
+size_t tm_jv_workspace_bytes(int64_t B, int32_t N, int32_t M);
+
+/* Solve B independent (N, M) float32 assignment problems.
+ *   costs      device, (B, N, M) contiguous; +inf marks a forbidden pair
+ *   out        device, (B, N) int64: row -> column, -1 for rows matched into
+ *              padding columns (N > M); identical to the reference CPU op
+ *   workspace  device, >= tm_jv_workspace_bytes(B, N, M), any contents
+ *   d_status   device, two uint32: [0] receives TM_JV_FLAG_* for the whole
+ *              batch, [1] is non-zero if a solve hit its iteration guard
+ * The +inf sentinel (max finite + 1) * (K + 1) is computed on the device over
+ * the whole batch, as the reference does; no host round trip happens inside.
+ * If the batch holds NaN or -inf, `out` is filled with -1 and the flag is set:
+ * call tm_jv_check_status to turn the flags into TM_ERR_NAN / TM_ERR_NEG_INF.
+ * B == 0, N == 0 or M == 0 launches nothing (the caller fills -1). */
+int tm_jv_dense_batch_f32(const float *costs, int64_t B, int32_t N, int32_t M, int64_t *out,
+                          void *workspace, size_t workspace_bytes, uint32_t *d_status,
+                          hipStream_t stream);
+
+/* Copy the two status words to the host and synchronise `stream` (the only
+ * host sync of the JV path, mirroring the reference's validation readback,
+ * cuda_common.cuh:241-249).  Returns TM_OK, TM_ERR_NAN, TM_ERR_NEG_INF,
+ * TM_ERR_INTERNAL or TM_ERR_HIP. */
+int tm_jv_check_status(const uint32_t *d_status, hipStream_t stream);
+
+/* ---- log-domain Sinkhorn (transport::log_sinkhorn / unbalanced_sinkhorn) */
+
+/* Device workspace tm_sinkhorn_f32 needs. */
+size_t tm_sinkhorn_workspace_bytes(int64_t B, int64_t N, int64_t M);
+
+/* Run the log-domain Sinkhorn iteration of the reference on a (B, N, M)
+ * float32 cost and write the log transport plan.
+ *   cost       device (B, N, M); +inf = forbidden pair; no NaN / -inf
+ *   a, b       device marginals (B, N) and (B, M), non-negative
+ *   eps_sched  HOST array of n_iter float64 epsilons (the reference schedule)
+ *   rho        <= 0: balanced (log_sinkhorn); > 0: unbalanced with KL
+ *              penalty rho (damping 1 / (1 + eps / rho) per step)
+ *   log_plan   device (B, N, M) output, may be NULL to skip the plan
+ *   log_u, log_v  device (B, N), (B, M) outputs: the final scaling
+ *              potentials (f = -eps * log_u, g = -eps * log_v)
+ *   workspace  device, >= tm_sinkhorn_workspace_bytes(B, N, M) */
+int tm_sinkhorn_f32(const float *cost, const float *a, const float *b, int64_t B, int64_t N,
+                    int64_t M, const double *eps_sched, int32_t n_iter, double rho,
+                    float *log_plan, float *log_u, float *log_v, void *workspace,
+                    size_t workspace_bytes, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TORCHMATCH_AMD_H */

@@ -1,0 +1,32 @@
+"""Shared pytest setup.
+
+Markers:
+  gpu -- needs a ROCm device (MI355X); run with ``-m gpu`` on the GPU box.
+
+The repository root is put on sys.path so ``oracle`` (the parity checkers)
+and ``torchmatch_amd`` import from the tree.
+"""
+
+from __future__ import annotations
+
+import sys
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+if str(ROOT) not in sys.path:
+    sys.path.insert(0, str(ROOT))
+
+
+def pytest_configure(config):
+    config.addinivalue_line("markers", "gpu: needs a ROCm GPU (gfx950)")
+
+
+@pytest.fixture(scope="session")
+def device():
+    import torch
+
+    if not torch.cuda.is_available():
+        pytest.skip("no ROCm device visible")
+    return torch.device("cuda:0")

@@ -1,0 +1,148 @@
+"""Pins the JV oracle (oracle/jv_oracle.c) before anything is compared to it.
+
+* against the reference's own solver compiled from its source
+  (oracle/_ref/libjv_ref.so, built by oracle/Makefile) on random, tied and
+  masked batches, square and rectangular;
+* against the committed golden fixtures (written from that same reference
+  build by tests/golden/make_jv_golden.py);
+* against scipy.optimize.linear_sum_assignment (optimal total cost) and
+  brute force over permutations (K <= 7), which pin optimality independently
+  of the reference;
+* against the reference tests' known answers (test_lap_inf_mask.py:50-126)
+  and the sentinel rule (ops.cpp:67-93).
+"""
+
+from __future__ import annotations
+
+import itertools
+import zlib
+import json
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import jv
+from torchmatch_amd import workloads
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+
+
+def _cost_total(c: np.ndarray, mapping: np.ndarray) -> np.ndarray:
+    b, n, _ = c.shape
+    valid = mapping >= 0
+    picked = np.take_along_axis(c, np.clip(mapping, 0, None)[..., None], axis=2)[..., 0]
+    return np.where(valid, picked, 0.0).astype(np.float64).sum(axis=1)
+
+
+def test_known_answers_from_reference_tests():
+    inf = np.inf
+    c = np.array([[[1.0, inf], [inf, 1.0]], [[2.0, inf], [inf, 3.0]]], dtype=np.float32)
+    assert jv.jv_dense_batch(c).tolist() == [[0, 1], [0, 1]]
+    with pytest.raises(jv.OracleError, match="NaN"):
+        jv.jv_dense_batch(np.array([[[1.0, 2.0], [3.0, 4.0]], [[1.0, np.nan], [3.0, 4.0]]]))
+    with pytest.raises(jv.OracleError, match="-inf"):
+        jv.jv_dense_batch(np.array([[[1.0, 2.0], [3.0, 4.0]], [[1.0, -inf], [3.0, 4.0]]]))
+
+
+def test_empty_shapes_give_minus_one():
+    assert jv.jv_dense_batch(np.zeros((0, 3, 3), np.float32)).shape == (0, 3)
+    out = jv.jv_dense_batch(np.zeros((2, 3, 0), np.float32))
+    assert out.shape == (2, 3) and (out == -1).all()
+
+
+def test_sentinel_rule():
+    c = np.array([[[1.5, np.inf], [np.inf, -2.0]]], dtype=np.float32)
+    assert jv.sentinel(c) == np.float32((np.float32(1.5) + np.float32(1)) * np.float32(3))
+    assert jv.sentinel(np.full((1, 2, 3), np.inf, np.float32)) == 1.0
+
+
+@pytest.mark.skipif(not jv.ref_available(), reason="reference build (oracle/_ref) absent")
+@pytest.mark.parametrize("kind", ["uniform", "tied", "masked", "tied_masked"])
+def test_oracle_matches_reference_build(kind):
+    rng = np.random.default_rng(zlib.crc32(kind.encode()))
+    for _ in range(25):
+        b, n, m = 32, int(rng.integers(1, 48)), int(rng.integers(1, 48))
+        if kind == "uniform":
+            c = rng.random((b, n, m), dtype=np.float32)
+        elif kind == "tied":
+            c = rng.integers(0, 3, (b, n, m)).astype(np.float32)
+        elif kind == "masked":
+            c = rng.random((b, n, m), dtype=np.float32)
+            c[rng.random((b, n, m)) < 0.6] = np.inf
+        else:
+            c = rng.integers(0, 2, (b, n, m)).astype(np.float32)
+            c[rng.random((b, n, m)) < 0.3] = np.inf
+        np.testing.assert_array_equal(jv.jv_dense_batch(c), jv.ref_jv_dense_batch(c))
+
+
+def _golden_cases():
+    index = json.loads((GOLDEN / "jv_golden.json").read_text())
+    return sorted(index.items())
+
+
+@pytest.mark.parametrize(("name", "meta"), _golden_cases(), ids=[n for n, _ in _golden_cases()])
+def test_oracle_matches_golden(name, meta):
+    if meta["shape"][1] * meta["shape"][2] > 100_000:
+        pytest.skip("large case: covered on the GPU against the fixture directly")
+    cost = getattr(workloads, meta["generator"])(**meta["kwargs"])
+    assert workloads.sha256(cost) == meta["sha256"], "input generator drifted"
+    want = np.load(GOLDEN / meta["file"])["mapping"].astype(np.int64)
+    np.testing.assert_array_equal(jv.jv_dense_batch(cost.numpy()), want)
+
+
+def test_optimal_cost_against_scipy():
+    sp = pytest.importorskip("scipy.optimize")
+    rng = np.random.default_rng(7)
+    for n, m in [(16, 16), (20, 33), (33, 20), (64, 64)]:
+        c = rng.random((16, n, m), dtype=np.float32)
+        got = _cost_total(c, jv.jv_dense_batch(c))
+        for b in range(c.shape[0]):
+            r, k = sp.linear_sum_assignment(c[b].astype(np.float64))
+            assert got[b] == pytest.approx(float(c[b][r, k].astype(np.float64).sum()), abs=1e-4)
+
+
+def test_optimal_cost_brute_force():
+    rng = np.random.default_rng(11)
+    for k in range(1, 8):
+        c = rng.integers(0, 5, (20, k, k)).astype(np.float32)
+        got = _cost_total(c, jv.jv_dense_batch(c))
+        for b in range(c.shape[0]):
+            best = min(
+                sum(float(c[b, i, p[i]]) for i in range(k))
+                for p in itertools.permutations(range(k))
+            )
+            assert got[b] == best
+
+
+def test_mapping_is_partial_permutation():
+    c = workloads.jv_uniform(64, 20, 30, seed=3).numpy()
+    out = jv.jv_dense_batch(c)
+    for row in out:
+        assert len(set(row.tolist())) == len(row)
+        assert ((row >= 0) & (row < 30)).all()
+    c = workloads.jv_uniform(64, 30, 20, seed=3).numpy()
+    out = jv.jv_dense_batch(c)
+    assert ((out >= 0).sum(axis=1) == 20).all()
+
+
+def test_planted_mistake_is_caught():
+    """A transposed operand must not pass the brute-force check (sanity of the pin)."""
+    rng = np.random.default_rng(5)
+    c = rng.random((50, 5, 5), dtype=np.float32)
+    wrong = jv.jv_dense_batch(np.ascontiguousarray(c.transpose(0, 2, 1)))
+    right = jv.jv_dense_batch(c)
+    assert not np.array_equal(_cost_total(c, wrong), _cost_total(c, right))
+
+
+def test_counted_run_matches_plain_run():
+    c = workloads.jv_uniform(16, 64, 64, seed=9).numpy()
+    out, counts = jv.jv_dense_batch_counted(c)
+    np.testing.assert_array_equal(out, jv.jv_dense_batch(c))
+    assert (counts[:, 0] >= 64 * 64).all()
+
+
+def test_torch_input_roundtrip():
+    c = torch.rand(4, 6, 6, generator=torch.Generator().manual_seed(0))
+    assert jv.jv_dense_batch(c.numpy()).shape == (4, 6)

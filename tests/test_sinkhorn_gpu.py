@@ -1,0 +1,172 @@
+"""Parity of the gfx950 Sinkhorn kernels with the reference computation.
+
+The oracle (oracle/sinkhorn.py) is the reference's torch code restated op for
+op on CPU.  Tolerance (north star: 1e-5 relative, max-abs reported):
+
+* plan  P = exp(log_plan):  max|P - P_ref| / max|P_ref|        <= 1e-5
+* potentials f, g:          max|f - f_ref| / max(1, max|f_ref|) <= 1e-5
+* -inf pattern of the log plan identical (forbidden cells, empty rows).
+
+float32 itself drifts ~1e-6 from float64 on these problems (CPU oracle at
+both precisions), so 1e-5 leaves room only for summation order and exp/log
+rounding.  Full-size configurations are checked through properties that do
+not need the CPU oracle: marginal error after convergence and the potential
+reconstruction identity.
+"""
+
+from __future__ import annotations
+
+import math
+
+import pytest
+import torch
+
+import torchmatch_amd  # noqa: F401
+from oracle import sinkhorn as sk
+from torchmatch_amd import workloads
+from torchmatch_amd.transport.matrix import Backend, marginal_error, solve
+
+pytestmark = pytest.mark.gpu
+
+REL_TOL = 1e-5
+
+
+def _rel(x: torch.Tensor, ref: torch.Tensor) -> float:
+    x, ref = x.double().cpu(), ref.double().cpu()
+    fin = torch.isfinite(ref)
+    assert torch.equal(fin, torch.isfinite(x)), "finite pattern differs"
+    if not fin.any():
+        return 0.0
+    return ((x[fin] - ref[fin]).abs().max() / max(1.0, ref[fin].abs().max().item())).item()
+
+
+def _plan_rel(log_plan: torch.Tensor, ref_log_plan: torch.Tensor) -> float:
+    assert torch.equal(torch.isneginf(log_plan.cpu()), torch.isneginf(ref_log_plan)), \
+        "-inf pattern differs"
+    p, q = log_plan.double().cpu().exp(), ref_log_plan.double().exp()
+    return ((p - q).abs().max() / q.abs().max()).item()
+
+
+CASES = [
+    # B, N, M, eps, n_iter
+    (2, 64, 64, 0.1, 50),
+    (2, 256, 256, 0.05, 200),
+    (3, 300, 200, 0.1, 100),
+    (1, 130, 517, 0.05, 80),
+    (2, 1024, 1024, 0.05, 60),
+]
+
+
+@pytest.mark.parametrize(("B", "N", "M", "eps", "n_iter"), CASES)
+def test_log_sinkhorn_matches_oracle(B, N, M, eps, n_iter, device):
+    cost = workloads.sinkhorn_points(B, N, M, 8, seed=N + M)
+    a = workloads.dirichlet(B, N, 1.0, seed=1)
+    b = workloads.dirichlet(B, M, 1.0, seed=2)
+    print(f"log_sinkhorn case {(B, N, M, eps, n_iter)}", flush=True)
+    ref_plan, ref_f, ref_g, _, _ = sk.log_sinkhorn_plan(cost, eps=eps, n_iter=n_iter, a=a, b=b)
+    plan, f, g = solve(cost.to(device), reg=eps, n_iter=n_iter, a=a.to(device), b=b.to(device),
+                       unpack=True)
+    torch.cuda.synchronize()
+    pr, fr, gr = _plan_rel(plan, ref_plan), _rel(f, ref_f), _rel(g, ref_g)
+    print(f"  plan rel {pr:.3e}  f rel {fr:.3e}  g rel {gr:.3e}", flush=True)
+    assert pr <= REL_TOL and fr <= REL_TOL and gr <= REL_TOL
+
+
+@pytest.mark.parametrize(("B", "N", "M", "eps", "n_iter", "rho"), [
+    (2, 64, 80, 0.1, 60, 1.0),
+    (1, 500, 300, 0.02, 100, 1.0),
+    (2, 256, 256, 0.05, 100, 0.5),
+])
+def test_unbalanced_matches_oracle(B, N, M, eps, n_iter, rho, device):
+    cost = workloads.sinkhorn_points(B, N, M, 8, seed=3)
+    a = workloads.dirichlet(B, N, 1.0, seed=4)
+    b = workloads.dirichlet(B, M, 1.3, seed=5)
+    ref_plan, _, _ = sk.unbalanced_sinkhorn_plan(cost, eps=eps, n_iter=n_iter, rho=rho, a=a, b=b)
+    plan = torch.ops.transport.unbalanced_sinkhorn(
+        cost.to(device), eps, n_iter, rho, a.to(device), b.to(device)
+    )
+    pr = _plan_rel(plan, ref_plan)
+    print(f"unbalanced {(B, N, M, eps, n_iter, rho)} plan rel {pr:.3e}", flush=True)
+    assert pr <= REL_TOL
+
+
+def test_forbidden_cells_rows_and_columns(device):
+    cost = workloads.sinkhorn_points(2, 40, 30, 4, seed=9)
+    cost[0, 3, :] = float("inf")         # all-+inf row
+    cost[1, :, 7] = float("inf")         # all-+inf column
+    cost[0, 5, 2] = float("inf")
+    cost[1, 9, 11] = float("inf")
+    a = workloads.uniform_marginal(2, 40)
+    b = workloads.uniform_marginal(2, 30)
+    ref_plan, ref_f, ref_g, _, _ = sk.log_sinkhorn_plan(cost, eps=0.1, n_iter=100, a=a, b=b)
+    plan, f, g = solve(cost.to(device), reg=0.1, n_iter=100, a=a.to(device), b=b.to(device),
+                       unpack=True)
+    assert torch.isneginf(plan[0, 3]).all() and torch.isneginf(plan[1, :, 7]).all()
+    assert not torch.isnan(plan).any()
+    assert _plan_rel(plan, ref_plan) <= REL_TOL
+    assert _rel(f, ref_f) <= REL_TOL and _rel(g, ref_g) <= REL_TOL
+
+
+def test_mask_argument_and_op_entry(device):
+    cost = workloads.sinkhorn_points(2, 50, 60, 8, seed=10)
+    mask = torch.rand(2, 50, 60, generator=torch.Generator().manual_seed(0)) > 0.2
+    a = workloads.uniform_marginal(2, 50)
+    b = workloads.uniform_marginal(2, 60)
+    ref_plan = sk.log_sinkhorn_plan(cost.masked_fill(~mask, float("inf")), eps=0.1, n_iter=70,
+                                    a=a, b=b)[0]
+    plan = torch.ops.transport.log_sinkhorn(cost.to(device), 0.1, 70, a.to(device),
+                                            b.to(device), mask.to(device))
+    assert _plan_rel(plan, ref_plan) <= REL_TOL
+
+
+def test_eps_scaling_schedule(device):
+    cost = workloads.sinkhorn_points(1, 120, 90, 8, seed=12)
+    a = workloads.uniform_marginal(1, 120)
+    b = workloads.uniform_marginal(1, 90)
+    ref_plan = sk.log_sinkhorn_plan(cost, eps=0.05, n_iter=120, a=a, b=b, scaling=0.7)[0]
+    plan = solve(cost[0].to(device), reg=0.05, n_iter=120, scaling=0.7)
+    assert _plan_rel(plan.unsqueeze(0), ref_plan) <= REL_TOL
+
+
+def test_uniform_cost_gives_uniform_plan(device):
+    """test_transport_log_sinkhorn.py:12-21 (closed form)."""
+    cost = torch.ones(4, 4, device=device)
+    plan = solve(cost, reg=0.1, n_iter=100).exp()
+    assert torch.allclose(plan, torch.full_like(plan, 1 / 16), atol=1e-6)
+
+
+def test_unbalanced_1x1_closed_form(device):
+    """test_transport_unbalanced_sinkhorn.py:59-87, at float32 precision."""
+    a0, b0, c00, rho, eps = 0.7, 0.9, 0.3, 0.5, 0.1
+    expected = (rho * (math.log(a0) + math.log(b0)) - c00) / (eps + 2.0 * rho)
+    log_plan = solve(
+        torch.tensor([[[c00]]], device=device), backend=Backend.UNBALANCED_SINKHORN,
+        reg=eps, n_iter=2000, rho=rho,
+        a=torch.tensor([[a0]], device=device), b=torch.tensor([[b0]], device=device),
+    )
+    assert abs(log_plan.item() - expected) < 1e-6
+
+
+def test_c4_shape_converges(device):
+    """C4 at full size (16, 2048, 2048), eps 0.05, 200 iterations: marginals."""
+    cost = workloads.sinkhorn_points(16, 2048, 2048, 8, seed=0).to(device)
+    a = torch.full((16, 2048), 1 / 2048, device=device)
+    plan = solve(cost, reg=0.05, n_iter=200, a=a, b=a)
+    row_err, col_err = marginal_error(plan, a, a)
+    print(f"C4 marginal error rows {row_err:.3e} cols {col_err:.3e}", flush=True)
+    assert col_err < 1e-6          # the last half-step fixes the columns
+    assert row_err < 5e-4
+    assert not torch.isnan(plan).any()
+
+
+def test_potentials_reconstruct_plan(device):
+    """log_plan = (-f - C - g) / eps (balanced, by construction of the plan)."""
+    cost = workloads.sinkhorn_points(2, 300, 400, 8, seed=13)
+    plan, f, g = solve(cost.to(device), reg=0.1, n_iter=50, unpack=True)
+    rec = (-f[:, :, None] - cost.to(device) - g[:, None, :]) / 0.1
+    assert (rec - plan).abs().max().item() < 1e-3
+
+
+def test_cpu_tensor_rejected():
+    with pytest.raises(ValueError, match="ROCm"):
+        solve(torch.rand(3, 3), reg=0.1, n_iter=5)

@@ -1,0 +1,72 @@
+"""Load the in-tree native extension and make sure the op schemas exist.
+
+``_C.so`` carries the device kernels of ``assignment::jonker_dense_batch``
+(CUDA dispatch key -- ROCm tensors report device type ``"cuda"``) and the
+private ``torchmatch_amd::sinkhorn`` op.  The schema of
+``assignment::jonker_dense_batch`` is owned by whoever defines the
+``assignment`` library: the reference CPU extension when it is loaded
+(``assignment/cpu/ops.cpp:486-495``), otherwise this module, with the same
+text and the same fake kernel as ``assignment/_loader.py:160-169``.
+
+There is no fallback: if the extension is missing, :func:`load` raises.
+"""
+
+from __future__ import annotations
+
+from pathlib import Path
+
+import torch
+
+_PKG = Path(__file__).resolve().parent
+OPS_SO = _PKG / "_C.so"
+CABI_SO = _PKG / "lib" / "libtorchmatch_amd.so"
+
+JONKER_DENSE_BATCH_SCHEMA = "jonker_dense_batch(Tensor costs) -> Tensor"
+
+_state: dict[str, object] = {"loaded": False, "libs": []}
+
+
+class ExtensionMissingError(RuntimeError):
+    """The gfx950 extension was not built (run ``python -m torchmatch_amd._build``)."""
+
+
+def _has_op(namespace: str, name: str) -> bool:
+    try:
+        getattr(getattr(torch.ops, namespace), name)
+    except (AttributeError, RuntimeError):
+        return False
+    return True
+
+
+def _ensure_assignment_schema() -> None:
+    if _has_op("assignment", "jonker_dense_batch"):
+        return
+    lib = torch.library.Library("assignment", "FRAGMENT")  # noqa: TOR901
+    lib.define(JONKER_DENSE_BATCH_SCHEMA)
+    _state["libs"].append(lib)  # keep the registration alive
+
+    @torch.library.register_fake("assignment::jonker_dense_batch", lib=lib)
+    def _fake(costs: torch.Tensor) -> torch.Tensor:
+        torch._check(costs.dim() == 3, lambda: "costs must be 3D (B, N, M)")
+        return costs.new_empty(costs.size(0), costs.size(1), dtype=torch.long)
+
+
+def load() -> None:
+    """Load ``_C.so`` once; raise :class:`ExtensionMissingError` if absent."""
+    if _state["loaded"]:
+        return
+    if not OPS_SO.exists() or not CABI_SO.exists():
+        msg = (
+            f"torchmatch_amd native extension not found ({OPS_SO}, {CABI_SO}); "
+            "build it with `python -m torchmatch_amd._build` -- there is no "
+            "non-native fallback"
+        )
+        raise ExtensionMissingError(msg)
+    _ensure_assignment_schema()
+    torch.ops.load_library(str(OPS_SO))
+    _state["loaded"] = True
+
+
+def native_library_paths() -> list[str]:
+    """Paths of the native libraries this package loads (for diagnostics)."""
+    return [str(OPS_SO), str(CABI_SO)]

@@ -1,0 +1,745 @@
+// jv_batch.hip -- batched Jonker-Volgenant (dense, float32) for gfx950.
+//
+// Reproduces the int64 row->col mapping of torchmatch's CPU
+// `assignment::jonker_dense_batch` bit for bit:
+//   sentinel + padding      sources/torchmatch/assignment/cpu/ops.cpp:67-93,176-289
+//   solver                  sources/torchmatch/assignment/cpu/jonker_dense_flat.h:27-274
+//
+// Launch structure (one stream, no host round trip between kernels):
+//   1. jv_stats_kernel     -- grid-stride pass over all B*N*M cells; each block
+//                             writes {max finite, min finite, flags} to its own
+//                             slot of a small workspace (no atomics, no memset).
+//   2. jv_solve_kernel     -- one problem per 64-lane workgroup.  The block
+//                             folds the per-block partials into the batch-global
+//                             sentinel (max_finite+1)*(K+1), loads its K x K tile
+//                             (padding 0, +inf -> sentinel) into LDS and into
+//                             registers (lane j keeps column j), and runs the
+//                             solver with one column / one cols[] position per
+//                             lane.  Block 0 publishes the NaN / -inf flags.
+//
+// The wave-parallel solver follows the reference step by step; parallelism is
+// only across columns, never across steps:
+//   * column reduction: lane-serial column minima, LDS atomics for the
+//     reverse-order claim, one wave-min per unique row for reduction transfer;
+//   * augmenting row reduction: one wave-wide (min, second min) per step, the
+//     first-index tie rule recovered with ballots;
+//   * augmenting paths: lane p holds cols[p] and the state of that column.
+//     find_dense / scan_dense swap cols[] entries in a fixed order; the swap
+//     positions are found with a prefix-min scan and ballots, and the swaps are
+//     replayed in that order, which gives exactly the sequential layout.
+// Inputs whose magnitudes reach 1e15 (where the solver's LARGE = 1e18
+// guards could become active) take a lane-serial transcription of the same
+// algorithm instead, so the mapping stays exact for every finite input.
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdint.h>
+
+#include "jv_batch.h"
+#include "wave.h"
+
+namespace tmamd {
+namespace {
+
+constexpr float kLarge = 1e18f;          // jonker_dense_flat.h:22-23
+constexpr float kFastRange = 1e15f;      // wave path valid for |cost| <= this
+constexpr int kTile = 64;                // K <= 64 path
+constexpr int kStatsBlock = 256;
+
+__device__ __forceinline__ float finf() { return __int_as_float(0x7f800000); }
+
+// ---------------------------------------------------------------------------
+// 1. statistics pass
+// ---------------------------------------------------------------------------
+__global__ void __launch_bounds__(kStatsBlock)
+jv_stats_kernel(const float *__restrict__ costs, int64_t n, JvStats *__restrict__ partial,
+                uint32_t *__restrict__ status) {
+    if (blockIdx.x == 0 && threadIdx.x == 0)
+        status[1] = 0;  // internal-error word, raised by jv_solve_kernel
+    float mx = -finf(), mn = finf();
+    uint32_t flags = 0;
+    const int64_t stride = (int64_t)gridDim.x * kStatsBlock;
+    const int64_t n4 = ((uintptr_t)costs % 16 == 0) ? n / 4 : 0;
+    const float4 *c4 = reinterpret_cast<const float4 *>(costs);
+    auto visit = [&](float x) {
+        if (isnan(x)) {
+            flags |= kJvFlagNan;
+        } else if (isinf(x)) {
+            flags |= (x < 0.f) ? kJvFlagNegInf : kJvFlagPosInf;
+        } else {
+            flags |= kJvFlagAnyFinite;
+            mx = fmaxf(mx, x);
+            mn = fminf(mn, x);
+        }
+    };
+    for (int64_t k = (int64_t)blockIdx.x * kStatsBlock + threadIdx.x; k < n4; k += stride) {
+        const float4 q = c4[k];
+        visit(q.x);
+        visit(q.y);
+        visit(q.z);
+        visit(q.w);
+    }
+    for (int64_t k = n4 * 4 + (int64_t)blockIdx.x * kStatsBlock + threadIdx.x; k < n;
+         k += stride)
+        visit(costs[k]);
+
+    mx = wave_max(mx);
+    mn = wave_min(mn);
+    // OR of the flags across the wave
+    uint32_t f = 0;
+#pragma unroll
+    for (int bit = 0; bit < 4; ++bit)
+        if (ballot((flags >> bit) & 1u))
+            f |= 1u << bit;
+
+    __shared__ float s_mx[kStatsBlock / 64], s_mn[kStatsBlock / 64];
+    __shared__ uint32_t s_f[kStatsBlock / 64];
+    const int w = threadIdx.x / 64;
+    if (lane_id() == 0) {
+        s_mx[w] = mx;
+        s_mn[w] = mn;
+        s_f[w] = f;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int k = 1; k < kStatsBlock / 64; ++k) {
+            mx = fmaxf(mx, s_mx[k]);
+            mn = fminf(mn, s_mn[k]);
+            f |= s_f[k];
+        }
+        partial[blockIdx.x].max_finite = mx;
+        partial[blockIdx.x].min_finite = mn;
+        partial[blockIdx.x].flags = f;
+        partial[blockIdx.x].pad = 0;
+    }
+}
+
+// Fold the per-block partials (uniform result in every lane of the wave).
+__device__ __forceinline__ void fold_stats(const JvStats *__restrict__ partial, int n_partial,
+                                           float &mx, float &mn, uint32_t &flags) {
+    mx = -finf();
+    mn = finf();
+    uint32_t f = 0;
+    for (int k = lane_id(); k < n_partial; k += 64) {
+        mx = fmaxf(mx, partial[k].max_finite);
+        mn = fminf(mn, partial[k].min_finite);
+        f |= partial[k].flags;
+    }
+    mx = wave_max(mx);
+    mn = wave_min(mn);
+    flags = 0;
+#pragma unroll
+    for (int bit = 0; bit < 4; ++bit)
+        if (ballot((f >> bit) & 1u))
+            flags |= 1u << bit;
+}
+
+// ---------------------------------------------------------------------------
+// 2a. lane-serial transcription (exact for any finite input; slow)
+// ---------------------------------------------------------------------------
+struct SerialScratch {
+    int32_t x[kTile], y[kTile], fr[kTile], pred[kTile], cols[kTile];
+    float v[kTile], d[kTile];
+    char unique[kTile];
+};
+
+__device__ uint32_t serial_find_tied(uint32_t n, uint32_t lo, const float *d, int32_t *cols) {
+    uint32_t hi = lo + 1;
+    float best = d[cols[lo]];
+    for (uint32_t k = lo + 1; k < n; ++k) {
+        const int32_t j = cols[k];
+        const float dj = d[j];
+        if (!(dj <= best))
+            continue;
+        if (dj < best) {
+            best = dj;
+            hi = lo;
+        }
+        cols[k] = cols[hi];
+        cols[hi] = j;
+        ++hi;
+    }
+    return hi;
+}
+
+__device__ int32_t serial_scan(uint32_t n, const float *c, uint32_t *plo, uint32_t *phi,
+                               SerialScratch &s) {
+    uint32_t lo = *plo, hi = *phi;
+    while (lo != hi) {
+        const int32_t jp = s.cols[lo++];
+        const int32_t i = s.y[jp];
+        const float level = s.d[jp];
+        const float *row = c + i * kTile;
+        const float h = row[jp] - s.v[jp] - level;
+        for (uint32_t k = hi; k < n; ++k) {
+            const int32_t j = s.cols[k];
+            const float r = row[j] - s.v[j] - h;
+            if (!(r < s.d[j]))
+                continue;
+            s.d[j] = r;
+            s.pred[j] = i;
+            if (r == level) {
+                if (s.y[j] < 0)
+                    return j;
+                s.cols[k] = s.cols[hi];
+                s.cols[hi] = j;
+                ++hi;
+            }
+        }
+    }
+    *plo = lo;
+    *phi = hi;
+    return -1;
+}
+
+__device__ void serial_solve(uint32_t n, const float *c, SerialScratch &s) {
+    for (uint32_t k = 0; k < n; ++k) {
+        s.unique[k] = 1;
+        s.x[k] = -1;
+        s.v[k] = kLarge;
+        s.y[k] = 0;
+    }
+    for (uint32_t i = 0; i < n; ++i)
+        for (uint32_t j = 0; j < n; ++j)
+            if (c[i * kTile + j] < s.v[j]) {
+                s.v[j] = c[i * kTile + j];
+                s.y[j] = (int32_t)i;
+            }
+    for (int32_t j = (int32_t)n - 1; j >= 0; --j) {
+        const int32_t i = s.y[j];
+        if (s.x[i] < 0) {
+            s.x[i] = j;
+        } else {
+            s.unique[i] = 0;
+            s.y[j] = -1;
+        }
+    }
+    int32_t n_free = 0;
+    for (uint32_t i = 0; i < n; ++i) {
+        if (s.x[i] < 0) {
+            s.fr[n_free++] = (int32_t)i;
+        } else if (s.unique[i]) {
+            const int32_t own = s.x[i];
+            float mn = kLarge;
+            for (uint32_t j = 0; j < n; ++j) {
+                if ((int32_t)j == own)
+                    continue;
+                const float r = c[i * kTile + j] - s.v[j];
+                if (r < mn)
+                    mn = r;
+            }
+            s.v[own] -= mn;
+        }
+    }
+    for (int round = 0; n_free > 0 && round < 2; ++round) {
+        uint32_t cur = 0, rr = 0;
+        int32_t still = 0;
+        while (cur < (uint32_t)n_free) {
+            ++rr;
+            const int32_t fi = s.fr[cur++];
+            const float *row = c + fi * kTile;
+            int32_t j1 = 0, j2 = -1;
+            float u1 = row[0] - s.v[0], u2 = kLarge;
+            for (uint32_t j = 1; j < n; ++j) {
+                const float r = row[j] - s.v[j];
+                if (!(r < u2))
+                    continue;
+                if (r >= u1) {
+                    u2 = r;
+                    j2 = (int32_t)j;
+                } else {
+                    u2 = u1;
+                    j2 = j1;
+                    u1 = r;
+                    j1 = (int32_t)j;
+                }
+            }
+            int32_t i0 = s.y[j1];
+            const float lowered = s.v[j1] - (u2 - u1);
+            const bool lowers = lowered < s.v[j1];
+            if (rr < cur * n) {
+                if (lowers) {
+                    s.v[j1] = lowered;
+                } else if (i0 >= 0 && j2 >= 0) {
+                    j1 = j2;
+                    i0 = s.y[j2];
+                }
+                if (i0 >= 0) {
+                    if (lowers)
+                        s.fr[--cur] = i0;
+                    else
+                        s.fr[still++] = i0;
+                }
+            } else if (i0 >= 0) {
+                s.fr[still++] = i0;
+            }
+            s.x[fi] = j1;
+            s.y[j1] = fi;
+        }
+        n_free = still;
+    }
+    for (int32_t f = 0; f < n_free; ++f) {
+        const int32_t start = s.fr[f];
+        uint32_t lo = 0, hi = 0, n_ready = 0;
+        int32_t final_j = -1;
+        for (uint32_t j = 0; j < n; ++j) {
+            s.cols[j] = (int32_t)j;
+            s.d[j] = c[start * kTile + j] - s.v[j];
+            s.pred[j] = start;
+        }
+        while (final_j < 0) {
+            if (lo == hi) {
+                n_ready = lo;
+                hi = serial_find_tied(n, lo, s.d, s.cols);
+                for (uint32_t k = lo; k < hi; ++k)
+                    if (s.y[s.cols[k]] < 0)
+                        final_j = s.cols[k];
+            }
+            if (final_j < 0)
+                final_j = serial_scan(n, c, &lo, &hi, s);
+        }
+        const float level = s.d[s.cols[lo]];
+        for (uint32_t k = 0; k < n_ready; ++k)
+            s.v[s.cols[k]] += s.d[s.cols[k]] - level;
+        int32_t j = final_j, i;
+        uint32_t steps = 0;
+        do {
+            i = s.pred[j];
+            s.y[j] = i;
+            const int32_t prev = s.x[i];
+            s.x[i] = j;
+            j = prev;
+            if (++steps >= n)
+                break;
+        } while (i != start);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// 2b. wave-parallel solver, K <= 64
+// ---------------------------------------------------------------------------
+
+// Exchange the per-position state of lanes a and b (a != b, both uniform).
+struct PosState {
+    int col, pr, yc;
+    float d, vc;
+};
+
+__device__ __forceinline__ void swap_lanes(PosState &st, int a, int b) {
+    const int lane = lane_id();
+    const int col_a = readlane_i(st.col, a), col_b = readlane_i(st.col, b);
+    const int pr_a = readlane_i(st.pr, a), pr_b = readlane_i(st.pr, b);
+    const int yc_a = readlane_i(st.yc, a), yc_b = readlane_i(st.yc, b);
+    const float d_a = readlane_f(st.d, a), d_b = readlane_f(st.d, b);
+    const float v_a = readlane_f(st.vc, a), v_b = readlane_f(st.vc, b);
+    if (lane == a) {
+        st.col = col_b;
+        st.pr = pr_b;
+        st.yc = yc_b;
+        st.d = d_b;
+        st.vc = v_b;
+    } else if (lane == b) {
+        st.col = col_a;
+        st.pr = pr_a;
+        st.yc = yc_a;
+        st.d = d_a;
+        st.vc = v_a;
+    }
+}
+
+struct WaveLds {
+    float c[kTile * kTile];  // row-major tile, stride 64
+    int32_t xmax[kTile];     // column-reduction claims
+    int32_t claims[kTile];
+    float vbuf[kTile];       // column-indexed scatter buffers
+    int32_t pbuf[kTile];
+};
+
+// Two-minimum of one row (jonker_dense_flat.h:193-210): (u1, j1) is the
+// first-index minimum; (u2, j2) the first-index minimum of the other columns,
+// with the reference's starting slot (LARGE, -1) winning ties.  Requires the
+// value at column 0 to be <= LARGE (the wave path guarantees it).
+__device__ __forceinline__ void row_two_min(float r, bool live, float &u1, int &j1, float &u2,
+                                            int &j2) {
+    const float val = live ? r : finf();
+    float m1, m2;
+    wave_min2(val, m1, m2);
+    const uint64_t at1 = ballot(live && r == m1);
+    j1 = first_lane(at1);
+    u1 = m1;
+    int jj;
+    if (m2 == m1) {
+        jj = first_lane(at1 & (at1 - 1));
+    } else {
+        jj = first_lane(ballot(live && r == m2));
+    }
+    if (m2 < kLarge) {
+        u2 = m2;
+        j2 = jj;
+    } else {
+        u2 = kLarge;
+        j2 = -1;
+    }
+}
+
+__device__ __forceinline__ bool wave_solve(const int K, WaveLds &L, float v, int y, int &x_out) {
+    const int lane = lane_id();
+    const bool live = lane < K;
+
+    // ---- column reduction (ccrrt_dense, jonker_dense_flat.h:124-176) ----
+    // (v, y) arrive as this lane's column minimum and its first arg-min row
+    if (live) {
+        L.xmax[lane] = -1;
+        L.claims[lane] = 0;
+    }
+    __syncthreads();
+    if (live) {
+        atomicMax(&L.xmax[y], lane);
+        atomicAdd(&L.claims[y], 1);
+    }
+    __syncthreads();
+    int x = live ? L.xmax[lane] : -1;                // lane = row
+    const bool unique_row = live ? (L.claims[lane] <= 1) : true;
+    if (live && L.xmax[y] != lane)
+        y = -1;                                      // lane = column
+    if (!live) {
+        v = finf();
+        y = -1;
+    }
+
+    // free rows (in increasing row order) and reduction transfer
+    int fr = 0;       // lane k holds free_rows[k]
+    int n_free = 0;
+    {
+        uint64_t m = ballot(live && x < 0);
+        while (m) {
+            const int row = first_lane(m);
+            m &= m - 1;
+            if (lane == n_free)
+                fr = row;
+            ++n_free;
+        }
+        // reduction transfer, unique rows in increasing order: each one sees
+        // the v lowered by the rows before it
+        uint64_t t = ballot(live && x >= 0 && unique_row);
+        while (t) {
+            const int i = first_lane(t);
+            t &= t - 1;
+            const int own = readlane_i(x, i);
+            const float r = L.c[i * kTile + lane] - v;
+            const float val = (live && lane != own) ? r : kLarge;
+            const float mn = fminf(wave_min(val), kLarge);
+            if (lane == own)
+                v -= mn;
+        }
+    }
+
+    // ---- augmenting row reduction (carr_dense, jonker_dense_flat.h:178-235) ----
+    // iteration guard: the reference's loop ends long before this; tripping it
+    // means a bug here, reported through the status word instead of spinning
+    const uint32_t rr_limit = 4u * (uint32_t)K * (uint32_t)K * (uint32_t)K + 64u;
+    for (int round = 0; n_free > 0 && round < 2; ++round) {
+        uint32_t cur = 0, rr = 0;
+        int still = 0;
+        while (cur < (uint32_t)n_free) {
+            ++rr;
+            if (rr > rr_limit)
+                return false;
+            const int fi = readlane_i(fr, (int)cur);
+            ++cur;
+            const float r = L.c[fi * kTile + lane] - v;
+            float u1, u2;
+            int j1, j2;
+            row_two_min(r, live, u1, j1, u2, j2);
+            int i0 = readlane_i(y, j1);
+            const float vj1 = readlane_f(v, j1);
+            const float lowered = vj1 - (u2 - u1);
+            const bool lowers = lowered < vj1;
+            if (rr < cur * (uint32_t)K) {
+                if (lowers) {
+                    if (lane == j1)
+                        v = lowered;
+                } else if (i0 >= 0 && j2 >= 0) {
+                    j1 = j2;
+                    i0 = readlane_i(y, j2);
+                }
+                if (i0 >= 0) {
+                    if (lowers) {
+                        --cur;
+                        if (lane == (int)cur)
+                            fr = i0;
+                    } else {
+                        if (lane == still)
+                            fr = i0;
+                        ++still;
+                    }
+                }
+            } else if (i0 >= 0) {
+                if (lane == still)
+                    fr = i0;
+                ++still;
+            }
+            if (lane == fi)
+                x = j1;
+            if (lane == j1)
+                y = fi;
+        }
+        n_free = still;
+    }
+
+    // ---- augmentation (ca_dense / find_path_dense, jonker_dense_flat.h:75-122,237-258) ----
+    int pred_col = 0;   // lane = column
+    for (int f = 0; f < n_free; ++f) {
+        const int start = readlane_i(fr, f);
+        PosState st;
+        st.col = lane;
+        st.d = live ? (L.c[start * kTile + lane] - v) : finf();
+        st.pr = start;
+        st.yc = y;
+        st.vc = v;
+        int lo = 0, hi = 0, n_ready = 0;
+        int final_j = -1;
+        while (final_j < 0) {
+            if (lo >= K)
+                return false;  // no unassigned column reachable: cannot happen
+            if (lo == hi) {
+                // find_dense over positions [lo, K)
+                n_ready = lo;
+                const bool act = live && lane >= lo;
+                const float val = act ? st.d : finf();
+                const float before = wave_shift_up(finf(), wave_prefix_min(val));
+                const bool later = act && lane > lo;
+                const uint64_t rec = ballot(later && st.d < before);
+                const uint64_t tie = ballot(later && st.d == before);
+                uint64_t ev = rec | tie;
+                hi = lo + 1;
+                while (ev) {
+                    const int k = first_lane(ev);
+                    ev &= ev - 1;
+                    if ((rec >> k) & 1ull) {
+                        swap_lanes(st, k, lo);
+                        hi = lo + 1;
+                    } else {
+                        if (k != hi)
+                            swap_lanes(st, k, hi);
+                        ++hi;
+                    }
+                }
+                const uint64_t open =
+                    ballot(live && lane >= lo && lane < hi && st.yc < 0);
+                if (open)
+                    final_j = readlane_i(st.col, last_lane(open));
+            }
+            if (final_j >= 0)
+                break;
+            // scan_dense: rows of the tied columns, one at a time
+            int slo = lo, shi = hi;
+            bool early = false;
+            while (slo != shi) {
+                const int q = slo++;
+                const int jq = readlane_i(st.col, q);
+                const int iq = readlane_i(st.yc, q);
+                const float level = readlane_f(st.d, q);
+                const float vq = readlane_f(st.vc, q);
+                const float cq = L.c[iq * kTile + jq];
+                const float h = cq - vq - level;
+                const bool act = live && lane >= shi;
+                const float cp = act ? L.c[iq * kTile + st.col] : 0.f;
+                const float r = cp - st.vc - h;
+                const bool better = act && r < st.d;
+                const bool tie = better && r == level;
+                const uint64_t ret = ballot(tie && st.yc < 0);
+                if (ret) {
+                    const int kk = first_lane(ret);
+                    if (better && lane <= kk) {
+                        st.d = r;
+                        st.pr = iq;
+                    }
+                    final_j = readlane_i(st.col, kk);
+                    early = true;
+                    break;
+                }
+                if (better) {
+                    st.d = r;
+                    st.pr = iq;
+                }
+                uint64_t tm = ballot(tie);
+                while (tm) {
+                    const int k = first_lane(tm);
+                    tm &= tm - 1;
+                    if (k != shi)
+                        swap_lanes(st, k, shi);
+                    ++shi;
+                }
+            }
+            if (!early) {
+                lo = slo;
+                hi = shi;
+            }
+        }
+        // dual update of the columns made ready before the last level
+        const float level = readlane_f(st.d, lo);
+        if (live && lane < n_ready)
+            st.vc += st.d - level;
+        if (live) {
+            L.vbuf[st.col] = st.vc;
+            L.pbuf[st.col] = st.pr;
+        }
+        __syncthreads();
+        if (live) {
+            v = L.vbuf[lane];
+            pred_col = L.pbuf[lane];
+        }
+        __syncthreads();
+        // flip the assignment along the predecessor chain
+        int j = final_j, i;
+        int steps = 0;
+        do {
+            i = readlane_i(pred_col, j);
+            if (lane == j)
+                y = i;
+            const int prev = readlane_i(x, i);
+            if (lane == i)
+                x = j;
+            j = prev;
+            if (++steps >= K)
+                break;
+        } while (i != start);
+    }
+    x_out = x;
+    return true;
+}
+
+__global__ void __launch_bounds__(64)
+jv_solve_kernel(const float *__restrict__ costs, int64_t B, int N, int M,
+                const JvStats *__restrict__ partial, int n_partial,
+                int64_t *__restrict__ out, uint32_t *__restrict__ status) {
+    __shared__ WaveLds L;
+    __shared__ SerialScratch S;
+    const int lane = lane_id();
+    const int K = N > M ? N : M;
+    const int64_t b = blockIdx.x;
+
+    float mx, mn;
+    uint32_t flags;
+    fold_stats(partial, n_partial, mx, mn, flags);
+    if (b == 0 && lane == 0)
+        status[0] = flags;
+    const bool bad = (flags & (kJvFlagNan | kJvFlagNegInf)) != 0;
+    int64_t *ob = out + b * N;
+    if (bad) {
+        for (int i = lane; i < N; i += 64)
+            ob[i] = -1;
+        return;
+    }
+    const bool any_finite = (flags & kJvFlagAnyFinite) != 0;
+    const float sentinel = any_finite ? (mx + 1.0f) * (float)(K + 1) : 1.0f;
+    const bool has_inf = (flags & kJvFlagPosInf) != 0;
+    bool fast = true;
+    if (any_finite && (mx > kFastRange || mn < -kFastRange))
+        fast = false;
+    if (has_inf && !(fabsf(sentinel) <= kFastRange))
+        fast = false;
+
+    // tile load: lane j reads column j of every row (coalesced row reads),
+    // and keeps the running column minimum with the first arg-min row
+    // (strict '<' from LARGE, jonker_dense_flat.h:136-144)
+    const float *src = costs + b * (int64_t)N * M;
+    float vmin = kLarge;
+    int ymin = 0;
+#pragma unroll 8
+    for (int i = 0; i < K; ++i) {
+        float val = 0.f;
+        if (i < N && lane < M) {
+            val = src[(int64_t)i * M + lane];
+            if (!isfinite(val))
+                val = sentinel;
+        }
+        L.c[i * kTile + lane] = val;
+        if (val < vmin) {
+            vmin = val;
+            ymin = i;
+        }
+    }
+    __syncthreads();
+
+    int x = -1;
+    if (fast) {
+        if (!wave_solve(K, L, vmin, ymin, x)) {
+            if (lane == 0)
+                atomicOr(&status[1], 1u);
+            x = -1;
+        }
+    } else {
+        if (lane == 0)
+            serial_solve((uint32_t)K, L.c, S);
+        __syncthreads();
+        if (lane < K)
+            x = S.x[lane];
+    }
+    if (lane < N)
+        ob[lane] = (x >= 0 && x < M) ? (int64_t)x : (int64_t)-1;
+}
+
+} // namespace
+} // namespace tmamd
+
+// ---------------------------------------------------------------------------
+// C-ABI
+// ---------------------------------------------------------------------------
+using namespace tmamd;
+
+extern "C" size_t tm_jv_workspace_bytes(int64_t B, int32_t N, int32_t M) {
+    (void)B;
+    (void)N;
+    (void)M;
+    return sizeof(JvStats) * (size_t)kJvMaxStatBlocks + 256;
+}
+
+extern "C" int tm_jv_dense_batch_f32(const float *costs, int64_t B, int32_t N, int32_t M,
+                                     int64_t *out, void *workspace, size_t workspace_bytes,
+                                     uint32_t *d_status, hipStream_t stream) {
+    if (B < 0 || N < 0 || M < 0)
+        return kTmErrInvalidArgument;
+    if (B == 0 || N == 0 || M == 0)
+        return kTmOk;  // caller fills -1
+    const int K = N > M ? N : M;
+    if (K > kTile)
+        return kTmErrUnsupportedShape;
+    if (workspace_bytes < tm_jv_workspace_bytes(B, N, M) || workspace == nullptr ||
+        d_status == nullptr)
+        return kTmErrWorkspace;
+    if (B > (int64_t)0x7fffffff)
+        return kTmErrUnsupportedShape;
+    const int64_t n = B * (int64_t)N * M;
+    int64_t blocks = (n / 4 + kStatsBlock - 1) / kStatsBlock;
+    blocks = blocks < 1 ? 1 : (blocks > kJvMaxStatBlocks ? kJvMaxStatBlocks : blocks);
+    JvStats *partial = static_cast<JvStats *>(workspace);
+    hipLaunchKernelGGL(jv_stats_kernel, dim3((unsigned)blocks), dim3(kStatsBlock), 0, stream,
+                       costs, n, partial, d_status);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess)
+        return kTmErrLaunch;
+    hipLaunchKernelGGL(jv_solve_kernel, dim3((unsigned)B), dim3(64), 0, stream, costs, B, N, M,
+                       partial, (int)blocks, out, d_status);
+    e = hipGetLastError();
+    return e == hipSuccess ? kTmOk : kTmErrLaunch;
+}
+
+extern "C" int32_t tm_jv_max_k(void) { return kTile; }
+
+extern "C" int tm_jv_check_status(const uint32_t *d_status, hipStream_t stream) {
+    uint32_t words[2] = {0, 0};
+    if (hipMemcpyAsync(words, d_status, sizeof(words), hipMemcpyDeviceToHost, stream) !=
+        hipSuccess)
+        return TM_ERR_HIP;
+    if (hipStreamSynchronize(stream) != hipSuccess)
+        return TM_ERR_HIP;
+    const uint32_t flags = words[0];
+    if (words[1] != 0)
+        return TM_ERR_INTERNAL;
+    if (flags & kJvFlagNan)
+        return TM_ERR_NAN;
+    if (flags & kJvFlagNegInf)
+        return TM_ERR_NEG_INF;
+    return TM_OK;
+}

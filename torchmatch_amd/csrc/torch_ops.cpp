@@ -1,0 +1,157 @@
+// torch_ops.cpp -- torch dispatcher registrations over the C ABI.
+//
+// Only CUDA-key kernels live here (ROCm tensors have device type "cuda").
+// The schema of `assignment::jonker_dense_batch` belongs to whoever defines
+// the `assignment` library (the reference CPU extension, ops.cpp:486-495, or
+// torchmatch_amd/_loader.py when that extension is absent); this file adds
+// the device kernel exactly where the reference's CUDA extension adds its own
+// (assignment/cuda/dispatch.cu:181-186).
+//
+// The private `torchmatch_amd::sinkhorn` op is what the Python custom ops
+// `transport::log_sinkhorn` / `transport::unbalanced_sinkhorn` call for
+// device tensors.
+#include <ATen/ATen.h>
+#include <c10/core/DeviceGuard.h>
+#include <c10/hip/HIPStream.h>
+#include <torch/library.h>
+
+#include <vector>
+
+#include "../../include/torchmatch_amd.h"
+
+namespace {
+
+hipStream_t current_stream(const at::Tensor &t) {
+    return c10::hip::getCurrentHIPStream(t.get_device()).stream();
+}
+
+// Mirrors check_not_capturing (assignment/cuda/dispatch.cu:97-106): the op
+// reads its validation flags back to the host, which stream capture forbids.
+void check_not_capturing(hipStream_t stream, const char *op_name) {
+    hipStreamCaptureStatus status = hipStreamCaptureStatusNone;
+    const hipError_t e = hipStreamIsCapturing(stream, &status);
+    TORCH_CHECK(e == hipSuccess, op_name, ": hipStreamIsCapturing failed: ",
+                hipGetErrorString(e));
+    TORCH_CHECK(status == hipStreamCaptureStatusNone, op_name,
+                " performs a host-side synchronization and cannot run inside CUDA graph "
+                "capture (e.g. torch.compile(mode=\"reduce-overhead\")); call it outside the "
+                "captured region.");
+}
+
+void check_rc(int rc, const char *op_name) {
+    switch (rc) {
+    case TM_OK:
+        return;
+    case TM_ERR_NAN:
+        TORCH_CHECK(false, "cost matrix contains NaN; use +inf for forbidden pairs, NaN "
+                           "signals an upstream bug");
+    case TM_ERR_NEG_INF:
+        TORCH_CHECK(false, "cost matrix contains -inf; -inf has no forbidden-edge meaning");
+    case TM_ERR_UNSUPPORTED_SHAPE:
+        TORCH_CHECK(false, op_name, ": shape not supported by the gfx950 kernels");
+    case TM_ERR_INVALID_ARGUMENT:
+        TORCH_CHECK(false, op_name, ": invalid argument");
+    case TM_ERR_WORKSPACE:
+        TORCH_CHECK(false, op_name, ": workspace too small");
+    case TM_ERR_INTERNAL:
+        TORCH_CHECK(false, op_name, ": internal error (iteration guard tripped)");
+    case TM_ERR_LAUNCH:
+        TORCH_CHECK(false, op_name, ": kernel launch failed: ",
+                    hipGetErrorString(hipGetLastError()));
+    default:
+        TORCH_CHECK(false, op_name, ": HIP runtime error (code ", rc, ")");
+    }
+}
+
+// CUDA-key kernel of assignment::jonker_dense_batch.
+// Reference: assignment/cuda/dispatch.cu:137-177; results follow the CPU op
+// assignment/cpu/ops.cpp:176-289 (rectangular input accepted, like the CPU op).
+at::Tensor jonker_dense_batch_hip(const at::Tensor &costs) {
+    TORCH_CHECK(costs.is_cuda(), "costs must be a CUDA tensor");
+    TORCH_CHECK(costs.dim() == 3, "costs must be 3D (B, N, M), got ", costs.dim());
+    TORCH_CHECK(costs.scalar_type() == at::kFloat || costs.scalar_type() == at::kDouble,
+                "costs must be float32 or float64, got ", costs.scalar_type());
+    TORCH_CHECK(costs.is_contiguous(), "costs must be contiguous");
+    const c10::DeviceGuard guard(costs.device());
+
+    const int64_t B = costs.size(0);
+    const int64_t N = costs.size(1);
+    const int64_t M = costs.size(2);
+    auto out = at::empty({B, N}, costs.options().dtype(at::kLong));
+    if (B == 0 || N == 0 || M == 0) {
+        out.fill_(-1);
+        return out;
+    }
+    const int64_t K = N > M ? N : M;
+    TORCH_CHECK(K <= tm_jv_max_k(), "jonker_dense_batch (gfx950) supports K = max(N, M) <= ",
+                tm_jv_max_k(), ", got K=", K);
+
+    const hipStream_t stream = current_stream(costs);
+    check_not_capturing(stream, "jonker_dense_batch");
+
+    // float64 input is solved in float32, as the reference device op does
+    // (dispatch.cu:156).
+    const at::Tensor cf = costs.scalar_type() == at::kFloat ? costs : costs.to(at::kFloat);
+    const size_t ws_bytes = tm_jv_workspace_bytes(B, (int32_t)N, (int32_t)M);
+    auto ws = at::empty({(int64_t)ws_bytes}, costs.options().dtype(at::kByte));
+    auto status = at::empty({2}, costs.options().dtype(at::kInt));
+    int rc = tm_jv_dense_batch_f32(cf.data_ptr<float>(), B, (int32_t)N, (int32_t)M,
+                                   out.data_ptr<int64_t>(), ws.data_ptr(), ws_bytes,
+                                   reinterpret_cast<uint32_t *>(status.data_ptr<int32_t>()),
+                                   stream);
+    check_rc(rc, "jonker_dense_batch");
+    rc = tm_jv_check_status(reinterpret_cast<const uint32_t *>(status.data_ptr<int32_t>()),
+                            stream);
+    check_rc(rc, "jonker_dense_batch");
+    return out;
+}
+
+// torchmatch_amd::sinkhorn -- device Sinkhorn over a precomputed epsilon
+// schedule.  Returns (log_plan, log_u, log_v); log_plan is empty when
+// write_plan is false.
+std::tuple<at::Tensor, at::Tensor, at::Tensor>
+sinkhorn_hip(const at::Tensor &cost, const at::Tensor &a, const at::Tensor &b,
+             at::ArrayRef<double> eps_sched, double rho, bool write_plan) {
+    TORCH_CHECK(cost.is_cuda() && a.is_cuda() && b.is_cuda(),
+                "sinkhorn: cost, a and b must be CUDA tensors");
+    TORCH_CHECK(cost.dim() == 3, "sinkhorn: cost must be 3D (B, N, M)");
+    TORCH_CHECK(cost.scalar_type() == at::kFloat && a.scalar_type() == at::kFloat &&
+                    b.scalar_type() == at::kFloat,
+                "sinkhorn: the gfx950 kernels compute in float32");
+    const int64_t B = cost.size(0), N = cost.size(1), M = cost.size(2);
+    TORCH_CHECK(a.dim() == 2 && a.size(0) == B && a.size(1) == N, "sinkhorn: a must be (B, N)");
+    TORCH_CHECK(b.dim() == 2 && b.size(0) == B && b.size(1) == M, "sinkhorn: b must be (B, M)");
+    TORCH_CHECK(!eps_sched.empty(), "sinkhorn: empty epsilon schedule");
+    const c10::DeviceGuard guard(cost.device());
+    const at::Tensor c = cost.contiguous(), ac = a.contiguous(), bc = b.contiguous();
+    auto log_u = at::empty({B, N}, cost.options());
+    auto log_v = at::empty({B, M}, cost.options());
+    at::Tensor log_plan = write_plan ? at::empty({B, N, M}, cost.options())
+                                     : at::empty({0}, cost.options());
+    if (B == 0)
+        return {log_plan, log_u, log_v};
+    const size_t ws_bytes = tm_sinkhorn_workspace_bytes(B, N, M);
+    auto ws = at::empty({(int64_t)ws_bytes}, cost.options().dtype(at::kByte));
+    const hipStream_t stream = current_stream(cost);
+    const int rc = tm_sinkhorn_f32(c.data_ptr<float>(), ac.data_ptr<float>(),
+                                   bc.data_ptr<float>(), B, N, M, eps_sched.data(),
+                                   (int32_t)eps_sched.size(), rho,
+                                   write_plan ? log_plan.data_ptr<float>() : nullptr,
+                                   log_u.data_ptr<float>(), log_v.data_ptr<float>(),
+                                   ws.data_ptr(), ws_bytes, stream);
+    check_rc(rc, "sinkhorn");
+    return {log_plan, log_u, log_v};
+}
+
+} // namespace
+
+TORCH_LIBRARY_IMPL(assignment, CUDA, m) {
+    m.impl("jonker_dense_batch", &jonker_dense_batch_hip);
+}
+
+TORCH_LIBRARY(torchmatch_amd, m) {
+    m.def("sinkhorn(Tensor cost, Tensor a, Tensor b, float[] eps_sched, float rho, "
+          "bool write_plan) -> (Tensor, Tensor, Tensor)");
+}
+
+TORCH_LIBRARY_IMPL(torchmatch_amd, CUDA, m) { m.impl("sinkhorn", &sinkhorn_hip); }

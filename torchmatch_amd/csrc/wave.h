@@ -1,0 +1,128 @@
+// wave.h -- wave64 building blocks for gfx950 (CDNA4).
+//
+// Everything here assumes a 64-lane wavefront with all lanes active, which is
+// how every kernel in this library launches (block sizes are multiples of 64
+// and no helper is called under divergent control flow).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace tmamd {
+
+// DPP control words (GFX9 encoding, valid on gfx950).
+enum : int {
+    kDppQuadXor1 = 0xB1,       // quad_perm:[1,0,3,2]
+    kDppQuadXor2 = 0x4E,       // quad_perm:[2,3,0,1]
+    kDppRowShr1 = 0x111,
+    kDppRowShr2 = 0x112,
+    kDppRowShr4 = 0x114,
+    kDppRowShr8 = 0x118,
+    kDppWaveShr1 = 0x138,
+    kDppRowMirror = 0x140,
+    kDppRowHalfMirror = 0x141,
+    kDppRowBcast15 = 0x142,
+    kDppRowBcast31 = 0x143,
+};
+
+__device__ __forceinline__ int lane_id() { return (int)__lane_id(); }
+
+__device__ __forceinline__ uint64_t ballot(bool p) { return __builtin_amdgcn_ballot_w64(p); }
+
+__device__ __forceinline__ int readlane_i(int x, int lane) {
+    return __builtin_amdgcn_readlane(x, lane);
+}
+__device__ __forceinline__ float readlane_f(float x, int lane) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), lane));
+}
+__device__ __forceinline__ int uniform_i(int x) { return __builtin_amdgcn_readfirstlane(x); }
+__device__ __forceinline__ float uniform_f(float x) {
+    return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(x)));
+}
+
+// Move `src` through a DPP pattern; lanes whose source is outside the pattern
+// keep `identity`.
+template <int CTRL, int ROW_MASK = 0xF, int BANK_MASK = 0xF>
+__device__ __forceinline__ float dpp_f(float identity, float src) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(identity),
+                                                      __float_as_int(src), CTRL,
+                                                      ROW_MASK, BANK_MASK, false));
+}
+
+// Minimum over the whole wave, returned uniformly (every lane gets it).  Exact:
+// min is order independent.  NaN lanes must not occur (callers guarantee).
+__device__ __forceinline__ float wave_min(float x) {
+    const float inf = __int_as_float(0x7f800000);
+    x = fminf(x, dpp_f<kDppQuadXor1>(inf, x));
+    x = fminf(x, dpp_f<kDppQuadXor2>(inf, x));
+    x = fminf(x, dpp_f<kDppRowHalfMirror>(inf, x));
+    x = fminf(x, dpp_f<kDppRowMirror>(inf, x));
+    const float a = fminf(readlane_f(x, 0), readlane_f(x, 16));
+    const float b = fminf(readlane_f(x, 32), readlane_f(x, 48));
+    return fminf(a, b);
+}
+
+// Maximum over the whole wave (uniform result).
+__device__ __forceinline__ float wave_max(float x) {
+    const float ninf = __int_as_float(0xff800000);
+    x = fmaxf(x, dpp_f<kDppQuadXor1>(ninf, x));
+    x = fmaxf(x, dpp_f<kDppQuadXor2>(ninf, x));
+    x = fmaxf(x, dpp_f<kDppRowHalfMirror>(ninf, x));
+    x = fmaxf(x, dpp_f<kDppRowMirror>(ninf, x));
+    const float a = fmaxf(readlane_f(x, 0), readlane_f(x, 16));
+    const float b = fmaxf(readlane_f(x, 32), readlane_f(x, 48));
+    return fmaxf(a, b);
+}
+
+// Smallest and second smallest value of the wave as a multiset (if the
+// minimum occurs twice, both results are equal).  Uniform results.
+__device__ __forceinline__ void wave_min2(float x, float &m1, float &m2) {
+    const float inf = __int_as_float(0x7f800000);
+    float a = x, b = inf;
+#define TMAMD_MIN2_STEP(CTRL)                                   \
+    {                                                           \
+        const float pa = dpp_f<CTRL>(inf, a);                   \
+        const float pb = dpp_f<CTRL>(inf, b);                   \
+        const float lo = fminf(a, pa);                          \
+        b = fminf(fmaxf(a, pa), fminf(b, pb));                  \
+        a = lo;                                                 \
+    }
+    TMAMD_MIN2_STEP(kDppQuadXor1)
+    TMAMD_MIN2_STEP(kDppQuadXor2)
+    TMAMD_MIN2_STEP(kDppRowHalfMirror)
+    TMAMD_MIN2_STEP(kDppRowMirror)
+#undef TMAMD_MIN2_STEP
+    // merge the four 16-lane rows
+    float r1 = readlane_f(a, 0), r2 = readlane_f(b, 0);
+#pragma unroll
+    for (int row = 16; row < 64; row += 16) {
+        const float q1 = readlane_f(a, row), q2 = readlane_f(b, row);
+        const float lo = fminf(r1, q1);
+        r2 = fminf(fmaxf(r1, q1), fminf(r2, q2));
+        r1 = lo;
+    }
+    m1 = r1;
+    m2 = r2;
+}
+
+// Inclusive prefix minimum across lanes 0..63 (lane p gets min of lanes 0..p).
+__device__ __forceinline__ float wave_prefix_min(float x) {
+    const float inf = __int_as_float(0x7f800000);
+    x = fminf(x, dpp_f<kDppRowShr1>(inf, x));
+    x = fminf(x, dpp_f<kDppRowShr2>(inf, x));
+    x = fminf(x, dpp_f<kDppRowShr4>(inf, x));
+    x = fminf(x, dpp_f<kDppRowShr8>(inf, x));
+    x = fminf(x, dpp_f<kDppRowBcast15, 0xA>(inf, x));
+    x = fminf(x, dpp_f<kDppRowBcast31, 0xC>(inf, x));
+    return x;
+}
+
+// Value of lane p-1 (lane 0 gets `identity`).
+__device__ __forceinline__ float wave_shift_up(float identity, float x) {
+    return dpp_f<kDppWaveShr1>(identity, x);
+}
+
+__device__ __forceinline__ int first_lane(uint64_t m) { return (int)__builtin_ctzll(m); }
+__device__ __forceinline__ int last_lane(uint64_t m) { return 63 - (int)__builtin_clzll(m); }
+
+} // namespace tmamd
