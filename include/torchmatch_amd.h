@@ -50,7 +50,8 @@ enum {
     TM_JV_FLAG_NAN = 1u,
     TM_JV_FLAG_NEG_INF = 2u,
     TM_JV_FLAG_POS_INF = 4u,
-    TM_JV_FLAG_ANY_FINITE = 8u
+    TM_JV_FLAG_ANY_FINITE = 8u,
+    TM_JV_FLAG_NEG_ZERO = 16u   /* input holds -0.0 (informational) */
 };
 
 /* ---- batched Jonker-Volgenant (assignment::jonker_dense_batch) -------- */

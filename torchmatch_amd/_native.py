@@ -26,6 +26,7 @@ TM_JV_FLAG_NAN = 1
 TM_JV_FLAG_NEG_INF = 2
 TM_JV_FLAG_POS_INF = 4
 TM_JV_FLAG_ANY_FINITE = 8
+TM_JV_FLAG_NEG_ZERO = 16
 
 # symbol -> (restype, argtypes); the declarations of include/torchmatch_amd.h
 _VP = ctypes.c_void_p

@@ -67,6 +67,8 @@ jv_stats_kernel(const float *__restrict__ costs, int64_t n, JvStats *__restrict_
             flags |= (x < 0.f) ? kJvFlagNegInf : kJvFlagPosInf;
         } else {
             flags |= kJvFlagAnyFinite;
+            if (__float_as_uint(x) == 0x80000000u)
+                flags |= kJvFlagNegZero;
             mx = fmaxf(mx, x);
             mn = fminf(mn, x);
         }
@@ -87,7 +89,7 @@ jv_stats_kernel(const float *__restrict__ costs, int64_t n, JvStats *__restrict_
     // OR of the flags across the wave
     uint32_t f = 0;
 #pragma unroll
-    for (int bit = 0; bit < 4; ++bit)
+    for (int bit = 0; bit < 5; ++bit)
         if (ballot((flags >> bit) & 1u))
             f |= 1u << bit;
 
@@ -128,7 +130,7 @@ __device__ __forceinline__ void fold_stats(const JvStats *__restrict__ partial, 
     mn = wave_min(mn);
     flags = 0;
 #pragma unroll
-    for (int bit = 0; bit < 4; ++bit)
+    for (int bit = 0; bit < 5; ++bit)
         if (ballot((f >> bit) & 1u))
             flags |= 1u << bit;
 }
@@ -357,31 +359,43 @@ struct WaveLds {
 // Two-minimum of one row (jonker_dense_flat.h:193-210): (u1, j1) is the
 // first-index minimum; (u2, j2) the first-index minimum of the other columns,
 // with the reference's starting slot (LARGE, -1) winning ties.  Requires the
-// value at column 0 to be <= LARGE (the wave path guarantees it).
-__device__ __forceinline__ void row_two_min(float r, bool live, float &u1, int &j1, float &u2,
-                                            int &j2) {
-    const float val = live ? r : finf();
-    float m1, m2;
-    wave_min2(val, m1, m2);
-    const uint64_t at1 = ballot(live && r == m1);
-    j1 = first_lane(at1);
-    u1 = m1;
-    int jj;
-    if (m2 == m1) {
+// value at column 0 to be <= LARGE (the wave path guarantees it).  Ordering
+// and ties use integer keys; u1 / u2 are the lanes' own float values.
+struct TwoMin {
+    int j1, j2;
+    float u1, u2;
+};
+
+__device__ __forceinline__ TwoMin row_two_min(float r, bool live) {
+    const int key = live ? fkey(r) : kKeyNone;
+    int k1, k2;
+    wave_min2_key(key, k1, k2);
+    k1 = uniform_i(k1);
+    k2 = uniform_i(k2);
+    const uint64_t at1 = ballot(key == k1);
+    TwoMin t;
+    t.j1 = first_lane(at1);
+    t.u1 = readlane_f(r, t.j1);
+    int jj = -1;
+    if (k2 == k1)
         jj = first_lane(at1 & (at1 - 1));
-    } else {
-        jj = first_lane(ballot(live && r == m2));
+    else if (k2 != kKeyNone)
+        jj = first_lane(ballot(key == k2));
+    t.j2 = -1;
+    t.u2 = kLarge;
+    if (jj >= 0) {
+        const float u = readlane_f(r, jj);
+        if (u < kLarge) {
+            t.u2 = u;
+            t.j2 = jj;
+        }
     }
-    if (m2 < kLarge) {
-        u2 = m2;
-        j2 = jj;
-    } else {
-        u2 = kLarge;
-        j2 = -1;
-    }
+    return t;
 }
 
-__device__ __forceinline__ bool wave_solve(const int K, WaveLds &L, float v, int y, int &x_out) {
+__device__ __forceinline__ bool wave_solve(const int K, WaveLds &L, float v,
+                                           int y, bool chain, int &x_out) {
+    uint64_t okm = 0;
     const int lane = lane_id();
     const bool live = lane < K;
 
@@ -419,15 +433,20 @@ __device__ __forceinline__ bool wave_solve(const int K, WaveLds &L, float v, int
             ++n_free;
         }
         // reduction transfer, unique rows in increasing order: each one sees
-        // the v lowered by the rows before it
+        // the v lowered by the rows before it; mn starts at LARGE and keeps
+        // the first (lowest column) minimum, as the sequential scan does
+        const int large_key = fkey(kLarge);
         uint64_t t = ballot(live && x >= 0 && unique_row);
         while (t) {
             const int i = first_lane(t);
             t &= t - 1;
             const int own = readlane_i(x, i);
             const float r = L.c[i * kTile + lane] - v;
-            const float val = (live && lane != own) ? r : kLarge;
-            const float mn = fminf(wave_min(val), kLarge);
+            const int key = (live && lane != own) ? fkey(r) : kKeyNone;
+            const int kmin = uniform_i(wave_min_key(key));
+            float mn = kLarge;
+            if (kmin < large_key)
+                mn = readlane_f(r, first_lane(ballot(key == kmin)));
             if (lane == own)
                 v -= mn;
         }
@@ -437,54 +456,138 @@ __device__ __forceinline__ bool wave_solve(const int K, WaveLds &L, float v, int
     // iteration guard: the reference's loop ends long before this; tripping it
     // means a bug here, reported through the status word instead of spinning
     const uint32_t rr_limit = 4u * (uint32_t)K * (uint32_t)K * (uint32_t)K + 64u;
+    // A general step follows the reference's branches with scalar selects.
+    // When it displaces the previous owner of its column with a lowered dual
+    // (the reference's `free_rows[--current] = i0`, almost every step on
+    // uniform costs), the loop enters a displacement chain: the displaced
+    // row's step is started before the previous step's outcome has reached
+    // the scalar unit, and each step's updates are applied inside its own
+    // argmin lane, gated there.  The first step that does not continue the
+    // chain is handed back, untouched, to the general step.  x is not kept
+    // during this phase; it is rebuilt from y afterwards (only assigned rows'
+    // x are ever read again).
     for (int round = 0; n_free > 0 && round < 2; ++round) {
         uint32_t cur = 0, rr = 0;
         int still = 0;
-        while (cur < (uint32_t)n_free) {
+        bool have = false;  // fi already known (handed back by a chain)
+        int fi = 0;
+        while (true) {
+            if (!have) {
+                if (cur >= (uint32_t)n_free)
+                    break;
+                fi = readlane_i(fr, (int)cur);
+            }
+            have = false;
             ++rr;
+            ++cur;
             if (rr > rr_limit)
                 return false;
-            const int fi = readlane_i(fr, (int)cur);
-            ++cur;
             const float r = L.c[fi * kTile + lane] - v;
-            float u1, u2;
-            int j1, j2;
-            row_two_min(r, live, u1, j1, u2, j2);
-            int i0 = readlane_i(y, j1);
+            const int key = live ? fkey(r) : kKeyNone;
+            int k1, k2;
+            wave_min2_key(key, k1, k2);
+            const uint64_t m1 = ballot(key == k1);
+            const uint64_t m2 = ballot(key == k2);
+            const bool same = uniform_i(k1) == uniform_i(k2);
+            const int j1 = first_lane(m1);
+            const uint64_t m1b = m1 & (m1 - 1);
+            const int j2c = same ? (m1b ? first_lane(m1b) : -1) : (m2 ? first_lane(m2) : -1);
+            const int j2r = j2c < 0 ? 0 : j2c;
+            const float u1 = readlane_f(r, j1);
+            const float u2c = readlane_f(r, j2r);
+            const int i0 = readlane_i(y, j1);
+            const int y2 = readlane_i(y, j2r);
             const float vj1 = readlane_f(v, j1);
+            // (LARGE, -1) start slot of the second minimum
+            const bool has2 = j2c >= 0 && u2c < kLarge;
+            const int j2 = has2 ? j2c : -1;
+            const float u2 = has2 ? u2c : kLarge;
             const float lowered = vj1 - (u2 - u1);
             const bool lowers = lowered < vj1;
-            if (rr < cur * (uint32_t)K) {
-                if (lowers) {
-                    if (lane == j1)
-                        v = lowered;
-                } else if (i0 >= 0 && j2 >= 0) {
-                    j1 = j2;
-                    i0 = readlane_i(y, j2);
-                }
-                if (i0 >= 0) {
-                    if (lowers) {
-                        --cur;
-                        if (lane == (int)cur)
-                            fr = i0;
-                    } else {
-                        if (lane == still)
-                            fr = i0;
-                        ++still;
-                    }
-                }
-            } else if (i0 >= 0) {
-                if (lane == still)
-                    fr = i0;
-                ++still;
-            }
-            if (lane == fi)
-                x = j1;
-            if (lane == j1)
+            const bool cap = rr < cur * (uint32_t)K;
+            const bool vupd = cap && lowers;
+            const bool swap2 = cap && !lowers && i0 >= 0 && j2 >= 0;
+            const int jsel = swap2 ? j2 : j1;
+            const int isel = swap2 ? y2 : i0;
+            const bool push_front = vupd && i0 >= 0;
+            const bool push_back = !vupd && isel >= 0;
+            if (vupd && lane == j1)
+                v = lowered;
+            if (push_back && lane == still)
+                fr = isel;
+            if (lane == jsel)
                 y = fi;
+            still += push_back ? 1 : 0;
+            if (!push_front)
+                continue;
+            // fr[--cur] = i0 is read straight back: keep i0 in a register
+            --cur;
+            fi = i0;
+            have = true;
+            if (!chain)
+                continue;
+
+            // ---- displacement chain ----
+            // Reduced costs are >= +0 throughout this phase (v starts at the
+            // column minima and only falls), so their raw bits order them and
+            // the second minimum's bits are its value.  A step continues the
+            // chain when the reference would take its `free_rows[--current]`
+            // branch: cap (rr_cnt < current * n, current counted after the
+            // read), dual lowered, column owned.  Anything else ends the chain
+            // and the general step above redoes that step exactly.
+            const uint32_t rr_cap = (cur + 1) * (uint32_t)K;
+            uint64_t okm;
+            int inext;
+            {
+                const float rc = L.c[fi * kTile + lane] - v;
+                const int kc = live ? __float_as_int(rc) : kKeyNone;
+                int c1, c2;
+                wave_min2_key(kc, c1, c2);
+                const int jc = first_lane(ballot(kc == c1));
+                inext = readlane_i(y, jc);
+                const float lowc = v - (__int_as_float(c2) - rc);
+                const bool okc = lane == jc && rr + 1 < rr_cap && lowc < v && y >= 0;
+                if (okc) {
+                    v = lowc;
+                    y = fi;
+                }
+                okm = ballot(okc);
+            }
+            while (true) {
+                // the displaced row, started before okm is consulted
+                const int fn = inext & (kTile - 1);
+                const float rn = L.c[fn * kTile + lane] - v;
+                const int kn = live ? __float_as_int(rn) : kKeyNone;
+                int n1, n2;
+                wave_min2_key(kn, n1, n2);
+                const int jn = first_lane(ballot(kn == n1));
+                const int inn = readlane_i(y, jn);
+                if (okm == 0)
+                    break;  // fi's step leaves the chain: the general step redoes it
+                ++rr;       // fi's step is committed (its ++current / --current cancel)
+                fi = fn;
+                const float lown = v - (__int_as_float(n2) - rn);
+                const bool okn = lane == jn && rr + 1 < rr_cap && lown < v && y >= 0;
+                if (okn) {
+                    v = lown;
+                    y = fi;
+                }
+                okm = ballot(okn);
+                inext = inn;
+            }
         }
         n_free = still;
     }
+    // x from y: every assigned column names its row (free rows keep -1;
+    // the augmentation below overwrites them before reading)
+    if (live)
+        L.xmax[lane] = -1;
+    __syncthreads();
+    if (live && y >= 0)
+        L.xmax[y] = lane;
+    __syncthreads();
+    x = live ? L.xmax[lane] : -1;
+    __syncthreads();
 
     // ---- augmentation (ca_dense / find_path_dense, jonker_dense_flat.h:75-122,237-258) ----
     int pred_col = 0;   // lane = column
@@ -502,14 +605,15 @@ __device__ __forceinline__ bool wave_solve(const int K, WaveLds &L, float v, int
             if (lo >= K)
                 return false;  // no unassigned column reachable: cannot happen
             if (lo == hi) {
-                // find_dense over positions [lo, K)
+                // find_dense over positions [lo, K): a new running minimum
+                // swaps with position lo, a tie with it swaps with hi
                 n_ready = lo;
                 const bool act = live && lane >= lo;
-                const float val = act ? st.d : finf();
-                const float before = wave_shift_up(finf(), wave_prefix_min(val));
+                const int dkey = act ? fkey(st.d) : kKeyNone;
+                const int before = wave_shift_up_key(wave_prefix_min_key(dkey));
                 const bool later = act && lane > lo;
-                const uint64_t rec = ballot(later && st.d < before);
-                const uint64_t tie = ballot(later && st.d == before);
+                const uint64_t rec = ballot(later && dkey < before);
+                const uint64_t tie = ballot(later && dkey == before);
                 uint64_t ev = rec | tie;
                 hi = lo + 1;
                 while (ev) {
@@ -646,7 +750,7 @@ jv_solve_kernel(const float *__restrict__ costs, int64_t B, int N, int M,
     const float *src = costs + b * (int64_t)N * M;
     float vmin = kLarge;
     int ymin = 0;
-#pragma unroll 8
+#pragma unroll 16
     for (int i = 0; i < K; ++i) {
         float val = 0.f;
         if (i < N && lane < M) {
@@ -664,7 +768,10 @@ jv_solve_kernel(const float *__restrict__ costs, int64_t B, int N, int M,
 
     int x = -1;
     if (fast) {
-        if (!wave_solve(K, L, vmin, ymin, x)) {
+        // displacement chains need K >= 2 and no -0.0 (their second minimum is
+        // read back from its key, which maps -0.0 to +0.0)
+        const bool chain = K >= 2 && (flags & kJvFlagNegZero) == 0;
+        if (!wave_solve(K, L, vmin, ymin, chain, x)) {
             if (lane == 0)
                 atomicOr(&status[1], 1u);
             x = -1;

@@ -126,3 +126,106 @@ __device__ __forceinline__ int first_lane(uint64_t m) { return (int)__builtin_ct
 __device__ __forceinline__ int last_lane(uint64_t m) { return 63 - (int)__builtin_clzll(m); }
 
 } // namespace tmamd
+
+namespace tmamd {
+
+// ---- integer-key reductions (no NaN canonicalisation, full-rate VALU) ------
+
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+
+// Order-preserving int32 key of a float that is not NaN: key(a) < key(b) iff
+// a < b, and -0.0 / +0.0 share one key (a + 0.0f turns -0.0 into +0.0), so
+// key equality is float equality.
+__device__ __forceinline__ int fkey(float f) {
+    const int b = __float_as_int(f + 0.0f);
+    return b ^ ((b >> 31) & 0x7fffffff);
+}
+constexpr int kKeyNone = 0x7fffffff;  // a NaN bit pattern: above every key
+
+// DPP move for patterns in which every lane has a source lane (quad_perm,
+// row mirrors), so the old value never shows and the move can fold into the
+// consuming ALU op.
+template <int CTRL>
+__device__ __forceinline__ int dpp_full(int x) {
+    return __builtin_amdgcn_mov_dpp(x, CTRL, 0xF, 0xF, true);
+}
+
+// Merge two (smallest, second smallest) multiset pairs.
+__device__ __forceinline__ void pair_merge(int &a, int &b, int pa, int pb) {
+    const int lo = min(a, pa);
+    b = min(max(a, pa), min(b, pb));
+    a = lo;
+}
+
+// Smallest and second smallest key of the wave (as a multiset), returned in
+// every lane.  Butterfly: 4 DPP stages inside each 16-lane row, then the
+// gfx950 row-swap permutes for the 16- and 32-lane exchanges.
+__device__ __forceinline__ void wave_min2_key(int key, int &k1, int &k2) {
+    int a = key, b = kKeyNone;
+    pair_merge(a, b, dpp_full<kDppQuadXor1>(a), dpp_full<kDppQuadXor1>(b));
+    pair_merge(a, b, dpp_full<kDppQuadXor2>(a), dpp_full<kDppQuadXor2>(b));
+    pair_merge(a, b, dpp_full<kDppRowHalfMirror>(a), dpp_full<kDppRowHalfMirror>(b));
+    pair_merge(a, b, dpp_full<kDppRowMirror>(a), dpp_full<kDppRowMirror>(b));
+    u32x2 sa = __builtin_amdgcn_permlane16_swap((unsigned)a, (unsigned)a, false, false);
+    u32x2 sb = __builtin_amdgcn_permlane16_swap((unsigned)b, (unsigned)b, false, false);
+    a = (int)sa[0];
+    b = (int)sb[0];
+    pair_merge(a, b, (int)sa[1], (int)sb[1]);
+    sa = __builtin_amdgcn_permlane32_swap((unsigned)a, (unsigned)a, false, false);
+    sb = __builtin_amdgcn_permlane32_swap((unsigned)b, (unsigned)b, false, false);
+    a = (int)sa[0];
+    b = (int)sb[0];
+    pair_merge(a, b, (int)sa[1], (int)sb[1]);
+    k1 = a;
+    k2 = b;
+}
+
+// Smallest key of the wave, returned in every lane.
+__device__ __forceinline__ int wave_min_key(int key) {
+    int a = key;
+    a = min(a, dpp_full<kDppQuadXor1>(a));
+    a = min(a, dpp_full<kDppQuadXor2>(a));
+    a = min(a, dpp_full<kDppRowHalfMirror>(a));
+    a = min(a, dpp_full<kDppRowMirror>(a));
+    u32x2 s = __builtin_amdgcn_permlane16_swap((unsigned)a, (unsigned)a, false, false);
+    a = min((int)s[0], (int)s[1]);
+    s = __builtin_amdgcn_permlane32_swap((unsigned)a, (unsigned)a, false, false);
+    return min((int)s[0], (int)s[1]);
+}
+
+// Inclusive prefix minimum of keys across lanes 0..63.
+__device__ __forceinline__ int wave_prefix_min_key(int x) {
+    const int none = kKeyNone;
+    x = min(x, __builtin_amdgcn_update_dpp(none, x, kDppRowShr1, 0xF, 0xF, false));
+    x = min(x, __builtin_amdgcn_update_dpp(none, x, kDppRowShr2, 0xF, 0xF, false));
+    x = min(x, __builtin_amdgcn_update_dpp(none, x, kDppRowShr4, 0xF, 0xF, false));
+    x = min(x, __builtin_amdgcn_update_dpp(none, x, kDppRowShr8, 0xF, 0xF, false));
+    x = min(x, __builtin_amdgcn_update_dpp(none, x, kDppRowBcast15, 0xA, 0xF, false));
+    x = min(x, __builtin_amdgcn_update_dpp(none, x, kDppRowBcast31, 0xC, 0xF, false));
+    return x;
+}
+
+// Key of lane p-1 (lane 0 gets kKeyNone).
+__device__ __forceinline__ int wave_shift_up_key(int x) {
+    return __builtin_amdgcn_update_dpp(kKeyNone, x, kDppWaveShr1, 0xF, 0xF, false);
+}
+
+// Register-resident 64-entry column (lane j keeps c[0..63][j]); reads take a
+// wave-uniform row index and compile to indexed VGPR moves.
+typedef float f32x32 __attribute__((ext_vector_type(32)));
+struct Col64 {
+    f32x32 lo, hi;
+    __device__ __forceinline__ float get(int i) const {  // i uniform, 0 <= i < 64
+        return (i < 32) ? lo[i] : hi[i - 32];
+    }
+};
+
+} // namespace tmamd
+
+namespace tmamd {
+// Inverse of fkey (the transform is an involution on bit patterns); exact for
+// every float except -0.0, which fkey folds into +0.0.
+__device__ __forceinline__ float key_to_float(int k) {
+    return __int_as_float(k ^ ((k >> 31) & 0x7fffffff));
+}
+} // namespace tmamd
