@@ -538,6 +538,7 @@ __device__ __forceinline__ bool wave_solve(const int K, WaveLds &L, float v,
             const uint32_t rr_cap = (cur + 1) * (uint32_t)K;
             uint64_t okm;
             int inext;
+            float cnext;  // row of the displaced owner, loaded ahead
             {
                 const float rc = L.c[fi * kTile + lane] - v;
                 const int kc = live ? __float_as_int(rc) : kKeyNone;
@@ -545,6 +546,7 @@ __device__ __forceinline__ bool wave_solve(const int K, WaveLds &L, float v,
                 wave_min2_key(kc, c1, c2);
                 const int jc = first_lane(ballot(kc == c1));
                 inext = readlane_i(y, jc);
+                cnext = L.c[(inext & (kTile - 1)) * kTile + lane];
                 const float lowc = v - (__int_as_float(c2) - rc);
                 const bool okc = lane == jc && rr + 1 < rr_cap && lowc < v && y >= 0;
                 if (okc) {
@@ -556,12 +558,13 @@ __device__ __forceinline__ bool wave_solve(const int K, WaveLds &L, float v,
             while (true) {
                 // the displaced row, started before okm is consulted
                 const int fn = inext & (kTile - 1);
-                const float rn = L.c[fn * kTile + lane] - v;
+                const float rn = cnext - v;
                 const int kn = live ? __float_as_int(rn) : kKeyNone;
                 int n1, n2;
                 wave_min2_key(kn, n1, n2);
                 const int jn = first_lane(ballot(kn == n1));
                 const int inn = readlane_i(y, jn);
+                cnext = L.c[(inn & (kTile - 1)) * kTile + lane];
                 if (okm == 0)
                     break;  // fi's step leaves the chain: the general step redoes it
                 ++rr;       // fi's step is committed (its ++current / --current cancel)
@@ -725,6 +728,17 @@ jv_solve_kernel(const float *__restrict__ costs, int64_t B, int N, int M,
 
     float mx, mn;
     uint32_t flags;
+    const float *src = costs + b * (int64_t)N * M;
+    // Square 64 x 64 tiles: issue the whole 16 KiB tile as 16 float4 loads per
+    // lane before folding the statistics, so the HBM latency overlaps the fold.
+    const bool wide = N == kTile && M == kTile && ((uintptr_t)src % 16) == 0;
+    float4 q[16];
+    if (wide) {
+        const float4 *src4 = reinterpret_cast<const float4 *>(src);
+#pragma unroll
+        for (int k = 0; k < 16; ++k)
+            q[k] = src4[k * 64 + lane];
+    }
     fold_stats(partial, n_partial, mx, mn, flags);
     if (b == 0 && lane == 0)
         status[0] = flags;
@@ -744,27 +758,43 @@ jv_solve_kernel(const float *__restrict__ costs, int64_t B, int N, int M,
     if (has_inf && !(fabsf(sentinel) <= kFastRange))
         fast = false;
 
-    // tile load: lane j reads column j of every row (coalesced row reads),
-    // and keeps the running column minimum with the first arg-min row
-    // (strict '<' from LARGE, jonker_dense_flat.h:136-144)
-    const float *src = costs + b * (int64_t)N * M;
+    // tile into LDS (padding 0, +inf -> sentinel); then lane j scans column j
+    // for its minimum and first arg-min row (strict '<' from LARGE,
+    // jonker_dense_flat.h:136-144)
+    if (wide) {
+        auto fix = [&](float x) { return isfinite(x) ? x : sentinel; };
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+            float4 t = q[k];
+            t.x = fix(t.x);
+            t.y = fix(t.y);
+            t.z = fix(t.z);
+            t.w = fix(t.w);
+            reinterpret_cast<float4 *>(L.c)[k * 64 + lane] = t;
+        }
+    } else {
+#pragma unroll 16
+        for (int i = 0; i < K; ++i) {
+            float val = 0.f;
+            if (i < N && lane < M) {
+                val = src[(int64_t)i * M + lane];
+                if (!isfinite(val))
+                    val = sentinel;
+            }
+            L.c[i * kTile + lane] = val;
+        }
+    }
+    __syncthreads();
     float vmin = kLarge;
     int ymin = 0;
 #pragma unroll 16
     for (int i = 0; i < K; ++i) {
-        float val = 0.f;
-        if (i < N && lane < M) {
-            val = src[(int64_t)i * M + lane];
-            if (!isfinite(val))
-                val = sentinel;
-        }
-        L.c[i * kTile + lane] = val;
+        const float val = L.c[i * kTile + lane];
         if (val < vmin) {
             vmin = val;
             ymin = i;
         }
     }
-    __syncthreads();
 
     int x = -1;
     if (fast) {
