@@ -15,12 +15,23 @@
 // The reference's -80 stand-in for all-+inf rows/columns only feeds lanes that
 // the reference then overwrites with -inf, so those sweeps are skipped here.
 //
-// Data layout (all row-major, float32, resident in HBM for the whole call):
+// HBM layout (row-major float32, resident for the whole call):
 //   K       (B, N, M)  log kernel, rewritten only when the schedule's epsilon
 //                      changes (once for a constant schedule)
-//   log_u/v (B, N) / (B, M) caller's outputs, updated in place every step
-//   colpart (B, n_chunk, M) float2 (max, sum) column partials
-// Per step: row sweep (reads K once), column sweep (reads K once), merge.
+//   log_u/v (B, N) / (B, M) the caller's outputs, updated in place every step
+//   colpart (B, n_chunk, M) float2 (max, sum) partials, only when the column
+//                      sweep splits rows into several chunks (large B*M small)
+// One step = row sweep (reads K once) + column sweep (reads K once): the
+// algorithmic minimum of 2 * B*N*M*4 bytes.
+//
+// Row sweep: each wave owns whole rows; its lanes hold a 256*NV-column slice
+// of log_v in registers for all its rows, and each row is an exact two-pass
+// LSE over registers (max, then sum of exp) when M <= 256*NV, an online
+// per-chunk merge beyond.  Column sweep: a block owns a 64-column strip over a
+// chunk of rows; 16 threads span the strip with float4 loads, 16 row groups
+// fold rows online (one rescale per group of U rows), and an LDS merge of the
+// 16 row groups yields the column LSE (or a partial when rows are chunked).
+// exp / log run on the native v_exp_f32 / v_log_f32 (base 2).
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdint.h>
@@ -31,18 +42,75 @@
 namespace tmamd {
 namespace {
 
-constexpr int kRowBlock = 256;            // 4 waves, one row per wave
-constexpr int kColBlock = 256;            // 4 columns per thread
-constexpr int kColStrip = kColBlock * 4;  // columns per column-sweep block
 constexpr int kMapBlock = 256;
+constexpr int kRowWaves = 4;          // waves per row-sweep block
+constexpr int kRowsPerWave = 4;       // rows per wave (reuse of the log_v slice)
+constexpr int kRowNV = 8;             // float4 per lane per row chunk (2048 cols)
+constexpr int kColStripCols = 64;     // columns per column-sweep block
+constexpr int kColThreads = 256;      // 16 column threads x 16 row groups
+constexpr int kColGroups = kColThreads / (kColStripCols / 4);  // 16
+constexpr int kColU = 8;              // rows per group fold
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
 
 __device__ __forceinline__ float f_inf() { return __int_as_float(0x7f800000); }
 
+// e^(x) for x <= 0 (or -inf) on the native base-2 unit
+__device__ __forceinline__ float exp_nonpos(float x) { return __builtin_amdgcn_exp2f(x * kLog2e); }
+// natural log of s >= 0 (log(0) = -inf)
+__device__ __forceinline__ float ln(float s) { return __builtin_amdgcn_logf(s) * kLn2; }
+
+__device__ __forceinline__ float lse_shift(float m) { return isinf(m) ? 0.f : m; }
+
+struct Lse {
+    float m;  // running max (may be -inf)
+    float s;  // sum of exp(t - shift(m))
+};
+
+__device__ __forceinline__ Lse lse_merge(Lse p, Lse q) {
+    const float m = fmaxf(p.m, q.m);
+    const float sh = lse_shift(m);
+    const float a = (p.s == 0.f) ? 0.f : p.s * exp_nonpos(lse_shift(p.m) - sh);
+    const float c = (q.s == 0.f) ? 0.f : q.s * exp_nonpos(lse_shift(q.m) - sh);
+    return Lse{m, a + c};
+}
+
+__device__ __forceinline__ float lse_value(Lse p) { return ln(p.s) + lse_shift(p.m); }
+
+__device__ __forceinline__ float wave_sum(float x) {
+    x += __shfl_xor(x, 1, 64);
+    x += __shfl_xor(x, 2, 64);
+    x += __shfl_xor(x, 4, 64);
+    x += __shfl_xor(x, 8, 64);
+    x += __shfl_xor(x, 16, 64);
+    x += __shfl_xor(x, 32, 64);
+    return x;
+}
+
+__device__ __forceinline__ Lse wave_lse(Lse p) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        Lse q;
+        q.m = __shfl_xor(p.m, off, 64);
+        q.s = __shfl_xor(p.s, off, 64);
+        p = lse_merge(p, q);
+    }
+    return p;
+}
+
+__device__ __forceinline__ float update_potential(float lse, float log_marg, float old,
+                                                  float damp, bool unbalanced) {
+    if (!isfinite(lse))
+        return old;
+    const float diff = log_marg - lse;
+    return unbalanced ? damp * diff : diff;
+}
+
+// ---- workspace ----------------------------------------------------------------
+
 struct SinkhornLayout {
     int64_t B, N, M;
-    int n_chunk;      // row chunks of the column sweep
-    int rows_per_chunk;
-    int n_strip;      // column strips of the column sweep
+    int n_chunk, rows_per_chunk, n_strip;
     size_t off_k, off_logmu, off_lognu, off_infrow, off_infcol, off_colpart, total;
 };
 
@@ -53,16 +121,14 @@ SinkhornLayout make_layout(int64_t B, int64_t N, int64_t M) {
     L.B = B;
     L.N = N;
     L.M = M;
-    L.n_strip = (int)((M + kColStrip - 1) / kColStrip);
-    // aim for ~2048 column-sweep blocks, at least 16 rows per chunk
-    int64_t want = 2048 / (B * L.n_strip > 0 ? B * L.n_strip : 1);
-    if (want < 1)
-        want = 1;
-    int64_t rpc = (N + want - 1) / want;
-    if (rpc < 16)
-        rpc = 16;
-    L.rows_per_chunk = (int)rpc;
-    L.n_chunk = (int)((N + rpc - 1) / rpc);
+    L.n_strip = (int)((M + kColStripCols - 1) / kColStripCols);
+    // split rows only when the strips alone give too few blocks to fill 256 CUs
+    int64_t blocks = B * L.n_strip;
+    int64_t chunks = 1;
+    while (blocks * chunks < 1024 && N / (chunks * 2) >= 256)
+        chunks *= 2;
+    L.n_chunk = (int)chunks;
+    L.rows_per_chunk = (int)((N + chunks - 1) / chunks);
     size_t off = 0;
     L.off_k = off;
     off = align_up(off + sizeof(float) * (size_t)(B * N * M), 256);
@@ -75,12 +141,13 @@ SinkhornLayout make_layout(int64_t B, int64_t N, int64_t M) {
     L.off_infcol = off;
     off = align_up(off + (size_t)(B * M), 256);
     L.off_colpart = off;
-    off = align_up(off + sizeof(float2) * (size_t)B * L.n_chunk * (size_t)M, 256);
+    if (L.n_chunk > 1)
+        off = align_up(off + sizeof(float2) * (size_t)B * L.n_chunk * (size_t)M, 256);
     L.total = off;
     return L;
 }
 
-// ---- elementwise preparation ------------------------------------------------
+// ---- elementwise preparation ----------------------------------------------------
 
 // K = -C / e (IEEE division, as torch's `-cost / step_eps` in float32).
 __global__ void __launch_bounds__(kMapBlock)
@@ -118,10 +185,10 @@ sk_fill(float *__restrict__ y, int64_t n, float value) {
 }
 
 // inf_row[b, i] = all_j C[b, i, j] == +inf (one wave per row).
-__global__ void __launch_bounds__(kRowBlock)
+__global__ void __launch_bounds__(256)
 sk_inf_rows(const float *__restrict__ C, uint8_t *__restrict__ inf_row, int64_t rows,
             int64_t M) {
-    const int64_t r = (int64_t)blockIdx.x * (kRowBlock / 64) + threadIdx.x / 64;
+    const int64_t r = (int64_t)blockIdx.x * 4 + threadIdx.x / 64;
     if (r >= rows)
         return;
     const float *row = C + r * M;
@@ -148,103 +215,106 @@ sk_inf_cols(const float *__restrict__ C, uint8_t *__restrict__ inf_col, int64_t 
     inf_col[t] = all_inf ? 1 : 0;
 }
 
-// ---- log-sum-exp helpers --------------------------------------------------------
+// ---- row sweep: log_u -------------------------------------------------------------
 
-// Running (shift, sum) pair: sum = sum_k exp(t_k - shift), where shift is the
-// running max, or 0 while that max is -inf (torch.logsumexp's rule).
-struct Lse {
-    float m;  // running max (may be -inf)
-    float s;  // sum of exp(t - shift(m))
-};
-
-__device__ __forceinline__ float lse_shift(float m) { return isinf(m) ? 0.f : m; }
-
-// Combine two partial pairs.
-__device__ __forceinline__ Lse lse_merge(Lse p, Lse q) {
-    const float m = fmaxf(p.m, q.m);
-    const float sh = lse_shift(m);
-    const float a = (p.s == 0.f) ? 0.f : p.s * expf(lse_shift(p.m) - sh);
-    const float c = (q.s == 0.f) ? 0.f : q.s * expf(lse_shift(q.m) - sh);
-    return Lse{m, a + c};
-}
-
-__device__ __forceinline__ float lse_value(Lse p) {
-    return logf(p.s) + lse_shift(p.m);
-}
-
-// Fold a group of values t[0..G) into a running pair (rescale once per group).
-template <int G>
-__device__ __forceinline__ void lse_push(Lse &acc, const float (&t)[G]) {
-    float gm = t[0];
-#pragma unroll
-    for (int k = 1; k < G; ++k)
-        gm = fmaxf(gm, t[k]);
-    if (gm > acc.m) {
-        if (acc.s != 0.f)
-            acc.s *= expf(lse_shift(acc.m) - lse_shift(gm));
-        acc.m = gm;
-    }
-    const float sh = lse_shift(acc.m);
-    float add = 0.f;
-#pragma unroll
-    for (int k = 0; k < G; ++k)
-        add += expf(t[k] - sh);
-    acc.s += add;
-}
-
-__device__ __forceinline__ Lse wave_lse(Lse p) {
-    // butterfly over the wave with DPP-free shuffles (ds_swizzle/bpermute)
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) {
-        Lse q;
-        q.m = __shfl_xor(p.m, off, 64);
-        q.s = __shfl_xor(p.s, off, 64);
-        p = lse_merge(p, q);
-    }
-    return p;
-}
-
-__device__ __forceinline__ float update_potential(float lse, float log_marg, float old,
-                                                  float damp, bool unbalanced) {
-    if (!isfinite(lse))
-        return old;
-    const float diff = log_marg - lse;
-    return unbalanced ? damp * diff : diff;
-}
-
-// ---- row sweep: log_u ----------------------------------------------------------
-
-// One wave per row: lse_c = LSE_j(K[i, j] + log_v[j]), then the log_u update.
-__global__ void __launch_bounds__(kRowBlock)
+// Each wave owns kRowsPerWave consecutive rows of one batch.  M % 4 == 0.
+// Chunks of 256*kRowNV columns: log_v slice and the row slice in registers.
+__global__ void __launch_bounds__(kRowWaves * 64)
 sk_row_sweep(const float *__restrict__ K, const float *__restrict__ log_v,
              const float *__restrict__ log_mu, const uint8_t *__restrict__ inf_row,
-             float *__restrict__ log_u, int64_t B, int64_t N, int64_t M, float damp,
-             int unbalanced) {
-    const int64_t r = (int64_t)blockIdx.x * (kRowBlock / 64) + threadIdx.x / 64;
+             float *__restrict__ log_u, int64_t n_batch, int64_t N, int64_t M,
+             int64_t waves_per_batch, float damp, int unbalanced) {
+    const int64_t gw = (int64_t)blockIdx.x * kRowWaves + threadIdx.x / 64;
+    const int64_t b = gw / waves_per_batch;
+    if (b >= n_batch)
+        return;  // surplus waves of the last block
+    const int64_t i_begin = (gw % waves_per_batch) * kRowsPerWave;
+    const int lane = lane_id();
+    const int64_t m4 = M / 4;
+    const float4 *lv4 = reinterpret_cast<const float4 *>(log_v + b * M);
+    constexpr int CH = 64 * kRowNV;  // float4 per chunk
+    const bool single_chunk = m4 <= CH;
+    float4 lv[kRowNV];
+    if (single_chunk) {
+#pragma unroll
+        for (int k = 0; k < kRowNV; ++k) {
+            const int64_t q = (int64_t)k * 64 + lane;
+            lv[k] = q < m4 ? lv4[q] : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    }
+    for (int rr = 0; rr < kRowsPerWave; ++rr) {
+        const int64_t i = i_begin + rr;
+        if (i >= N)
+            break;
+        const int64_t r = b * N + i;
+        if (inf_row[r])
+            continue;  // lse = -inf: log_u keeps its value
+        const float4 *row4 = reinterpret_cast<const float4 *>(K + r * M);
+        Lse acc{-f_inf(), 0.f};
+        for (int64_t base = 0; base < m4; base += CH) {
+            float t[4 * kRowNV];
+#pragma unroll
+            for (int k = 0; k < kRowNV; ++k) {
+                const int64_t q = base + (int64_t)k * 64 + lane;
+                if (q < m4) {
+                    const float4 kk = row4[q];
+                    const float4 vv = single_chunk ? lv[k] : lv4[q];
+                    t[4 * k + 0] = kk.x + vv.x;
+                    t[4 * k + 1] = kk.y + vv.y;
+                    t[4 * k + 2] = kk.z + vv.z;
+                    t[4 * k + 3] = kk.w + vv.w;
+                } else {
+                    t[4 * k + 0] = t[4 * k + 1] = t[4 * k + 2] = t[4 * k + 3] = -f_inf();
+                }
+            }
+            float m = t[0];
+#pragma unroll
+            for (int k = 1; k < 4 * kRowNV; ++k)
+                m = fmaxf(m, t[k]);
+            m = wave_max(m);  // the chunk maximum, in every lane
+            const float newm = fmaxf(acc.m, m);
+            const float sh = lse_shift(newm);
+            float s = 0.f;
+#pragma unroll
+            for (int k = 0; k < 4 * kRowNV; ++k)
+                s += exp_nonpos(t[k] - sh);
+            s = wave_sum(s);
+            if (acc.s != 0.f)
+                s += acc.s * exp_nonpos(lse_shift(acc.m) - sh);
+            acc.m = newm;
+            acc.s = s;
+        }
+        if (lane == 0) {
+            const float lse = lse_value(acc);
+            log_u[r] = update_potential(lse, log_mu[r], log_u[r], damp, unbalanced != 0);
+        }
+    }
+}
+
+// Generic row sweep for M % 4 != 0: one wave per row, online LSE.
+__global__ void __launch_bounds__(256)
+sk_row_sweep_scalar(const float *__restrict__ K, const float *__restrict__ log_v,
+                    const float *__restrict__ log_mu, const uint8_t *__restrict__ inf_row,
+                    float *__restrict__ log_u, int64_t B, int64_t N, int64_t M, float damp,
+                    int unbalanced) {
+    const int64_t r = (int64_t)blockIdx.x * 4 + threadIdx.x / 64;
     if (r >= B * N)
         return;
     const int64_t b = r / N;
     const int lane = lane_id();
     if (inf_row[r])
-        return;  // lse = -inf: log_u keeps its value
+        return;
     const float *row = K + r * M;
     const float *lv = log_v + b * M;
     Lse acc{-f_inf(), 0.f};
-    if ((M & 3) == 0) {
-        const float4 *row4 = reinterpret_cast<const float4 *>(row);
-        const float4 *lv4 = reinterpret_cast<const float4 *>(lv);
-        const int64_t m4 = M / 4;
-        for (int64_t q = lane; q < m4; q += 64) {
-            const float4 k = row4[q];
-            const float4 v = lv4[q];
-            const float t[4] = {k.x + v.x, k.y + v.y, k.z + v.z, k.w + v.w};
-            lse_push<4>(acc, t);
+    for (int64_t j = lane; j < M; j += 64) {
+        const float t = row[j] + lv[j];
+        if (t > acc.m) {
+            if (acc.s != 0.f)
+                acc.s *= exp_nonpos(lse_shift(acc.m) - lse_shift(t));
+            acc.m = t;
         }
-    } else {
-        for (int64_t j = lane; j < M; j += 64) {
-            const float t[1] = {row[j] + lv[j]};
-            lse_push<1>(acc, t);
-        }
+        acc.s += exp_nonpos(t - lse_shift(acc.m));
     }
     acc = wave_lse(acc);
     if (lane == 0) {
@@ -253,49 +323,99 @@ sk_row_sweep(const float *__restrict__ K, const float *__restrict__ log_v,
     }
 }
 
-// ---- column sweep: log_v -------------------------------------------------------
+// ---- column sweep: log_v ----------------------------------------------------------
 
-// grid (n_strip, n_chunk, B); thread t owns columns strip*1024 + 4t .. +3 and
-// folds rows [chunk*R, chunk*R + R) into per-column partial pairs.
-__global__ void __launch_bounds__(kColBlock)
-sk_col_partial(const float *__restrict__ K, const float *__restrict__ log_u,
-               float2 *__restrict__ colpart, int64_t N, int64_t M, int rows_per_chunk,
-               int n_chunk) {
+// grid (n_strip, n_chunk, B).  Thread tc = tid % 16 owns columns
+// strip*64 + 4*tc .. +3, row group tg = tid / 16 folds rows chunk_start + tg,
+// + 16, ... .  With one chunk the block finishes the LSE and updates log_v;
+// otherwise it writes (max, sum) partials for sk_col_merge.
+template <bool VEC>
+__global__ void __launch_bounds__(kColThreads)
+sk_col_sweep(const float *__restrict__ K, const float *__restrict__ log_u,
+             const float *__restrict__ log_nu, const uint8_t *__restrict__ inf_col,
+             float *__restrict__ log_v, float2 *__restrict__ colpart, int64_t N, int64_t M,
+             int rows_per_chunk, int n_chunk, float damp, int unbalanced) {
     const int strip = blockIdx.x, chunk = blockIdx.y;
     const int64_t b = blockIdx.z;
-    const int64_t j0 = (int64_t)strip * kColStrip + 4 * threadIdx.x;
+    const int tc = threadIdx.x % (kColStripCols / 4);
+    const int tg = threadIdx.x / (kColStripCols / 4);
+    const int64_t j0 = (int64_t)strip * kColStripCols + 4 * tc;
     const int64_t i0 = (int64_t)chunk * rows_per_chunk;
     const int64_t i1 = (i0 + rows_per_chunk < N) ? i0 + rows_per_chunk : N;
     const float *Kb = K + b * N * M;
     const float *lu = log_u + b * N;
-    Lse acc[4] = {{-f_inf(), 0.f}, {-f_inf(), 0.f}, {-f_inf(), 0.f}, {-f_inf(), 0.f}};
-    if (j0 < M) {
-        if ((M & 3) == 0) {
-            for (int64_t i = i0; i < i1; ++i) {
-                const float4 k = *reinterpret_cast<const float4 *>(Kb + i * M + j0);
-                const float u = lu[i];
-                const float t0[1] = {k.x + u}, t1[1] = {k.y + u}, t2[1] = {k.z + u},
-                            t3[1] = {k.w + u};
-                lse_push<1>(acc[0], t0);
-                lse_push<1>(acc[1], t1);
-                lse_push<1>(acc[2], t2);
-                lse_push<1>(acc[3], t3);
-            }
-        } else {
-            for (int64_t i = i0; i < i1; ++i) {
-                const float u = lu[i];
+    Lse acc[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+        acc[c] = Lse{-f_inf(), 0.f};
+    const bool colok = j0 < M;
+    for (int64_t ib = i0 + tg; ib < i1; ib += (int64_t)kColGroups * kColU) {
+        float t[kColU][4];
+#pragma unroll
+        for (int u = 0; u < kColU; ++u) {
+            const int64_t i = ib + (int64_t)u * kColGroups;
+            if (colok && i < i1) {
+                const float lui = lu[i];
+                if (VEC) {
+                    const float4 k4 = *reinterpret_cast<const float4 *>(Kb + i * M + j0);
+                    t[u][0] = k4.x + lui;
+                    t[u][1] = k4.y + lui;
+                    t[u][2] = k4.z + lui;
+                    t[u][3] = k4.w + lui;
+                } else {
+#pragma unroll
+                    for (int c = 0; c < 4; ++c)
+                        t[u][c] = (j0 + c < M) ? Kb[i * M + j0 + c] + lui : -f_inf();
+                }
+            } else {
 #pragma unroll
                 for (int c = 0; c < 4; ++c)
-                    if (j0 + c < M) {
-                        const float t[1] = {Kb[i * M + j0 + c] + u};
-                        lse_push<1>(acc[c], t);
-                    }
+                    t[u][c] = -f_inf();
             }
         }
 #pragma unroll
-        for (int c = 0; c < 4; ++c)
-            if (j0 + c < M)
-                colpart[(b * n_chunk + chunk) * M + j0 + c] = make_float2(acc[c].m, acc[c].s);
+        for (int c = 0; c < 4; ++c) {
+            float gm = t[0][c];
+#pragma unroll
+            for (int u = 1; u < kColU; ++u)
+                gm = fmaxf(gm, t[u][c]);
+            if (gm > acc[c].m) {
+                if (acc[c].s != 0.f)
+                    acc[c].s *= exp_nonpos(lse_shift(acc[c].m) - lse_shift(gm));
+                acc[c].m = gm;
+            }
+            const float sh = lse_shift(acc[c].m);
+            float add = 0.f;
+#pragma unroll
+            for (int u = 0; u < kColU; ++u)
+                add += exp_nonpos(t[u][c] - sh);
+            acc[c].s += add;
+        }
+    }
+    // merge the 16 row groups of each column in LDS
+    __shared__ float2 part[kColGroups][kColStripCols];
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+        part[tg][4 * tc + c] = make_float2(acc[c].m, acc[c].s);
+    __syncthreads();
+    if (threadIdx.x < kColStripCols) {
+        const int cc = threadIdx.x;
+        const int64_t j = (int64_t)strip * kColStripCols + cc;
+        if (j < M) {
+            Lse tot{-f_inf(), 0.f};
+#pragma unroll
+            for (int g = 0; g < kColGroups; ++g)
+                tot = lse_merge(tot, Lse{part[g][cc].x, part[g][cc].y});
+            if (n_chunk == 1) {
+                const int64_t t = b * M + j;
+                if (!inf_col[t]) {
+                    const float lse = lse_value(tot);
+                    log_v[t] = update_potential(lse, log_nu[t], log_v[t], damp, unbalanced != 0);
+                }
+            } else {
+                colpart[(b * n_chunk + chunk) * M + j] = make_float2(tot.m, tot.s);
+            }
+        }
     }
 }
 
@@ -319,9 +439,35 @@ sk_col_merge(const float2 *__restrict__ colpart, const float *__restrict__ log_n
     log_v[t] = update_potential(lse, log_nu[t], log_v[t], damp, unbalanced != 0);
 }
 
-// ---- final plan ----------------------------------------------------------------
+// ---- final plan -------------------------------------------------------------------
 
-// log_plan[b,i,j] = (log_u[b,i] + (-C[b,i,j] / e)) + log_v[b,j]
+// log_plan[b,i,j] = (log_u[b,i] + (-C[b,i,j] / e)) + log_v[b,j]; M % 4 == 0 path
+// with float4 rows, generic path otherwise.
+__global__ void __launch_bounds__(kMapBlock)
+sk_plan4(const float *__restrict__ C, const float *__restrict__ log_u,
+         const float *__restrict__ log_v, float *__restrict__ plan, int64_t B, int64_t N,
+         int64_t M, float eps) {
+    const int64_t m4 = M / 4;
+    const int64_t n4 = B * N * m4;
+    const int64_t stride = (int64_t)gridDim.x * kMapBlock;
+    const float4 *c4 = reinterpret_cast<const float4 *>(C);
+    float4 *p4 = reinterpret_cast<float4 *>(plan);
+    for (int64_t k = (int64_t)blockIdx.x * kMapBlock + threadIdx.x; k < n4; k += stride) {
+        const int64_t row = k / m4;
+        const int64_t q = k - row * m4;
+        const int64_t b = row / N;
+        const float u = log_u[row];
+        const float4 v = reinterpret_cast<const float4 *>(log_v + b * M)[q];
+        const float4 c = c4[k];
+        float4 o;
+        o.x = (u + (-c.x / eps)) + v.x;
+        o.y = (u + (-c.y / eps)) + v.y;
+        o.z = (u + (-c.z / eps)) + v.z;
+        o.w = (u + (-c.w / eps)) + v.w;
+        p4[k] = o;
+    }
+}
+
 __global__ void __launch_bounds__(kMapBlock)
 sk_plan(const float *__restrict__ C, const float *__restrict__ log_u,
         const float *__restrict__ log_v, float *__restrict__ plan, int64_t B, int64_t N,
@@ -368,7 +514,7 @@ extern "C" int tm_sinkhorn_f32(const float *cost, const float *a, const float *b
     const SinkhornLayout L = make_layout(B, N, M);
     if (workspace == nullptr || workspace_bytes < L.total)
         return TM_ERR_WORKSPACE;
-    if (L.n_strip > 65535 || L.n_chunk > 65535 || B > 65535)
+    if (L.n_strip > 0x7fffffff || L.n_chunk > 65535 || B > 65535)
         return TM_ERR_UNSUPPORTED_SHAPE;
     char *ws = static_cast<char *>(workspace);
     float *K = reinterpret_cast<float *>(ws + L.off_k);
@@ -379,6 +525,7 @@ extern "C" int tm_sinkhorn_f32(const float *cost, const float *a, const float *b
     float2 *colpart = reinterpret_cast<float2 *>(ws + L.off_colpart);
     const bool unbalanced = rho > 0.0;
     const int64_t nK = B * N * M;
+    const bool vec = (M % 4) == 0 && ((uintptr_t)cost % 16) == 0 && ((uintptr_t)log_v % 16) == 0;
 
 #define TM_LAUNCH(...)                                                                    \
     do {                                                                                  \
@@ -395,12 +542,16 @@ extern "C" int tm_sinkhorn_f32(const float *cost, const float *a, const float *b
               log_u, B * N, 0.f);
     TM_LAUNCH(sk_fill, dim3(grid_for(B * M, kMapBlock, 1 << 30)), dim3(kMapBlock), 0, stream,
               log_v, B * M, 0.f);
-    TM_LAUNCH(sk_inf_rows, dim3(grid_for(B * N, kRowBlock / 64, 1 << 30)), dim3(kRowBlock), 0,
-              stream, cost, inf_row, B * N, M);
+    TM_LAUNCH(sk_inf_rows, dim3(grid_for(B * N, 4, 1 << 30)), dim3(256), 0, stream, cost,
+              inf_row, B * N, M);
     TM_LAUNCH(sk_inf_cols, dim3(grid_for(B * M, kMapBlock, 1 << 30)), dim3(kMapBlock), 0,
               stream, cost, inf_col, B, N, M);
 
     const int map_grid = grid_for(nK / 4 + 1, kMapBlock, 8192);
+    const int64_t waves_per_batch = (N + kRowsPerWave - 1) / kRowsPerWave;
+    const int64_t row_waves = B * waves_per_batch;
+    const dim3 row_grid((unsigned)((row_waves + kRowWaves - 1) / kRowWaves));
+    const dim3 col_grid((unsigned)L.n_strip, (unsigned)L.n_chunk, (unsigned)B);
     float cur_eps = -1.f;
     for (int32_t s = 0; s < n_iter; ++s) {
         const float e = (float)eps_sched[s];
@@ -409,19 +560,33 @@ extern "C" int tm_sinkhorn_f32(const float *cost, const float *a, const float *b
             cur_eps = e;
         }
         const float damp = unbalanced ? (float)(1.0 / (1.0 + eps_sched[s] / rho)) : 1.f;
-        TM_LAUNCH(sk_row_sweep, dim3(grid_for(B * N, kRowBlock / 64, 1 << 30)), dim3(kRowBlock),
-                  0, stream, K, log_v, log_mu, inf_row, log_u, B, N, M, damp,
-                  unbalanced ? 1 : 0);
-        TM_LAUNCH(sk_col_partial, dim3(L.n_strip, L.n_chunk, (unsigned)B), dim3(kColBlock), 0,
-                  stream, K, log_u, colpart, N, M, L.rows_per_chunk, L.n_chunk);
-        TM_LAUNCH(sk_col_merge, dim3(grid_for(B * M, kMapBlock, 1 << 30)), dim3(kMapBlock), 0,
-                  stream, colpart, log_nu, inf_col, log_v, B, M, L.n_chunk, damp,
-                  unbalanced ? 1 : 0);
+        if (vec) {
+            TM_LAUNCH(sk_row_sweep, row_grid, dim3(kRowWaves * 64), 0, stream, K, log_v, log_mu,
+                      inf_row, log_u, B, N, M, waves_per_batch, damp, unbalanced ? 1 : 0);
+            TM_LAUNCH(sk_col_sweep<true>, col_grid, dim3(kColThreads), 0, stream, K, log_u,
+                      log_nu, inf_col, log_v, colpart, N, M, L.rows_per_chunk, L.n_chunk, damp,
+                      unbalanced ? 1 : 0);
+        } else {
+            TM_LAUNCH(sk_row_sweep_scalar, dim3(grid_for(B * N, 4, 1 << 30)), dim3(256), 0,
+                      stream, K, log_v, log_mu, inf_row, log_u, B, N, M, damp,
+                      unbalanced ? 1 : 0);
+            TM_LAUNCH(sk_col_sweep<false>, col_grid, dim3(kColThreads), 0, stream, K, log_u,
+                      log_nu, inf_col, log_v, colpart, N, M, L.rows_per_chunk, L.n_chunk, damp,
+                      unbalanced ? 1 : 0);
+        }
+        if (L.n_chunk > 1)
+            TM_LAUNCH(sk_col_merge, dim3(grid_for(B * M, kMapBlock, 1 << 30)), dim3(kMapBlock),
+                      0, stream, colpart, log_nu, inf_col, log_v, B, M, L.n_chunk, damp,
+                      unbalanced ? 1 : 0);
     }
     if (log_plan != nullptr) {
         const float ef = (float)eps_sched[n_iter - 1];
-        TM_LAUNCH(sk_plan, dim3(grid_for(nK, kMapBlock, 8192)), dim3(kMapBlock), 0, stream,
-                  cost, log_u, log_v, log_plan, B, N, M, ef);
+        if (vec && ((uintptr_t)log_plan % 16) == 0)
+            TM_LAUNCH(sk_plan4, dim3(grid_for(nK / 4, kMapBlock, 8192)), dim3(kMapBlock), 0,
+                      stream, cost, log_u, log_v, log_plan, B, N, M, ef);
+        else
+            TM_LAUNCH(sk_plan, dim3(grid_for(nK, kMapBlock, 8192)), dim3(kMapBlock), 0, stream,
+                      cost, log_u, log_v, log_plan, B, N, M, ef);
     }
 #undef TM_LAUNCH
     return TM_OK;
