@@ -92,6 +92,18 @@ def test_random_batches_vs_oracle(kind, device):
         np.testing.assert_array_equal(got, want, err_msg=f"{kind} {(b, n, m)}")
 
 
+@pytest.mark.parametrize("kind", ["uniform", "tied", "masked", "tied_masked", "negative"])
+def test_large_k_vs_oracle(kind, device):
+    """K > 64: the global-memory kernel (cost outside LDS)."""
+    rng = np.random.default_rng(zlib.crc32(("large" + kind).encode()))
+    for n, m in [(65, 65), (100, 80), (80, 100), (128, 128), (200, 130), (300, 300)]:
+        c = _random_batch(rng, kind, 6, n, m)
+        want = jv.jv_dense_batch(c)
+        print(f"large kind {kind} shape {(6, n, m)}", flush=True)
+        got = run_op(torch.from_numpy(c), device)
+        np.testing.assert_array_equal(got, want, err_msg=f"{kind} {(6, n, m)}")
+
+
 def test_c2_full_size_mapping_and_total_cost(device):
     cost = workloads.jv_uniform(1024, 64, 64, seed=0)
     want = jv.jv_dense_batch(cost.numpy())

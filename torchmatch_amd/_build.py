@@ -27,7 +27,7 @@ LIB_DIR = PKG / "lib"
 CABI_SO = LIB_DIR / "libtorchmatch_amd.so"
 OPS_SO = PKG / "_C.so"
 
-HIP_SOURCES = ["jv_batch.hip", "sinkhorn.hip"]
+HIP_SOURCES = ["jv_batch.hip", "jv_large.hip", "sinkhorn.hip"]
 ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
 ARCH = "gfx950"
 

@@ -1,6 +1,7 @@
 // jv_batch.h -- internal declarations shared by the JV kernels and the C ABI.
 #pragma once
 
+#include <hip/hip_runtime_api.h>
 #include <stdint.h>
 
 #include "../../include/torchmatch_amd.h"
@@ -29,5 +30,11 @@ struct JvStats {
     uint32_t flags;
     uint32_t pad;
 };
+
+// K in (64, jv_large_max_k()]: one workgroup per problem, cost read from
+// global memory (jv_large.hip).
+int launch_jv_large(const float *costs, int64_t B, int N, int M, const JvStats *partial,
+                    int n_partial, int64_t *out, uint32_t *status, hipStream_t stream);
+int jv_large_max_k();
 
 } // namespace tmamd

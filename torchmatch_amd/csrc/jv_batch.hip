@@ -35,17 +35,14 @@
 #include <stdint.h>
 
 #include "jv_batch.h"
+#include "jv_common.h"
 #include "wave.h"
 
 namespace tmamd {
 namespace {
 
-constexpr float kLarge = 1e18f;          // jonker_dense_flat.h:22-23
-constexpr float kFastRange = 1e15f;      // wave path valid for |cost| <= this
 constexpr int kTile = 64;                // K <= 64 path
 constexpr int kStatsBlock = 256;
-
-__device__ __forceinline__ float finf() { return __int_as_float(0x7f800000); }
 
 // ---------------------------------------------------------------------------
 // 1. statistics pass
@@ -113,26 +110,6 @@ jv_stats_kernel(const float *__restrict__ costs, int64_t n, JvStats *__restrict_
         partial[blockIdx.x].flags = f;
         partial[blockIdx.x].pad = 0;
     }
-}
-
-// Fold the per-block partials (uniform result in every lane of the wave).
-__device__ __forceinline__ void fold_stats(const JvStats *__restrict__ partial, int n_partial,
-                                           float &mx, float &mn, uint32_t &flags) {
-    mx = -finf();
-    mn = finf();
-    uint32_t f = 0;
-    for (int k = lane_id(); k < n_partial; k += 64) {
-        mx = fmaxf(mx, partial[k].max_finite);
-        mn = fminf(mn, partial[k].min_finite);
-        f |= partial[k].flags;
-    }
-    mx = wave_max(mx);
-    mn = wave_min(mn);
-    flags = 0;
-#pragma unroll
-    for (int bit = 0; bit < 5; ++bit)
-        if (ballot((f >> bit) & 1u))
-            flags |= 1u << bit;
 }
 
 // ---------------------------------------------------------------------------
@@ -840,7 +817,7 @@ extern "C" int tm_jv_dense_batch_f32(const float *costs, int64_t B, int32_t N, i
     if (B == 0 || N == 0 || M == 0)
         return kTmOk;  // caller fills -1
     const int K = N > M ? N : M;
-    if (K > kTile)
+    if (K > jv_large_max_k())
         return kTmErrUnsupportedShape;
     if (workspace_bytes < tm_jv_workspace_bytes(B, N, M) || workspace == nullptr ||
         d_status == nullptr)
@@ -856,13 +833,15 @@ extern "C" int tm_jv_dense_batch_f32(const float *costs, int64_t B, int32_t N, i
     hipError_t e = hipGetLastError();
     if (e != hipSuccess)
         return kTmErrLaunch;
+    if (K > kTile)
+        return launch_jv_large(costs, B, N, M, partial, (int)blocks, out, d_status, stream);
     hipLaunchKernelGGL(jv_solve_kernel, dim3((unsigned)B), dim3(64), 0, stream, costs, B, N, M,
                        partial, (int)blocks, out, d_status);
     e = hipGetLastError();
     return e == hipSuccess ? kTmOk : kTmErrLaunch;
 }
 
-extern "C" int32_t tm_jv_max_k(void) { return kTile; }
+extern "C" int32_t tm_jv_max_k(void) { return jv_large_max_k(); }
 
 extern "C" int tm_jv_check_status(const uint32_t *d_status, hipStream_t stream) {
     uint32_t words[2] = {0, 0};

@@ -1,0 +1,539 @@
+// jv_large.hip -- batched Jonker-Volgenant for 64 < K <= 1024 (gfx950).
+//
+// Same contract as the K <= 64 kernel in jv_batch.hip: the int64 row->col
+// mapping of torchmatch's CPU `jonker_dense_batch` bit for bit
+// (sources/torchmatch/assignment/cpu/ops.cpp:176-289,
+//  sources/torchmatch/assignment/cpu/jonker_dense_flat.h:27-274).
+//
+// One 64-lane workgroup per problem.  A K x K tile no longer fits in LDS, so
+// the cost is read from global memory (L2 / Infinity Cache) through a view
+// that pads virtually (rows >= N and columns >= M read 0) and maps +inf to
+// the batch sentinel -- the padded tile is never materialised.  Per-column
+// state (v, y, d, pred), per-row state (x), the free-row list and the cols[]
+// permutation live in LDS (about 36 KiB).  Lane l handles columns / positions
+// l, l + 64, l + 128, ... of every K-wide pass; passes that must respect the
+// reference's sequential order (first index on ties, the swaps of find_dense
+// and scan_dense) are resolved with per-chunk ballots in increasing index
+// order, and the swap sequence itself is replayed by lane 0 on cols[] -- swaps
+// are rare events, the K-wide relaxations around them are parallel.
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdint.h>
+
+#include "jv_batch.h"
+#include "jv_common.h"
+#include "wave.h"
+
+namespace tmamd {
+namespace {
+
+constexpr int kMaxLargeK = 1024;
+constexpr int kMaxChunks = kMaxLargeK / 64;
+
+struct LargeLds {
+    float v[kMaxLargeK];
+    float d[kMaxLargeK];
+    float rbuf[kMaxLargeK];
+    int32_t y[kMaxLargeK];
+    int32_t x[kMaxLargeK];
+    int32_t fr[kMaxLargeK];
+    int32_t pred[kMaxLargeK];
+    int32_t cols[kMaxLargeK];
+    int32_t ev[kMaxLargeK];  // claims in the column reduction, swap events later
+};
+
+// The virtually padded K x K tile: 0 outside (N, M), +inf -> sentinel.
+struct CostView {
+    const float *src;
+    int N, M;
+    float sentinel;
+    __device__ __forceinline__ float at(int i, int j) const {
+        if (i >= N || j >= M)
+            return 0.f;
+        const float c = src[(int64_t)i * M + j];
+        return isfinite(c) ? c : sentinel;
+    }
+};
+
+__device__ __forceinline__ void lds_sync() { __syncthreads(); }
+
+// Lane-0 serial swap replay: events are positions with bit 31 set for a new
+// running minimum (swap with lo) and clear for a tie (swap with hi).
+__device__ __forceinline__ int replay_find_events(LargeLds &L, int n_ev, int lo) {
+    int hi = lo + 1;
+    for (int k = 0; k < n_ev; ++k) {
+        const int e = L.ev[k];
+        const int pos = e & 0x7fffffff;
+        if (e < 0) {
+            const int t = L.cols[pos];
+            L.cols[pos] = L.cols[lo];
+            L.cols[lo] = t;
+            hi = lo + 1;
+        } else {
+            const int t = L.cols[pos];
+            L.cols[pos] = L.cols[hi];
+            L.cols[hi] = t;
+            ++hi;
+        }
+    }
+    return hi;
+}
+
+// Append the set bits of `mask` (positions base + lane) to L.ev in increasing
+// order, tagged with `tag`; returns the new count (uniform).
+__device__ __forceinline__ int append_events(LargeLds &L, int n_ev, uint64_t mask, int base,
+                                             uint32_t tag_mask_rec, uint64_t rec_mask) {
+    const int lane = lane_id();
+    const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+    if ((mask >> lane) & 1ull) {
+        const int slot = n_ev + __builtin_popcountll(mask & below);
+        const bool rec = (rec_mask >> lane) & 1ull;
+        L.ev[slot] = (base + lane) | (rec ? (int)tag_mask_rec : 0);
+    }
+    return n_ev + __builtin_popcountll(mask);
+}
+
+__device__ bool large_solve(const int K, const int E, LargeLds &L, const CostView &C) {
+    const int lane = lane_id();
+
+    // ---- column reduction (ccrrt_dense, jonker_dense_flat.h:124-176) ----
+    {
+        float vmin[kMaxChunks];
+        int ymin[kMaxChunks];
+#pragma unroll
+        for (int e = 0; e < kMaxChunks; ++e) {
+            vmin[e] = kLarge;
+            ymin[e] = 0;
+        }
+        const int rows_real = C.N < K ? C.N : K;
+        for (int i = 0; i < rows_real; ++i) {
+#pragma unroll
+            for (int e = 0; e < kMaxChunks; ++e) {
+                const int j = e * 64 + lane;
+                if (e < E && j < K) {
+                    const float c = C.at(i, j);
+                    if (c < vmin[e]) {
+                        vmin[e] = c;
+                        ymin[e] = i;
+                    }
+                }
+            }
+        }
+        // padding rows (all 0): the first one wins where 0 is a strict new minimum
+#pragma unroll
+        for (int e = 0; e < kMaxChunks; ++e) {
+            const int j = e * 64 + lane;
+            if (e < E && j < K) {
+                if (rows_real < K && 0.f < vmin[e]) {
+                    vmin[e] = 0.f;
+                    ymin[e] = rows_real;
+                }
+                L.v[j] = vmin[e];
+                L.y[j] = ymin[e];
+                L.x[j] = -1;   // K rows == K columns
+                L.ev[j] = 0;   // claim counts
+            }
+        }
+    }
+    lds_sync();
+    for (int e = 0; e < E; ++e) {
+        const int j = e * 64 + lane;
+        if (j < K) {
+            atomicMax(&L.x[L.y[j]], j);
+            atomicAdd(&L.ev[L.y[j]], 1);
+        }
+    }
+    lds_sync();
+    for (int e = 0; e < E; ++e) {
+        const int j = e * 64 + lane;
+        if (j < K && L.x[L.y[j]] != j)
+            L.y[j] = -1;
+    }
+    lds_sync();
+    // free rows in increasing order, then reduction transfer for unique rows
+    int n_free = 0;
+    for (int e = 0; e < E; ++e) {
+        const int i = e * 64 + lane;
+        const bool fre = i < K && L.x[i] < 0;
+        const uint64_t m = ballot(fre);
+        const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+        if (fre)
+            L.fr[n_free + __builtin_popcountll(m & below)] = i;
+        n_free += __builtin_popcountll(m);
+    }
+    lds_sync();
+    for (int e = 0; e < E; ++e) {
+        uint64_t t = ballot(e * 64 + lane < K && L.x[e * 64 + lane] >= 0 &&
+                            L.ev[e * 64 + lane] <= 1);
+        while (t) {
+            const int i = e * 64 + first_lane(t);
+            t &= t - 1;
+            const int own = L.x[i];
+            // mn = LARGE, then `if (c < mn) mn = c` over j != own in order
+            int best = kKeyNone;
+            for (int e2 = 0; e2 < E; ++e2) {
+                const int j = e2 * 64 + lane;
+                float r = finf();
+                if (j < K && j != own)
+                    r = C.at(i, j) - L.v[j];
+                if (j < K)
+                    L.rbuf[j] = r;
+                if (j < K && j != own)
+                    best = min(best, fkey(r));
+            }
+            best = uniform_i(wave_min_key(best));
+            lds_sync();
+            float mn = kLarge;
+            if (best < fkey(kLarge)) {
+                for (int e2 = 0; e2 < E; ++e2) {
+                    const int j = e2 * 64 + lane;
+                    const uint64_t hit = ballot(j < K && j != own && fkey(L.rbuf[j]) == best);
+                    if (hit) {
+                        mn = L.rbuf[e2 * 64 + first_lane(hit)];
+                        break;
+                    }
+                }
+            }
+            if (lane == 0)
+                L.v[own] -= mn;
+            lds_sync();
+        }
+    }
+
+    // ---- augmenting row reduction (carr_dense, jonker_dense_flat.h:178-235) ----
+    const uint32_t rr_limit = 4u * (uint32_t)K * (uint32_t)K + 64u;
+    for (int round = 0; n_free > 0 && round < 2; ++round) {
+        uint32_t cur = 0, rr = 0;
+        int still = 0;
+        while (cur < (uint32_t)n_free) {
+            ++rr;
+            if (rr > rr_limit)
+                return false;
+            const int fi = L.fr[cur];
+            ++cur;
+            // reduced costs of row fi, lane-local two-minimum by (value, column)
+            int a = kKeyNone, bk = kKeyNone;
+            for (int e = 0; e < E; ++e) {
+                const int j = e * 64 + lane;
+                if (j < K) {
+                    const float r = C.at(fi, j) - L.v[j];
+                    L.rbuf[j] = r;
+                    const int k = fkey(r);
+                    if (k < a) {
+                        bk = a;
+                        a = k;
+                    } else if (k < bk) {
+                        bk = k;
+                    }
+                }
+            }
+            int k1, k2;
+            {
+                int p1, p2;
+                wave_min2_key(a, p1, p2);
+                // the multiset two-minimum of the per-lane pairs: merge with b
+                const int bmin = uniform_i(wave_min_key(bk));
+                k1 = uniform_i(p1);
+                k2 = min(uniform_i(p2), bmin);
+            }
+            lds_sync();
+            const float r0 = L.rbuf[0];
+            int j1 = -1, j2 = -1;
+            float u1, u2;
+            if (!(r0 <= kLarge)) {
+                // the reference seeds (v1, j1) with column 0; beyond LARGE that
+                // seed changes the outcome: run its scan verbatim
+                float w1 = r0, w2 = kLarge;
+                int i1 = 0, i2 = -1;
+                if (lane == 0) {
+                    for (int j = 1; j < K; ++j) {
+                        const float r = L.rbuf[j];
+                        if (!(r < w2))
+                            continue;
+                        if (r >= w1) {
+                            w2 = r;
+                            i2 = j;
+                        } else {
+                            w2 = w1;
+                            i2 = i1;
+                            w1 = r;
+                            i1 = j;
+                        }
+                    }
+                }
+                j1 = readlane_i(i1, 0);
+                j2 = readlane_i(i2, 0);
+                u1 = readlane_f(w1, 0);
+                u2 = readlane_f(w2, 0);
+            } else {
+                // first column (in index order) at k1; second: the next one at
+                // k1 if k2 == k1, else the first at k2
+                int found = 0;
+                for (int e = 0; e < E && found < 2; ++e) {
+                    const int j = e * 64 + lane;
+                    const int k = j < K ? fkey(L.rbuf[j]) : kKeyNone;
+                    uint64_t m1 = ballot(k == k1);
+                    if (found == 0 && m1) {
+                        j1 = e * 64 + first_lane(m1);
+                        m1 &= m1 - 1;
+                        found = 1;
+                    }
+                    if (k2 == k1) {
+                        if (found == 1 && m1) {
+                            j2 = e * 64 + first_lane(m1);
+                            found = 2;
+                        }
+                    }
+                }
+                if (k2 != k1 && k2 != kKeyNone) {
+                    for (int e = 0; e < E; ++e) {
+                        const int j = e * 64 + lane;
+                        const int k = j < K ? fkey(L.rbuf[j]) : kKeyNone;
+                        const uint64_t m2 = ballot(k == k2);
+                        if (m2) {
+                            j2 = e * 64 + first_lane(m2);
+                            break;
+                        }
+                    }
+                }
+                u1 = L.rbuf[j1];
+                u2 = kLarge;
+                if (j2 >= 0) {
+                    const float w = L.rbuf[j2];
+                    if (w < kLarge)
+                        u2 = w;
+                    else
+                        j2 = -1;
+                }
+            }
+            int jsel = j1;
+            int i0 = L.y[j1];
+            const float vj1 = L.v[j1];
+            const float lowered = vj1 - (u2 - u1);
+            const bool lowers = lowered < vj1;
+            lds_sync();
+            if (rr < cur * (uint32_t)K) {
+                if (lowers) {
+                    if (lane == 0)
+                        L.v[j1] = lowered;
+                } else if (i0 >= 0 && j2 >= 0) {
+                    jsel = j2;
+                    i0 = L.y[j2];
+                }
+                if (i0 >= 0) {
+                    if (lowers) {
+                        --cur;
+                        if (lane == 0)
+                            L.fr[cur] = i0;
+                    } else {
+                        if (lane == 0)
+                            L.fr[still] = i0;
+                        ++still;
+                    }
+                }
+            } else if (i0 >= 0) {
+                if (lane == 0)
+                    L.fr[still] = i0;
+                ++still;
+            }
+            if (lane == 0) {
+                L.x[fi] = jsel;
+                L.y[jsel] = fi;
+            }
+            lds_sync();
+        }
+        n_free = still;
+    }
+
+    // ---- augmentation (ca_dense / find_path_dense, jonker_dense_flat.h:75-122,237-258) ----
+    for (int f = 0; f < n_free; ++f) {
+        const int start = L.fr[f];
+        for (int e = 0; e < E; ++e) {
+            const int j = e * 64 + lane;
+            if (j < K) {
+                L.cols[j] = j;
+                L.d[j] = C.at(start, j) - L.v[j];
+                L.pred[j] = start;
+            }
+        }
+        lds_sync();
+        int lo = 0, hi = 0, n_ready = 0, final_j = -1;
+        while (final_j < 0) {
+            if (lo >= K)
+                return false;
+            if (lo == hi) {
+                // find_dense over positions [lo, K): classify each position
+                // against the running minimum of the positions before it
+                n_ready = lo;
+                int carry = kKeyNone;
+                int n_ev = 0;
+                for (int base = lo; base < K; base += 64) {
+                    const int p = base + lane;
+                    const int dk = p < K ? fkey(L.d[L.cols[p]]) : kKeyNone;
+                    const int incl = wave_prefix_min_key(dk);
+                    const int before = min(carry, wave_shift_up_key(incl));
+                    const bool later = p > lo && p < K;
+                    const uint64_t rec = ballot(later && dk < before);
+                    const uint64_t tie = ballot(later && dk == before);
+                    n_ev = append_events(L, n_ev, rec | tie, base, 0x80000000u, rec);
+                    carry = min(carry, readlane_i(incl, 63));
+                }
+                lds_sync();
+                int h = 0;
+                if (lane == 0)
+                    h = replay_find_events(L, n_ev, lo);
+                hi = readlane_i(h, 0);
+                lds_sync();
+                // the LAST unassigned column of the tied block wins
+                int last = -1;
+                for (int base = lo; base < hi; base += 64) {
+                    const int p = base + lane;
+                    const uint64_t open = ballot(p < hi && L.y[L.cols[p]] < 0);
+                    if (open)
+                        last = base + last_lane(open);
+                }
+                if (last >= 0)
+                    final_j = L.cols[last];
+            }
+            if (final_j >= 0)
+                break;
+            // scan_dense
+            int slo = lo, shi = hi;
+            bool early = false;
+            while (slo != shi) {
+                const int q = slo++;
+                const int jq = L.cols[q];
+                const int iq = L.y[jq];
+                const float level = L.d[jq];
+                const float hq = C.at(iq, jq) - L.v[jq] - level;
+                int n_ev = 0;
+                const int base0 = shi;
+                for (int base = base0; base < K; base += 64) {
+                    const int p = base + lane;
+                    int jp = 0;
+                    float r = 0.f, dp = 0.f;
+                    bool better = false;
+                    if (p < K) {
+                        jp = L.cols[p];
+                        r = C.at(iq, jp) - L.v[jp] - hq;
+                        dp = L.d[jp];
+                        better = r < dp;
+                    }
+                    const bool tie = better && r == level;
+                    const uint64_t ret = ballot(tie && L.y[jp] < 0);
+                    if (ret) {
+                        const int kk = first_lane(ret);
+                        if (better && lane <= kk) {
+                            L.d[jp] = r;
+                            L.pred[jp] = iq;
+                        }
+                        final_j = readlane_i(jp, kk);
+                        early = true;
+                        break;
+                    }
+                    if (better) {
+                        L.d[jp] = r;
+                        L.pred[jp] = iq;
+                    }
+                    n_ev = append_events(L, n_ev, ballot(tie), base, 0u, 0ull);
+                }
+                lds_sync();
+                if (early)
+                    break;
+                int h = 0;
+                if (lane == 0) {
+                    h = shi;
+                    for (int k = 0; k < n_ev; ++k) {
+                        const int pos = L.ev[k];
+                        const int t = L.cols[pos];
+                        L.cols[pos] = L.cols[h];
+                        L.cols[h] = t;
+                        ++h;
+                    }
+                }
+                shi = readlane_i(h, 0);
+                lds_sync();
+            }
+            if (!early) {
+                lo = slo;
+                hi = shi;
+            }
+        }
+        const float level = L.d[L.cols[lo]];
+        for (int base = 0; base < n_ready; base += 64) {
+            const int p = base + lane;
+            if (p < n_ready) {
+                const int j = L.cols[p];
+                L.v[j] += L.d[j] - level;
+            }
+        }
+        lds_sync();
+        if (lane == 0) {
+            int j = final_j, i;
+            int steps = 0;
+            do {
+                i = L.pred[j];
+                L.y[j] = i;
+                const int prev = L.x[i];
+                L.x[i] = j;
+                j = prev;
+                if (++steps >= K)
+                    break;
+            } while (i != start);
+        }
+        lds_sync();
+    }
+    return true;
+}
+
+__global__ void __launch_bounds__(64)
+jv_solve_large_kernel(const float *__restrict__ costs, int64_t B, int N, int M,
+                      const JvStats *__restrict__ partial, int n_partial,
+                      int64_t *__restrict__ out, uint32_t *__restrict__ status) {
+    __shared__ LargeLds L;
+    const int lane = lane_id();
+    const int K = N > M ? N : M;
+    const int E = (K + 63) / 64;
+    const int64_t b = blockIdx.x;
+    float mx, mn;
+    uint32_t flags;
+    fold_stats(partial, n_partial, mx, mn, flags);
+    if (b == 0 && lane == 0)
+        status[0] = flags;
+    int64_t *ob = out + b * N;
+    if (flags & (kJvFlagNan | kJvFlagNegInf)) {
+        for (int i = lane; i < N; i += 64)
+            ob[i] = -1;
+        return;
+    }
+    const bool any_finite = (flags & kJvFlagAnyFinite) != 0;
+    CostView C;
+    C.src = costs + b * (int64_t)N * M;
+    C.N = N;
+    C.M = M;
+    C.sentinel = any_finite ? (mx + 1.0f) * (float)(K + 1) : 1.0f;
+    if (!large_solve(K, E, L, C)) {
+        if (lane == 0)
+            atomicOr(&status[1], 1u);
+        for (int i = lane; i < N; i += 64)
+            ob[i] = -1;
+        return;
+    }
+    for (int i = lane; i < N; i += 64) {
+        const int j = L.x[i];
+        ob[i] = (j >= 0 && j < M) ? (int64_t)j : (int64_t)-1;
+    }
+}
+
+} // namespace
+
+int launch_jv_large(const float *costs, int64_t B, int N, int M, const JvStats *partial,
+                    int n_partial, int64_t *out, uint32_t *status, hipStream_t stream) {
+    hipLaunchKernelGGL(jv_solve_large_kernel, dim3((unsigned)B), dim3(64), 0, stream, costs, B,
+                       N, M, partial, n_partial, out, status);
+    return hipGetLastError() == hipSuccess ? kTmOk : kTmErrLaunch;
+}
+
+int jv_large_max_k() { return kMaxLargeK; }
+
+} // namespace tmamd
