@@ -2,7 +2,7 @@
 """Benchmark of the hot path on one MI355X: batched JV (C2) + log_sinkhorn (C4).
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-sinkhorn]
-                    [--no-cpu-baseline] [--with-c5]
+                    [--no-extra] [--no-cpu-baseline] [--copy-calibration]
 
 Prints ONE JSON line.  ``value`` is the BASELINE metric's lead figure:
 batched JV solves/s on C2 = float32 (1024, 64, 64) i.i.d. U[0,1), one step =
@@ -14,6 +14,10 @@ iterations/s and HBM GB/s from the slope between 200- and 20-iteration runs
 reference's own JV solver (oracle/_ref, compiled from its source) or, where
 absent, the C restatement, on this host's cores, rank 0 only, on a bounded
 sample; Sinkhorn's CPU baseline is the op-for-op torch restatement.
+Extra legs (skipped by --no-extra): C3 = JV on (64, 512, 768) with 20% +inf
+(solves/s) and C5 = unbalanced Sinkhorn on (1, 16384, 16384) (iterations/s,
+HBM GB/s).  --copy-calibration runs only a 256 MiB device copy, the known
+traffic that profiler byte counters are scaled against.
 """
 
 from __future__ import annotations
@@ -31,6 +35,16 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0  # MI355X published HBM3E bandwidth
+
+# HBM bytes per launch from rocprofv3 --pmc FETCH_SIZE (x2.00, the factor a
+# 256 MiB device copy calibrates) and WRITE_SIZE (x1.00), per dispatch; the
+# runs and commands are recorded in profiles/kernels_bench_default.md.
+MEASURED_TRAFFIC = {
+    # jv_stats_kernel + jv_solve_kernel on C2
+    "jv_c2": int(((8213.5 + 8301.5) * 2 + 8.0 + 512.0) * 1024),
+    # sk_row_sweep + sk_col_sweep + sk_col_merge per C4 iteration
+    "sinkhorn_c4": int(((132805.1 + 131633.1 + 420.0) * 2 + 474.0 + 512.0 + 128.0) * 1024),
+}
 
 
 def _events_time_ms(fn, steps: int, stream) -> float:
@@ -95,7 +109,7 @@ def bench_jv(steps: int, warmup: int, device) -> dict:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 6),
-            "traffic": None,
+            "traffic": MEASURED_TRAFFIC["jv_c2"],
             "note": "stats pre-pass + LDS-resident solve per launch; the solve is a "
                     "latency-bound sequential chain per problem, HBM is not binding",
         },
@@ -140,9 +154,56 @@ def bench_sinkhorn(device, n_long: int = 200, n_short: int = 20, reps: int = 3) 
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(gbs / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": MEASURED_TRAFFIC["sinkhorn_c4"],
         },
     }
+
+
+def bench_jv_c3(device, reps: int = 3) -> dict:
+    """C3: (64, 512, 768) squared distances + jitter, 20% +inf (K = 768 kernel)."""
+    from torchmatch_amd import workloads
+
+    cost = workloads.jv_rect_masked().to(device)
+    op = torch.ops.assignment.jonker_dense_batch
+    op(cost)
+    torch.cuda.synchronize()
+    ms = _events_time_ms(lambda: op(cost), reps, torch.cuda.current_stream(device)) / reps
+    return {"config": {"workload": "jonker_dense_batch C3", "B": 64, "N": 512, "M": 768},
+            "solves_per_s": 64 / (ms * 1e-3), "ms_per_batch": ms}
+
+
+def bench_unbalanced_c5(device, n_long: int = 100, n_short: int = 20) -> dict:
+    """C5: unbalanced Sinkhorn on (1, 16384, 16384), reg 0.02, rho 1 (slope)."""
+    from torchmatch_amd import workloads
+
+    N = 16384
+    cost = workloads.sinkhorn_points(1, N, N, 8, seed=0).to(device)
+    a = workloads.dirichlet(1, N, 1.0, seed=1).to(device)
+    b = workloads.dirichlet(1, N, 1.3, seed=2).to(device)
+    op = torch.ops.transport.unbalanced_sinkhorn
+    stream = torch.cuda.current_stream(device)
+    op(cost, 0.02, n_short, 1.0, a, b)
+    torch.cuda.synchronize()
+    t_long = _events_time_ms(lambda: op(cost, 0.02, n_long, 1.0, a, b), 1, stream)
+    t_short = _events_time_ms(lambda: op(cost, 0.02, n_short, 1.0, a, b), 1, stream)
+    per_iter_ms = (t_long - t_short) / (n_long - n_short)
+    gbs = 2 * N * N * 4 / (per_iter_ms * 1e-3) / 1e9
+    return {"config": {"workload": "unbalanced_sinkhorn C5", "B": 1, "N": N, "M": N,
+                       "reg": 0.02, "rho": 1.0},
+            "iters_per_s": 1e3 / per_iter_ms, "ms_per_iter": per_iter_ms,
+            "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
+                         "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None}}
+
+
+def copy_calibration(device, mib: int = 256, reps: int = 5) -> dict:
+    """A plain device copy of known size, for scaling rocprofv3 FETCH/WRITE_SIZE."""
+    n = mib * (1 << 20) // 4
+    x = torch.rand(n, device=device)
+    y = torch.empty_like(x)
+    for _ in range(reps):
+        y.copy_(x)
+    torch.cuda.synchronize()
+    return {"copy_bytes_each_way": n * 4, "reps": reps}
 
 
 def cpu_baseline_jv(budget_s: float = 10.0) -> dict:
@@ -202,6 +263,10 @@ def main() -> int:
     p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--no-sinkhorn", action="store_true")
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--no-extra", action="store_true",
+                   help="skip the C3 (K=768 JV) and C5 (unbalanced 16384^2) legs")
+    p.add_argument("--copy-calibration", action="store_true",
+                   help="only run a 256 MiB device copy (profiler counter calibration)")
     args = p.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU only (each box has one MI355X); "
@@ -213,6 +278,9 @@ def main() -> int:
     import torchmatch_amd  # noqa: F401
 
     device = torch.device("cuda:0")
+    if args.copy_calibration:
+        print(json.dumps(copy_calibration(device)), flush=True)
+        return 0
     jv_res = bench_jv(args.steps, args.warmup, device)
     line = {
         "metric": "batched JV solves/s (B=1024,N=64) + log_sinkhorn iters/s & HBM GB/s, 1 GPU",
@@ -238,6 +306,11 @@ def main() -> int:
         sk = bench_sinkhorn(device)
         line["sinkhorn"] = {k: (round(v, 4) if isinstance(v, float) else v)
                             for k, v in sk.items()}
+    if not args.no_extra:
+        line["jv_c3"] = {k: (round(v, 3) if isinstance(v, float) else v)
+                         for k, v in bench_jv_c3(device).items()}
+        line["unbalanced_c5"] = {k: (round(v, 4) if isinstance(v, float) else v)
+                                 for k, v in bench_unbalanced_c5(device).items()}
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline_jv()
         if not args.no_sinkhorn:
