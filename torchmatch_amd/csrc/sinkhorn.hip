@@ -44,7 +44,7 @@ namespace {
 
 constexpr int kMapBlock = 256;
 constexpr int kRowWaves = 4;          // waves per row-sweep block
-constexpr int kRowsPerWave = 4;       // rows per wave (reuse of the log_v slice)
+constexpr int kRowsPerWave = 1;       // rows per wave (occupancy beats log_v reuse)
 constexpr int kRowNV = 8;             // float4 per lane per row chunk (2048 cols)
 constexpr int kColStripCols = 64;     // columns per column-sweep block
 constexpr int kColThreads = 256;      // 16 column threads x 16 row groups
@@ -218,7 +218,18 @@ sk_inf_cols(const float *__restrict__ C, uint8_t *__restrict__ inf_col, int64_t 
 // ---- row sweep: log_u -------------------------------------------------------------
 
 // Each wave owns kRowsPerWave consecutive rows of one batch.  M % 4 == 0.
-// Chunks of 256*kRowNV columns: log_v slice and the row slice in registers.
+// Single-chunk rows (M <= 256*kRowNV): all the wave's row loads are issued
+// before any reduction, and each row is an exact two-pass LSE over registers.
+// Longer rows: chunks of 256*kRowNV columns merged online.
+__device__ __forceinline__ void row_lse_update(Lse acc, int64_t r, const float *__restrict__ log_mu,
+                                               float *__restrict__ log_u, float damp,
+                                               int unbalanced) {
+    if (lane_id() == 0) {
+        const float lse = lse_value(acc);
+        log_u[r] = update_potential(lse, log_mu[r], log_u[r], damp, unbalanced != 0);
+    }
+}
+
 __global__ void __launch_bounds__(kRowWaves * 64)
 sk_row_sweep(const float *__restrict__ K, const float *__restrict__ log_v,
              const float *__restrict__ log_mu, const uint8_t *__restrict__ inf_row,
@@ -233,14 +244,55 @@ sk_row_sweep(const float *__restrict__ K, const float *__restrict__ log_v,
     const int64_t m4 = M / 4;
     const float4 *lv4 = reinterpret_cast<const float4 *>(log_v + b * M);
     constexpr int CH = 64 * kRowNV;  // float4 per chunk
-    const bool single_chunk = m4 <= CH;
-    float4 lv[kRowNV];
-    if (single_chunk) {
+    if (m4 <= CH) {
+        float4 kk[kRowsPerWave][kRowNV];
+#pragma unroll
+        for (int rr = 0; rr < kRowsPerWave; ++rr) {
+            const int64_t i = i_begin + rr;
+            const float4 *row4 = reinterpret_cast<const float4 *>(K + (b * N + i) * M);
+#pragma unroll
+            for (int k = 0; k < kRowNV; ++k) {
+                const int64_t q = (int64_t)k * 64 + lane;
+                kk[rr][k] = (i < N && q < m4) ? row4[q]
+                                              : make_float4(-f_inf(), -f_inf(), -f_inf(), -f_inf());
+            }
+        }
+        float4 lv[kRowNV];
 #pragma unroll
         for (int k = 0; k < kRowNV; ++k) {
             const int64_t q = (int64_t)k * 64 + lane;
             lv[k] = q < m4 ? lv4[q] : make_float4(0.f, 0.f, 0.f, 0.f);
         }
+#pragma unroll
+        for (int rr = 0; rr < kRowsPerWave; ++rr) {
+            const int64_t i = i_begin + rr;
+            if (i >= N)
+                break;
+            const int64_t r = b * N + i;
+            if (inf_row[r])
+                continue;  // lse = -inf: log_u keeps its value
+            float t[4 * kRowNV];
+#pragma unroll
+            for (int k = 0; k < kRowNV; ++k) {
+                t[4 * k + 0] = kk[rr][k].x + lv[k].x;
+                t[4 * k + 1] = kk[rr][k].y + lv[k].y;
+                t[4 * k + 2] = kk[rr][k].z + lv[k].z;
+                t[4 * k + 3] = kk[rr][k].w + lv[k].w;
+            }
+            float m = t[0];
+#pragma unroll
+            for (int k = 1; k < 4 * kRowNV; ++k)
+                m = fmaxf(m, t[k]);
+            m = wave_max_all(m);
+            const float sh = lse_shift(m);
+            float s = 0.f;
+#pragma unroll
+            for (int k = 0; k < 4 * kRowNV; ++k)
+                s += exp_nonpos(t[k] - sh);
+            s = wave_sum_all(s);
+            row_lse_update(Lse{m, s}, r, log_mu, log_u, damp, unbalanced);
+        }
+        return;
     }
     for (int rr = 0; rr < kRowsPerWave; ++rr) {
         const int64_t i = i_begin + rr;
@@ -248,7 +300,7 @@ sk_row_sweep(const float *__restrict__ K, const float *__restrict__ log_v,
             break;
         const int64_t r = b * N + i;
         if (inf_row[r])
-            continue;  // lse = -inf: log_u keeps its value
+            continue;
         const float4 *row4 = reinterpret_cast<const float4 *>(K + r * M);
         Lse acc{-f_inf(), 0.f};
         for (int64_t base = 0; base < m4; base += CH) {
@@ -257,12 +309,12 @@ sk_row_sweep(const float *__restrict__ K, const float *__restrict__ log_v,
             for (int k = 0; k < kRowNV; ++k) {
                 const int64_t q = base + (int64_t)k * 64 + lane;
                 if (q < m4) {
-                    const float4 kk = row4[q];
-                    const float4 vv = single_chunk ? lv[k] : lv4[q];
-                    t[4 * k + 0] = kk.x + vv.x;
-                    t[4 * k + 1] = kk.y + vv.y;
-                    t[4 * k + 2] = kk.z + vv.z;
-                    t[4 * k + 3] = kk.w + vv.w;
+                    const float4 kq = row4[q];
+                    const float4 vq = lv4[q];
+                    t[4 * k + 0] = kq.x + vq.x;
+                    t[4 * k + 1] = kq.y + vq.y;
+                    t[4 * k + 2] = kq.z + vq.z;
+                    t[4 * k + 3] = kq.w + vq.w;
                 } else {
                     t[4 * k + 0] = t[4 * k + 1] = t[4 * k + 2] = t[4 * k + 3] = -f_inf();
                 }
@@ -271,23 +323,20 @@ sk_row_sweep(const float *__restrict__ K, const float *__restrict__ log_v,
 #pragma unroll
             for (int k = 1; k < 4 * kRowNV; ++k)
                 m = fmaxf(m, t[k]);
-            m = wave_max(m);  // the chunk maximum, in every lane
+            m = wave_max_all(m);
             const float newm = fmaxf(acc.m, m);
             const float sh = lse_shift(newm);
             float s = 0.f;
 #pragma unroll
             for (int k = 0; k < 4 * kRowNV; ++k)
                 s += exp_nonpos(t[k] - sh);
-            s = wave_sum(s);
+            s = wave_sum_all(s);
             if (acc.s != 0.f)
                 s += acc.s * exp_nonpos(lse_shift(acc.m) - sh);
             acc.m = newm;
             acc.s = s;
         }
-        if (lane == 0) {
-            const float lse = lse_value(acc);
-            log_u[r] = update_potential(lse, log_mu[r], log_u[r], damp, unbalanced != 0);
-        }
+        row_lse_update(acc, r, log_mu, log_u, damp, unbalanced);
     }
 }
 

@@ -229,3 +229,51 @@ __device__ __forceinline__ float key_to_float(int k) {
     return __int_as_float(k ^ ((k >> 31) & 0x7fffffff));
 }
 } // namespace tmamd
+
+namespace tmamd {
+// Float butterfly reductions over the whole wave, result in every lane:
+// 4 DPP stages inside each 16-lane row, then the gfx950 row swaps.  No LDS
+// (unlike __shfl_xor, which goes through ds_bpermute).
+template <int CTRL>
+__device__ __forceinline__ float dpp_full_f(float x) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), CTRL, 0xF, 0xF, true));
+}
+
+__device__ __forceinline__ float row_swap16_pair(float x, float &other) {
+    const u32x2 s = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x),
+                                                     false, false);
+    other = __uint_as_float(s[1]);
+    return __uint_as_float(s[0]);
+}
+
+__device__ __forceinline__ float row_swap32_pair(float x, float &other) {
+    const u32x2 s = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x),
+                                                     false, false);
+    other = __uint_as_float(s[1]);
+    return __uint_as_float(s[0]);
+}
+
+__device__ __forceinline__ float wave_sum_all(float x) {
+    x += dpp_full_f<kDppQuadXor1>(x);
+    x += dpp_full_f<kDppQuadXor2>(x);
+    x += dpp_full_f<kDppRowHalfMirror>(x);
+    x += dpp_full_f<kDppRowMirror>(x);
+    float o;
+    float a = row_swap16_pair(x, o);
+    x = a + o;
+    a = row_swap32_pair(x, o);
+    return a + o;
+}
+
+__device__ __forceinline__ float wave_max_all(float x) {
+    x = fmaxf(x, dpp_full_f<kDppQuadXor1>(x));
+    x = fmaxf(x, dpp_full_f<kDppQuadXor2>(x));
+    x = fmaxf(x, dpp_full_f<kDppRowHalfMirror>(x));
+    x = fmaxf(x, dpp_full_f<kDppRowMirror>(x));
+    float o;
+    float a = row_swap16_pair(x, o);
+    x = fmaxf(a, o);
+    a = row_swap32_pair(x, o);
+    return fmaxf(a, o);
+}
+} // namespace tmamd
