@@ -370,9 +370,100 @@ __device__ __forceinline__ TwoMin row_two_min(float r, bool live) {
     return t;
 }
 
+// Row cache of the augmenting row reduction (K >= 4).  Lane i keeps, for row
+// i, the three columns that were its smallest reduced costs when the row was
+// last scanned (ascending column order), their costs, the current duals and
+// owners of those columns, and tau = the fourth smallest reduced cost of that
+// scan.  Duals only fall in that phase, so every other reduced cost of the row
+// is still >= tau.  When the second smallest cached value is < tau, the two
+// cached minima are the row's two minima (first index on ties: the cached
+// columns are compared in column order), and a step needs no row scan.  Every
+// lane also keeps its row's would-be lowered dual, so a cached step reads all
+// it needs from one lane.  A row never scanned has all values 0 and tau 0
+// (reduced costs are >= 0 in that phase), so it is never taken as cached.
+//
+// The helpers take the cached entries by value: selecting among struct
+// fields or captured references lets the compiler turn the selects into
+// indexed private-memory loads.
+struct CacheRank {
+    int t1q, t1o;          // smallest: column, its owner
+    float t1r, t2r, low;   // two smallest values, lowered dual of t1q
+    uint64_t hitm, stepm;  // rows: cached / cached chain step
+};
+
+// Each row's two smallest cached values; the smallest's column is the first
+// cached column holding it.  stepm: the row's step would lower the dual of an
+// owned column (the reference's `free_rows[--current]` branch).
+__device__ __forceinline__ CacheRank cache_rank(int q0, int q1, int q2, int o0, int o1, int o2,
+                                                float g0, float g1, float g2, float w0,
+                                                float w1, float w2, float tau) {
+    CacheRank c;
+    const float r0 = g0 - w0, r1 = g1 - w1, r2 = g2 - w2;
+    c.t1r = fminf(fminf(r0, r1), r2);
+    c.t2r = __builtin_amdgcn_fmed3f(r0, r1, r2);
+    const bool e0 = r0 == c.t1r, e1 = r1 == c.t1r;
+    c.t1q = e0 ? q0 : (e1 ? q1 : q2);
+    const float t1w = e0 ? w0 : (e1 ? w1 : w2);
+    c.t1o = e0 ? o0 : (e1 ? o1 : o2);
+    c.low = t1w - (c.t2r - c.t1r);
+    const bool h = c.t2r < tau;
+    c.hitm = ballot(h);
+    c.stepm = ballot(h && c.low < t1w && c.t1o >= 0);
+    return c;
+}
+
+// Column of each row's second smallest cached value, (value, column) order.
+__device__ __forceinline__ int cache_second(int q0, int q1, int q2, float g0, float g1,
+                                            float g2, float w0, float w1, float w2,
+                                            float t1r) {
+    const float r0 = g0 - w0, r1 = g1 - w1, r2 = g2 - w2;
+    const int not0 = r2 < r1 ? q2 : q1;
+    const int not1 = r2 < r0 ? q2 : q0;
+    const int not2 = r1 < r0 ? q1 : q0;
+    return r0 == t1r ? not0 : (r1 == t1r ? not1 : not2);
+}
+
+// A fresh scan of one row (lane = column, `r` its reduced costs, `crow` its
+// costs): the three smallest (value, column) in column order with their costs,
+// duals and owners, and the fourth smallest value (K >= 4 live lanes).
+struct CacheFill {
+    int s0, s1, s2, oa, ob, oc;
+    float ga, gb, gc, wa, wb, wc, tau;
+};
+
+__device__ __forceinline__ CacheFill cache_fill(float crow, float v, int y, bool live) {
+    const int lane = lane_id();
+    const int key = live ? fkey(crow - v) : kKeyNone;
+    int k1, k2;
+    wave_min2_key(key, k1, k2);
+    const uint64_t m1 = ballot(key == k1);
+    const uint64_t m2 = ballot(key == k2);
+    const int j1 = first_lane(m1);
+    const int j2 = uniform_i(k1) == uniform_i(k2) ? first_lane(m1 & (m1 - 1)) : first_lane(m2);
+    const int key3 = (lane == j1 || lane == j2) ? kKeyNone : key;
+    int k3, k4;
+    wave_min2_key(key3, k3, k4);
+    const int j3 = first_lane(ballot(key3 == k3));
+    CacheFill f;
+    f.tau = key_to_float(uniform_i(k4));
+    const int lo12 = min(j1, j2), hi12 = max(j1, j2);
+    f.s0 = min(lo12, j3);
+    f.s2 = max(hi12, j3);
+    f.s1 = max(lo12, min(hi12, j3));
+    f.ga = readlane_f(crow, f.s0);
+    f.gb = readlane_f(crow, f.s1);
+    f.gc = readlane_f(crow, f.s2);
+    f.wa = readlane_f(v, f.s0);
+    f.wb = readlane_f(v, f.s1);
+    f.wc = readlane_f(v, f.s2);
+    f.oa = readlane_i(y, f.s0);
+    f.ob = readlane_i(y, f.s1);
+    f.oc = readlane_i(y, f.s2);
+    return f;
+}
+
 __device__ __forceinline__ bool wave_solve(const int K, WaveLds &L, float v,
                                            int y, bool chain, int &x_out) {
-    uint64_t okm = 0;
     const int lane = lane_id();
     const bool live = lane < K;
 
@@ -443,6 +534,15 @@ __device__ __forceinline__ bool wave_solve(const int K, WaveLds &L, float v,
     // chain is handed back, untouched, to the general step.  x is not kept
     // during this phase; it is rebuilt from y afterwards (only assigned rows'
     // x are ever read again).
+    //
+    // row cache (see CacheRank above), lane = row
+    const bool cache = chain && K >= 4;
+    int q0 = kTile, q1 = kTile, q2 = kTile;  // cached columns
+    int o0 = -1, o1 = -1, o2 = -1;           // their owners
+    float g0 = 0.f, g1 = 0.f, g2 = 0.f;      // their costs in this row
+    float w0 = 0.f, w1 = 0.f, w2 = 0.f;      // their duals
+    float tau = 0.f;
+    CacheRank rc = cache_rank(q0, q1, q2, o0, o1, o2, g0, g1, g2, w0, w1, w2, tau);
     for (int round = 0; n_free > 0 && round < 2; ++round) {
         uint32_t cur = 0, rr = 0;
         int still = 0;
@@ -453,32 +553,97 @@ __device__ __forceinline__ bool wave_solve(const int K, WaveLds &L, float v,
                 if (cur >= (uint32_t)n_free)
                     break;
                 fi = readlane_i(fr, (int)cur);
+                have = true;
+            }
+            if (cache) {
+                // ---- cached displacement chain ----
+                // Steps that take the `free_rows[--current]` branch (cap, dual
+                // lowered, column owned) run here from the cache alone: such a
+                // step leaves `current` where it was, so fi stays pending at
+                // position cur.  A row without a usable cache is rescanned
+                // first.  The first step that is not such a step goes to the
+                // general step below.
+                const uint32_t rr_cap = (cur + 1) * (uint32_t)K;
+                while (true) {
+                    while (((rc.stepm >> fi) & 1ull) && rr + 1 < rr_cap) {
+                        const int c1 = readlane_i(rc.t1q, fi);
+                        const float low = readlane_f(rc.low, fi);
+                        const int ic = readlane_i(rc.t1o, fi);
+                        ++rr;
+                        const bool m0 = q0 == c1, m1 = q1 == c1, m2 = q2 == c1;
+                        w0 = m0 ? low : w0;
+                        w1 = m1 ? low : w1;
+                        w2 = m2 ? low : w2;
+                        o0 = m0 ? fi : o0;
+                        o1 = m1 ? fi : o1;
+                        o2 = m2 ? fi : o2;
+                        if (lane == c1) {
+                            v = low;
+                            y = fi;
+                        }
+                        rc = cache_rank(q0, q1, q2, o0, o1, o2, g0, g1, g2, w0, w1, w2, tau);
+                        fi = ic;
+                    }
+                    if (rr + 1 >= rr_cap || ((rc.hitm >> fi) & 1ull))
+                        break;
+                    const CacheFill f = cache_fill(L.c[fi * kTile + lane], v, y, live);
+                    if (lane == fi) {
+                        q0 = f.s0;
+                        q1 = f.s1;
+                        q2 = f.s2;
+                        o0 = f.oa;
+                        o1 = f.ob;
+                        o2 = f.oc;
+                        g0 = f.ga;
+                        g1 = f.gb;
+                        g2 = f.gc;
+                        w0 = f.wa;
+                        w1 = f.wb;
+                        w2 = f.wc;
+                        tau = f.tau;
+                    }
+                    rc = cache_rank(q0, q1, q2, o0, o1, o2, g0, g1, g2, w0, w1, w2, tau);
+                    if (!((rc.stepm >> fi) & 1ull))
+                        break;
+                }
             }
             have = false;
             ++rr;
             ++cur;
             if (rr > rr_limit)
                 return false;
-            const float r = L.c[fi * kTile + lane] - v;
-            const int key = live ? fkey(r) : kKeyNone;
-            int k1, k2;
-            wave_min2_key(key, k1, k2);
-            const uint64_t m1 = ballot(key == k1);
-            const uint64_t m2 = ballot(key == k2);
-            const bool same = uniform_i(k1) == uniform_i(k2);
-            const int j1 = first_lane(m1);
-            const uint64_t m1b = m1 & (m1 - 1);
-            const int j2c = same ? (m1b ? first_lane(m1b) : -1) : (m2 ? first_lane(m2) : -1);
-            const int j2r = j2c < 0 ? 0 : j2c;
-            const float u1 = readlane_f(r, j1);
-            const float u2c = readlane_f(r, j2r);
+            int j1, j2;
+            float u1, u2;
+            const bool hit = cache && ((rc.hitm >> fi) & 1ull);
+            if (hit) {
+                // u2 < tau < LARGE: the (LARGE, -1) start slot cannot win
+                j1 = readlane_i(rc.t1q, fi);
+                u1 = readlane_f(rc.t1r, fi);
+                j2 = readlane_i(cache_second(q0, q1, q2, g0, g1, g2, w0, w1, w2, rc.t1r), fi);
+                u2 = readlane_f(rc.t2r, fi);
+            } else {
+                const float r = L.c[fi * kTile + lane] - v;
+                const int key = live ? fkey(r) : kKeyNone;
+                int k1, k2;
+                wave_min2_key(key, k1, k2);
+                const uint64_t m1 = ballot(key == k1);
+                const uint64_t m2 = ballot(key == k2);
+                const bool same = uniform_i(k1) == uniform_i(k2);
+                j1 = first_lane(m1);
+                const uint64_t m1b = m1 & (m1 - 1);
+                const int j2c =
+                    same ? (m1b ? first_lane(m1b) : -1) : (m2 ? first_lane(m2) : -1);
+                u1 = readlane_f(r, j1);
+                const float u2c = readlane_f(r, j2c < 0 ? 0 : j2c);
+                // (LARGE, -1) start slot of the second minimum
+                const bool has2 = j2c >= 0 && u2c < kLarge;
+                j2 = has2 ? j2c : -1;
+                u2 = has2 ? u2c : kLarge;
+            }
+            const int j2r = j2 < 0 ? 0 : j2;
             const int i0 = readlane_i(y, j1);
             const int y2 = readlane_i(y, j2r);
             const float vj1 = readlane_f(v, j1);
-            // (LARGE, -1) start slot of the second minimum
-            const bool has2 = j2c >= 0 && u2c < kLarge;
-            const int j2 = has2 ? j2c : -1;
-            const float u2 = has2 ? u2c : kLarge;
             const float lowered = vj1 - (u2 - u1);
             const bool lowers = lowered < vj1;
             const bool cap = rr < cur * (uint32_t)K;
@@ -495,13 +660,24 @@ __device__ __forceinline__ bool wave_solve(const int K, WaveLds &L, float v,
             if (lane == jsel)
                 y = fi;
             still += push_back ? 1 : 0;
+            if (cache) {
+                if (vupd) {
+                    w0 = q0 == j1 ? lowered : w0;
+                    w1 = q1 == j1 ? lowered : w1;
+                    w2 = q2 == j1 ? lowered : w2;
+                }
+                o0 = q0 == jsel ? fi : o0;
+                o1 = q1 == jsel ? fi : o1;
+                o2 = q2 == jsel ? fi : o2;
+                rc = cache_rank(q0, q1, q2, o0, o1, o2, g0, g1, g2, w0, w1, w2, tau);
+            }
             if (!push_front)
                 continue;
             // fr[--cur] = i0 is read straight back: keep i0 in a register
             --cur;
             fi = i0;
             have = true;
-            if (!chain)
+            if (!chain || cache)
                 continue;
 
             // ---- displacement chain ----
