@@ -406,9 +406,8 @@ __device__ __forceinline__ CacheRank cache_rank(int q0, int q1, int q2, int o0, 
     const float t1w = e0 ? w0 : (e1 ? w1 : w2);
     c.t1o = e0 ? o0 : (e1 ? o1 : o2);
     c.low = t1w - (c.t2r - c.t1r);
-    const bool h = c.t2r < tau;
-    c.hitm = ballot(h);
-    c.stepm = ballot(h && c.low < t1w && c.t1o >= 0);
+    c.hitm = ballot(c.t2r < tau);
+    c.stepm = c.hitm & ballot(c.low < t1w) & ballot(c.t1o >= 0);
     return c;
 }
 
@@ -436,20 +435,31 @@ __device__ __forceinline__ CacheFill cache_fill(float crow, float v, int y, bool
     const int key = live ? fkey(crow - v) : kKeyNone;
     int k1, k2;
     wave_min2_key(key, k1, k2);
-    const uint64_t m1 = ballot(key == k1);
-    const uint64_t m2 = ballot(key == k2);
-    const int j1 = first_lane(m1);
-    const int j2 = uniform_i(k1) == uniform_i(k2) ? first_lane(m1 & (m1 - 1)) : first_lane(m2);
-    const int key3 = (lane == j1 || lane == j2) ? kKeyNone : key;
+    // Usually exactly two lanes hold keys <= the second smallest, and they
+    // are the first two in (value, column) order: drop them and take the
+    // next two minima straight away.  Ties at the second value drop exactly
+    // the first two lanes instead.
+    int key3 = key <= k2 ? kKeyNone : key;
     int k3, k4;
     wave_min2_key(key3, k3, k4);
-    const int j3 = first_lane(ballot(key3 == k3));
+    uint64_t sel = ballot(key <= k2);
+    if (__builtin_popcountll(sel) != 2) {
+        const uint64_t m1 = ballot(key == k1);
+        const uint64_t m2 = ballot(key == k2);
+        const int j1 = first_lane(m1);
+        const int j2 =
+            uniform_i(k1) == uniform_i(k2) ? first_lane(m1 & (m1 - 1)) : first_lane(m2);
+        key3 = (lane == j1 || lane == j2) ? kKeyNone : key;
+        wave_min2_key(key3, k3, k4);
+        sel = (1ull << j1) | (1ull << j2);
+    }
+    sel |= 1ull << first_lane(ballot(key3 == k3));
     CacheFill f;
-    f.tau = key_to_float(uniform_i(k4));
-    const int lo12 = min(j1, j2), hi12 = max(j1, j2);
-    f.s0 = min(lo12, j3);
-    f.s2 = max(hi12, j3);
-    f.s1 = max(lo12, min(hi12, j3));
+    f.tau = key_to_float(k4);
+    f.s0 = first_lane(sel);
+    sel &= sel - 1;
+    f.s1 = first_lane(sel);
+    f.s2 = last_lane(sel);
     f.ga = readlane_f(crow, f.s0);
     f.gb = readlane_f(crow, f.s1);
     f.gc = readlane_f(crow, f.s2);
