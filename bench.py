@@ -36,6 +36,13 @@ sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0  # MI355X published HBM3E bandwidth
 
+# Reduced-cost relaxations c[i][j] - v[j] that the reference algorithm performs
+# on the C2 seed-0 batch (all phases, summed over the 1024 problems), counted
+# by the instrumented C restatement; tests/test_oracle_jv.py recomputes it.
+# Each relaxation touches a cost, a dual and a distance: 12 algorithmic bytes.
+JV_C2_RELAXATIONS = 28_681_299
+JV_BYTES_PER_RELAXATION = 12
+
 # HBM bytes per launch from rocprofv3 --pmc FETCH_SIZE (x2.00, the factor a
 # 256 MiB device copy calibrates) and WRITE_SIZE (x1.00), per dispatch; the
 # runs and commands are recorded in profiles/kernels_bench_default.md.
@@ -97,6 +104,21 @@ def bench_jv(steps: int, warmup: int, device) -> dict:
     assert torch.equal(outk, out)
     bytes_per_launch = B * N * M * 4 + B * N * 8
     achieved = bytes_per_launch / (kernel_ms * 1e-3) / 1e9
+    # LDS roofline of the solve: algorithmic LDS bytes (12 per relaxation) over
+    # the launch time, against the measured LDS read peak
+    lds_bytes = JV_C2_RELAXATIONS * JV_BYTES_PER_RELAXATION
+    lds_achieved = lds_bytes / (kernel_ms * 1e-3) / 1e9
+    peak = lds_read_peak(device)
+    lds_roofline = {
+        "bound": "lds",
+        "achieved": round(lds_achieved, 1),
+        "peak": round(peak["gbs"], 1) if peak else None,
+        "unit": "GB/s",
+        "frac": round(lds_achieved / peak["gbs"], 5) if peak else None,
+        "algorithmic_bytes": lds_bytes,
+        "relaxations_per_solve": round(JV_C2_RELAXATIONS / B, 1),
+        "peak_probe": peak["probe"] if peak else "probe library not built",
+    }
     return {
         "solves_per_s": B / (ms_per_step * 1e-3),
         "ms_per_step": ms_per_step,
@@ -113,9 +135,36 @@ def bench_jv(steps: int, warmup: int, device) -> dict:
             "note": "stats pre-pass + LDS-resident solve per launch; the solve is a "
                     "latency-bound sequential chain per problem, HBM is not binding",
         },
+        "lds_roofline": lds_roofline,
         "cost_sha256": workloads.sha256(cost_cpu),
         "out": out,
     }
+
+
+def lds_read_peak(device, iters: int = 4096, reps: int = 5) -> dict | None:
+    """LDS read bandwidth of the whole chip (lib/libtm_lds_probe.so): 8
+    workgroups of 256 lanes per CU stream conflict-free 16-byte LDS reads."""
+    import ctypes
+
+    from torchmatch_amd import _build
+
+    if not _build.PROBE_SO.exists():
+        return None
+    lib = ctypes.CDLL(str(_build.PROBE_SO))
+    lib.tm_probe_lds_read.restype = ctypes.c_int64
+    lib.tm_probe_lds_read.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
+                                      ctypes.c_void_p]
+    cus = torch.cuda.get_device_properties(device).multi_processor_count
+    blocks = 8 * cus
+    sink = torch.zeros(blocks, dtype=torch.int32, device=device)
+    stream = torch.cuda.current_stream(device)
+    run = lambda: lib.tm_probe_lds_read(sink.data_ptr(), blocks, iters, stream.cuda_stream)
+    nbytes = run()
+    if nbytes <= 0:
+        return None
+    best = min(_events_time_ms(run, 1, stream) for _ in range(reps))
+    return {"gbs": nbytes / (best * 1e-3) / 1e9, "cus": cus,
+            "probe": f"{blocks} workgroups x 256 lanes x {iters} ds_read_b128"}
 
 
 def bench_sinkhorn(device, n_long: int = 200, n_short: int = 20, reps: int = 3) -> dict:
@@ -301,6 +350,7 @@ def main() -> int:
         "kernel": {"ms_per_launch": round(jv_res["kernel_ms"], 5),
                    "solves_per_s": round(jv_res["kernel_solves_per_s"], 1)},
         "roofline": jv_res["roofline"],
+        "lds_roofline": jv_res["lds_roofline"],
     }
     if not args.no_sinkhorn:
         sk = bench_sinkhorn(device)

@@ -143,6 +143,18 @@ def test_counted_run_matches_plain_run():
     assert (counts[:, 0] >= 64 * 64).all()
 
 
+def test_bench_relaxation_count():
+    """bench.py prices the JV LDS roofline in relaxations on C2 seed 0; the
+    constant it carries must be what the counted oracle run gives."""
+    import bench
+
+    c = workloads.jv_uniform(1024, 64, 64, seed=0).numpy()
+    out, counts = jv.jv_dense_batch_counted(c)
+    assert int(counts[:, 0].sum()) == bench.JV_C2_RELAXATIONS
+    # every problem scans its full K x K tile at least once (column reduction)
+    assert (counts[:, 0] >= 64 * 64).all()
+
+
 def test_torch_input_roundtrip():
     c = torch.rand(4, 6, 6, generator=torch.Generator().manual_seed(0))
     assert jv.jv_dense_batch(c.numpy()).shape == (4, 6)

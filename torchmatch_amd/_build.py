@@ -5,7 +5,10 @@ Produces, next to this file:
 * ``lib/libtorchmatch_amd.so`` -- the C-ABI library (``include/torchmatch_amd.h``):
   the HIP kernels in ``csrc/*.hip``, compiled by ``hipcc --offload-arch=gfx950``;
 * ``_C.so`` -- torch dispatcher registrations (``csrc/torch_ops.cpp``) linked
-  against the C-ABI library; loaded with ``torch.ops.load_library``.
+  against the C-ABI library; loaded with ``torch.ops.load_library``;
+* ``lib/libtm_lds_probe.so`` -- the LDS read-bandwidth microbenchmark
+  (``csrc/lds_probe.hip``) that ``bench.py`` prices the JV kernels against;
+  measurement support, not part of the C ABI.
 
 ``python -m torchmatch_amd._build`` runs it; ``__graft_entry__.build()`` calls
 :func:`build` too.  hipcc cross-compiles, so no GPU is needed.
@@ -26,6 +29,7 @@ INCLUDE = PKG.parent / "include"
 LIB_DIR = PKG / "lib"
 CABI_SO = LIB_DIR / "libtorchmatch_amd.so"
 OPS_SO = PKG / "_C.so"
+PROBE_SO = LIB_DIR / "libtm_lds_probe.so"
 
 HIP_SOURCES = ["jv_batch.hip", "jv_large.hip", "sinkhorn.hip"]
 ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
@@ -74,6 +78,16 @@ def build_cabi(verbose: bool = True) -> Path:
     return CABI_SO
 
 
+def build_probe(verbose: bool = True) -> Path:
+    """Compile the LDS bandwidth probe into lib/libtm_lds_probe.so."""
+    LIB_DIR.mkdir(exist_ok=True)
+    tmp = PROBE_SO.with_suffix(".so.tmp")
+    _run(["hipcc", *HIPCC_FLAGS, "-shared", "-o", str(tmp), str(CSRC / "lds_probe.hip"),
+          f"-Wl,-rpath,{ROCM / 'lib'}"], verbose)
+    os.replace(tmp, PROBE_SO)
+    return PROBE_SO
+
+
 def build_ops(verbose: bool = True) -> Path:
     """Compile the torch op registrations into _C.so."""
     import torch
@@ -105,6 +119,7 @@ def build_ops(verbose: bool = True) -> Path:
 def build(verbose: bool = True) -> None:
     build_cabi(verbose)
     build_ops(verbose)
+    build_probe(verbose)
 
 
 if __name__ == "__main__":
