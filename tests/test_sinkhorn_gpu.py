@@ -54,6 +54,10 @@ CASES = [
     (3, 300, 200, 0.1, 100),
     (1, 130, 517, 0.05, 80),
     (2, 1024, 1024, 0.05, 60),
+    # rows longer than one 2048-column chunk: several waves per row
+    (1, 48, 4100, 0.05, 40),
+    (1, 32, 16384, 0.05, 30),
+    (1, 16, 40000, 0.1, 20),
 ]
 
 
@@ -76,6 +80,7 @@ def test_log_sinkhorn_matches_oracle(B, N, M, eps, n_iter, device):
     (2, 64, 80, 0.1, 60, 1.0),
     (1, 500, 300, 0.02, 100, 1.0),
     (2, 256, 256, 0.05, 100, 0.5),
+    (1, 64, 8192, 0.02, 50, 1.0),
 ])
 def test_unbalanced_matches_oracle(B, N, M, eps, n_iter, rho, device):
     cost = workloads.sinkhorn_points(B, N, M, 8, seed=3)
@@ -105,6 +110,21 @@ def test_forbidden_cells_rows_and_columns(device):
     assert not torch.isnan(plan).any()
     assert _plan_rel(plan, ref_plan) <= REL_TOL
     assert _rel(f, ref_f) <= REL_TOL and _rel(g, ref_g) <= REL_TOL
+
+
+def test_forbidden_rows_long_rows(device):
+    """All-+inf rows and columns with rows split over several waves."""
+    cost = workloads.sinkhorn_points(1, 24, 6000, 4, seed=11)
+    cost[0, 5, :] = float("inf")
+    cost[0, :, 4321] = float("inf")
+    cost[0, 7, 2000:4500] = float("inf")
+    a = workloads.dirichlet(1, 24, 1.0, seed=12)
+    b = workloads.dirichlet(1, 6000, 1.0, seed=13)
+    ref_plan, _, _, _, _ = sk.log_sinkhorn_plan(cost, eps=0.1, n_iter=30, a=a, b=b)
+    plan = torch.ops.transport.log_sinkhorn(cost.to(device), 0.1, 30, a.to(device), b.to(device))
+    pr = _plan_rel(plan, ref_plan)
+    print(f"forbidden long rows plan rel {pr:.3e}", flush=True)
+    assert pr <= REL_TOL
 
 
 def test_mask_argument_and_op_entry(device):

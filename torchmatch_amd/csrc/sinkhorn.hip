@@ -24,13 +24,14 @@
 // One step = row sweep (reads K once) + column sweep (reads K once): the
 // algorithmic minimum of 2 * B*N*M*4 bytes.
 //
-// Row sweep: each wave owns whole rows; its lanes hold a 256*NV-column slice
-// of log_v in registers for all its rows, and each row is an exact two-pass
-// LSE over registers (max, then sum of exp) when M <= 256*NV, an online
-// per-chunk merge beyond.  Column sweep: a block owns a 64-column strip over a
-// chunk of rows; 16 threads span the strip with float4 loads, 16 row groups
-// fold rows online (one rescale per group of U rows), and an LDS merge of the
-// 16 row groups yields the column LSE (or a partial when rows are chunked).
+// Row sweep: rows of up to 256*NV columns belong to one wave each, and each
+// is an exact two-pass LSE over registers (max, then sum of exp); longer rows
+// are split over the waves of a block, one 256*NV-column chunk per wave, whose
+// (max, sum) pairs merge in LDS.  Column sweep: a block owns a column strip over a
+// chunk of rows; 16 threads span the 64-column strip with float4 loads, 16
+// row groups fold rows online (one rescale per group of U rows), and an LDS
+// merge of the row groups yields the column LSE (or a partial when rows are
+// chunked).
 // exp / log run on the native v_exp_f32 / v_log_f32 (base 2).
 #include <hip/hip_runtime.h>
 #include <math.h>
@@ -46,9 +47,9 @@ constexpr int kMapBlock = 256;
 constexpr int kRowWaves = 4;          // waves per row-sweep block
 constexpr int kRowsPerWave = 1;       // rows per wave (occupancy beats log_v reuse)
 constexpr int kRowNV = 8;             // float4 per lane per row chunk (2048 cols)
-constexpr int kColStripCols = 64;     // columns per column-sweep block
-constexpr int kColThreads = 256;      // 16 column threads x 16 row groups
-constexpr int kColGroups = kColThreads / (kColStripCols / 4);  // 16
+constexpr int kColThreads = 256;      // column-sweep block: strip threads x row groups
+constexpr int kColStrip = 64;         // strip width (columns): 16 threads x 16 row groups
+constexpr int64_t kColBlocksTarget = 5 * 256;  // column-sweep blocks to aim for
 constexpr int kColU = 8;              // rows per group fold
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
@@ -121,12 +122,16 @@ SinkhornLayout make_layout(int64_t B, int64_t N, int64_t M) {
     L.B = B;
     L.N = N;
     L.M = M;
-    L.n_strip = (int)((M + kColStripCols - 1) / kColStripCols);
-    // split rows only when the strips alone give too few blocks to fill 256 CUs
-    int64_t blocks = B * L.n_strip;
-    int64_t chunks = 1;
-    while (blocks * chunks < 1024 && N / (chunks * 2) >= 256)
-        chunks *= 2;
+    L.n_strip = (int)((M + kColStrip - 1) / kColStrip);
+    // split rows into chunks until the column sweep has about five blocks per
+    // CU (its 68 VGPRs allow seven; five measured best), keeping >= 256 rows
+    // per chunk
+    const int64_t blocks = B * L.n_strip;
+    int64_t chunks = kColBlocksTarget / blocks;
+    if (chunks < 1)
+        chunks = 1;
+    while (chunks > 1 && N / chunks < 256)
+        --chunks;
     L.n_chunk = (int)chunks;
     L.rows_per_chunk = (int)((N + chunks - 1) / chunks);
     size_t off = 0;
@@ -217,10 +222,6 @@ sk_inf_cols(const float *__restrict__ C, uint8_t *__restrict__ inf_col, int64_t 
 
 // ---- row sweep: log_u -------------------------------------------------------------
 
-// Each wave owns kRowsPerWave consecutive rows of one batch.  M % 4 == 0.
-// Single-chunk rows (M <= 256*kRowNV): all the wave's row loads are issued
-// before any reduction, and each row is an exact two-pass LSE over registers.
-// Longer rows: chunks of 256*kRowNV columns merged online.
 __device__ __forceinline__ void row_lse_update(Lse acc, int64_t r, const float *__restrict__ log_mu,
                                                float *__restrict__ log_u, float damp,
                                                int unbalanced) {
@@ -230,6 +231,9 @@ __device__ __forceinline__ void row_lse_update(Lse acc, int64_t r, const float *
     }
 }
 
+// Each wave owns kRowsPerWave consecutive rows of one batch; M % 4 == 0 and
+// M <= 256*kRowNV.  All the wave's row loads are issued before any reduction,
+// and each row is an exact two-pass LSE over registers.
 __global__ void __launch_bounds__(kRowWaves * 64)
 sk_row_sweep(const float *__restrict__ K, const float *__restrict__ log_v,
              const float *__restrict__ log_mu, const uint8_t *__restrict__ inf_row,
@@ -244,7 +248,7 @@ sk_row_sweep(const float *__restrict__ K, const float *__restrict__ log_v,
     const int64_t m4 = M / 4;
     const float4 *lv4 = reinterpret_cast<const float4 *>(log_v + b * M);
     constexpr int CH = 64 * kRowNV;  // float4 per chunk
-    if (m4 <= CH) {
+    {  // m4 <= CH here (longer rows take sk_row_sweep_split)
         float4 kk[kRowsPerWave][kRowNV];
 #pragma unroll
         for (int rr = 0; rr < kRowsPerWave; ++rr) {
@@ -292,51 +296,73 @@ sk_row_sweep(const float *__restrict__ K, const float *__restrict__ log_v,
             s = wave_sum_all(s);
             row_lse_update(Lse{m, s}, r, log_mu, log_u, damp, unbalanced);
         }
-        return;
     }
-    for (int rr = 0; rr < kRowsPerWave; ++rr) {
-        const int64_t i = i_begin + rr;
-        if (i >= N)
-            break;
-        const int64_t r = b * N + i;
-        if (inf_row[r])
-            continue;
-        const float4 *row4 = reinterpret_cast<const float4 *>(K + r * M);
-        Lse acc{-f_inf(), 0.f};
-        for (int64_t base = 0; base < m4; base += CH) {
-            float t[4 * kRowNV];
+}
+
+// Rows longer than one chunk (M > 256*kRowNV, M % 4 == 0): a block of W waves
+// owns one row; wave w takes chunks w, w+W, ... (each an exact two-pass LSE
+// over registers, merged online when a wave has several), and the W partial
+// (max, sum) pairs merge in LDS in wave order.  Every wave keeps a whole
+// chunk's loads in flight, as the short-row sweep does.
+template <int W>
+__global__ void __launch_bounds__(W * 64)
+sk_row_sweep_split(const float *__restrict__ K, const float *__restrict__ log_v,
+                   const float *__restrict__ log_mu, const uint8_t *__restrict__ inf_row,
+                   float *__restrict__ log_u, int64_t N, int64_t M, float damp, int unbalanced) {
+    const int64_t r = blockIdx.x;  // b * N + i
+    if (inf_row[r])
+        return;  // lse = -inf: log_u keeps its value
+    const int64_t b = r / N;
+    const int w = threadIdx.x / 64;
+    const int lane = lane_id();
+    const int64_t m4 = M / 4;
+    constexpr int CH = 64 * kRowNV;
+    const float4 *row4 = reinterpret_cast<const float4 *>(K + r * M);
+    const float4 *lv4 = reinterpret_cast<const float4 *>(log_v + b * M);
+    Lse acc{-f_inf(), 0.f};
+    for (int64_t base = (int64_t)w * CH; base < m4; base += (int64_t)W * CH) {
+        float4 kk[kRowNV], lv[kRowNV];
 #pragma unroll
-            for (int k = 0; k < kRowNV; ++k) {
-                const int64_t q = base + (int64_t)k * 64 + lane;
-                if (q < m4) {
-                    const float4 kq = row4[q];
-                    const float4 vq = lv4[q];
-                    t[4 * k + 0] = kq.x + vq.x;
-                    t[4 * k + 1] = kq.y + vq.y;
-                    t[4 * k + 2] = kq.z + vq.z;
-                    t[4 * k + 3] = kq.w + vq.w;
-                } else {
-                    t[4 * k + 0] = t[4 * k + 1] = t[4 * k + 2] = t[4 * k + 3] = -f_inf();
-                }
-            }
-            float m = t[0];
-#pragma unroll
-            for (int k = 1; k < 4 * kRowNV; ++k)
-                m = fmaxf(m, t[k]);
-            m = wave_max_all(m);
-            const float newm = fmaxf(acc.m, m);
-            const float sh = lse_shift(newm);
-            float s = 0.f;
-#pragma unroll
-            for (int k = 0; k < 4 * kRowNV; ++k)
-                s += exp_nonpos(t[k] - sh);
-            s = wave_sum_all(s);
-            if (acc.s != 0.f)
-                s += acc.s * exp_nonpos(lse_shift(acc.m) - sh);
-            acc.m = newm;
-            acc.s = s;
+        for (int k = 0; k < kRowNV; ++k) {
+            const int64_t q = base + (int64_t)k * 64 + lane;
+            kk[k] = q < m4 ? row4[q] : make_float4(-f_inf(), -f_inf(), -f_inf(), -f_inf());
         }
-        row_lse_update(acc, r, log_mu, log_u, damp, unbalanced);
+#pragma unroll
+        for (int k = 0; k < kRowNV; ++k) {
+            const int64_t q = base + (int64_t)k * 64 + lane;
+            lv[k] = q < m4 ? lv4[q] : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+        float t[4 * kRowNV];
+#pragma unroll
+        for (int k = 0; k < kRowNV; ++k) {
+            t[4 * k + 0] = kk[k].x + lv[k].x;
+            t[4 * k + 1] = kk[k].y + lv[k].y;
+            t[4 * k + 2] = kk[k].z + lv[k].z;
+            t[4 * k + 3] = kk[k].w + lv[k].w;
+        }
+        float m = t[0];
+#pragma unroll
+        for (int k = 1; k < 4 * kRowNV; ++k)
+            m = fmaxf(m, t[k]);
+        m = wave_max_all(m);
+        const float sh = lse_shift(m);
+        float sum = 0.f;
+#pragma unroll
+        for (int k = 0; k < 4 * kRowNV; ++k)
+            sum += exp_nonpos(t[k] - sh);
+        sum = wave_sum_all(sum);
+        acc = lse_merge(acc, Lse{m, sum});
+    }
+    __shared__ float2 part[W];
+    if (lane == 0)
+        part[w] = make_float2(acc.m, acc.s);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        Lse tot{part[0].x, part[0].y};
+#pragma unroll
+        for (int k = 1; k < W; ++k)
+            tot = lse_merge(tot, Lse{part[k].x, part[k].y});
+        log_u[r] = update_potential(lse_value(tot), log_mu[r], log_u[r], damp, unbalanced != 0);
     }
 }
 
@@ -378,7 +404,7 @@ sk_row_sweep_scalar(const float *__restrict__ K, const float *__restrict__ log_v
 // strip*64 + 4*tc .. +3, row group tg = tid / 16 folds rows chunk_start + tg,
 // + 16, ... .  With one chunk the block finishes the LSE and updates log_v;
 // otherwise it writes (max, sum) partials for sk_col_merge.
-template <bool VEC>
+template <bool VEC, int SW>
 __global__ void __launch_bounds__(kColThreads)
 sk_col_sweep(const float *__restrict__ K, const float *__restrict__ log_u,
              const float *__restrict__ log_nu, const uint8_t *__restrict__ inf_col,
@@ -386,9 +412,10 @@ sk_col_sweep(const float *__restrict__ K, const float *__restrict__ log_u,
              int rows_per_chunk, int n_chunk, float damp, int unbalanced) {
     const int strip = blockIdx.x, chunk = blockIdx.y;
     const int64_t b = blockIdx.z;
-    const int tc = threadIdx.x % (kColStripCols / 4);
-    const int tg = threadIdx.x / (kColStripCols / 4);
-    const int64_t j0 = (int64_t)strip * kColStripCols + 4 * tc;
+    constexpr int G = kColThreads / (SW / 4);  // row groups
+    const int tc = threadIdx.x % (SW / 4);
+    const int tg = threadIdx.x / (SW / 4);
+    const int64_t j0 = (int64_t)strip * SW + 4 * tc;
     const int64_t i0 = (int64_t)chunk * rows_per_chunk;
     const int64_t i1 = (i0 + rows_per_chunk < N) ? i0 + rows_per_chunk : N;
     const float *Kb = K + b * N * M;
@@ -398,11 +425,11 @@ sk_col_sweep(const float *__restrict__ K, const float *__restrict__ log_u,
     for (int c = 0; c < 4; ++c)
         acc[c] = Lse{-f_inf(), 0.f};
     const bool colok = j0 < M;
-    for (int64_t ib = i0 + tg; ib < i1; ib += (int64_t)kColGroups * kColU) {
+    for (int64_t ib = i0 + tg; ib < i1; ib += (int64_t)G * kColU) {
         float t[kColU][4];
 #pragma unroll
         for (int u = 0; u < kColU; ++u) {
-            const int64_t i = ib + (int64_t)u * kColGroups;
+            const int64_t i = ib + (int64_t)u * G;
             if (colok && i < i1) {
                 const float lui = lu[i];
                 if (VEC) {
@@ -441,19 +468,19 @@ sk_col_sweep(const float *__restrict__ K, const float *__restrict__ log_u,
             acc[c].s += add;
         }
     }
-    // merge the 16 row groups of each column in LDS
-    __shared__ float2 part[kColGroups][kColStripCols];
+    // merge the G row groups of each column in LDS
+    __shared__ float2 part[G][SW];
 #pragma unroll
     for (int c = 0; c < 4; ++c)
         part[tg][4 * tc + c] = make_float2(acc[c].m, acc[c].s);
     __syncthreads();
-    if (threadIdx.x < kColStripCols) {
+    if (threadIdx.x < SW) {
         const int cc = threadIdx.x;
-        const int64_t j = (int64_t)strip * kColStripCols + cc;
+        const int64_t j = (int64_t)strip * SW + cc;
         if (j < M) {
             Lse tot{-f_inf(), 0.f};
 #pragma unroll
-            for (int g = 0; g < kColGroups; ++g)
+            for (int g = 0; g < G; ++g)
                 tot = lse_merge(tot, Lse{part[g][cc].x, part[g][cc].y});
             if (n_chunk == 1) {
                 const int64_t t = b * M + j;
@@ -563,7 +590,7 @@ extern "C" int tm_sinkhorn_f32(const float *cost, const float *a, const float *b
     const SinkhornLayout L = make_layout(B, N, M);
     if (workspace == nullptr || workspace_bytes < L.total)
         return TM_ERR_WORKSPACE;
-    if (L.n_strip > 0x7fffffff || L.n_chunk > 65535 || B > 65535)
+    if (L.n_strip > 0x7fffffff || L.n_chunk > 65535 || B > 65535 || B * N > 0x7fffffff)
         return TM_ERR_UNSUPPORTED_SHAPE;
     char *ws = static_cast<char *>(workspace);
     float *K = reinterpret_cast<float *>(ws + L.off_k);
@@ -610,18 +637,34 @@ extern "C" int tm_sinkhorn_f32(const float *cost, const float *a, const float *b
         }
         const float damp = unbalanced ? (float)(1.0 / (1.0 + eps_sched[s] / rho)) : 1.f;
         if (vec) {
-            TM_LAUNCH(sk_row_sweep, row_grid, dim3(kRowWaves * 64), 0, stream, K, log_v, log_mu,
-                      inf_row, log_u, B, N, M, waves_per_batch, damp, unbalanced ? 1 : 0);
-            TM_LAUNCH(sk_col_sweep<true>, col_grid, dim3(kColThreads), 0, stream, K, log_u,
-                      log_nu, inf_col, log_v, colpart, N, M, L.rows_per_chunk, L.n_chunk, damp,
-                      unbalanced ? 1 : 0);
+            const int64_t chunks = (M / 4 + 64 * kRowNV - 1) / (64 * kRowNV);
+            const dim3 split_grid((unsigned)(B * N));
+            const int ub = unbalanced ? 1 : 0;
+            if (chunks <= 1)
+                TM_LAUNCH(sk_row_sweep, row_grid, dim3(kRowWaves * 64), 0, stream, K, log_v,
+                          log_mu, inf_row, log_u, B, N, M, waves_per_batch, damp, ub);
+            else if (chunks <= 2)
+                TM_LAUNCH(sk_row_sweep_split<2>, split_grid, dim3(2 * 64), 0, stream, K, log_v,
+                          log_mu, inf_row, log_u, N, M, damp, ub);
+            else if (chunks <= 4)
+                TM_LAUNCH(sk_row_sweep_split<4>, split_grid, dim3(4 * 64), 0, stream, K, log_v,
+                          log_mu, inf_row, log_u, N, M, damp, ub);
+            else if (chunks <= 8)
+                TM_LAUNCH(sk_row_sweep_split<8>, split_grid, dim3(8 * 64), 0, stream, K, log_v,
+                          log_mu, inf_row, log_u, N, M, damp, ub);
+            else
+                TM_LAUNCH(sk_row_sweep_split<16>, split_grid, dim3(16 * 64), 0, stream, K, log_v,
+                          log_mu, inf_row, log_u, N, M, damp, ub);
+            TM_LAUNCH((sk_col_sweep<true, kColStrip>), col_grid, dim3(kColThreads), 0, stream, K,
+                      log_u, log_nu, inf_col, log_v, colpart, N, M, L.rows_per_chunk, L.n_chunk,
+                      damp, unbalanced ? 1 : 0);
         } else {
             TM_LAUNCH(sk_row_sweep_scalar, dim3(grid_for(B * N, 4, 1 << 30)), dim3(256), 0,
                       stream, K, log_v, log_mu, inf_row, log_u, B, N, M, damp,
                       unbalanced ? 1 : 0);
-            TM_LAUNCH(sk_col_sweep<false>, col_grid, dim3(kColThreads), 0, stream, K, log_u,
-                      log_nu, inf_col, log_v, colpart, N, M, L.rows_per_chunk, L.n_chunk, damp,
-                      unbalanced ? 1 : 0);
+            TM_LAUNCH((sk_col_sweep<false, kColStrip>), col_grid, dim3(kColThreads), 0, stream, K,
+                      log_u, log_nu, inf_col, log_v, colpart, N, M, L.rows_per_chunk, L.n_chunk,
+                      damp, unbalanced ? 1 : 0);
         }
         if (L.n_chunk > 1)
             TM_LAUNCH(sk_col_merge, dim3(grid_for(B * M, kMapBlock, 1 << 30)), dim3(kMapBlock),
