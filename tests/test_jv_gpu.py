@@ -96,7 +96,8 @@ def test_random_batches_vs_oracle(kind, device):
 def test_large_k_vs_oracle(kind, device):
     """K > 64: the global-memory kernel (cost outside LDS)."""
     rng = np.random.default_rng(zlib.crc32(("large" + kind).encode()))
-    for n, m in [(65, 65), (100, 80), (80, 100), (128, 128), (200, 130), (300, 300)]:
+    for n, m in [(65, 65), (100, 80), (80, 100), (128, 128), (200, 130), (300, 300),
+                 (1000, 1024)]:
         c = _random_batch(rng, kind, 6, n, m)
         want = jv.jv_dense_batch(c)
         print(f"large kind {kind} shape {(6, n, m)}", flush=True)

@@ -40,6 +40,7 @@ struct LargeLds {
     int32_t pred[kMaxLargeK];
     int32_t cols[kMaxLargeK];
     int32_t ev[kMaxLargeK];  // claims in the column reduction, swap events later
+    int32_t emap[kMaxLargeK];  // position -> index in the current tie run, else -1
 };
 
 // The virtually padded K x K tile: 0 outside (N, M), +inf -> sentinel.
@@ -55,26 +56,105 @@ struct CostView {
     }
 };
 
+// Row i of the padded tile into registers, lane l holding columns l, l + 64,
+// ...: every load is issued before any is used, so a row costs one memory
+// latency rather than one per 64-column chunk.
+__device__ __forceinline__ void load_row(const CostView &C, int i, int E, int K,
+                                         float (&cr)[kMaxChunks]) {
+    const int lane = lane_id();
+#pragma unroll
+    for (int e = 0; e < kMaxChunks; ++e) {
+        const int j = e * 64 + lane;
+        cr[e] = (e < E && j < K) ? C.at(i, j) : 0.f;
+    }
+}
+
 __device__ __forceinline__ void lds_sync() { __syncthreads(); }
 
-// Lane-0 serial swap replay: events are positions with bit 31 set for a new
-// running minimum (swap with lo) and clear for a tie (swap with hi).
-__device__ __forceinline__ int replay_find_events(LargeLds &L, int n_ev, int lo) {
-    int hi = lo + 1;
-    for (int k = 0; k < n_ev; ++k) {
-        const int e = L.ev[k];
-        const int pos = e & 0x7fffffff;
-        if (e < 0) {
-            const int t = L.cols[pos];
-            L.cols[pos] = L.cols[lo];
-            L.cols[lo] = t;
-            hi = lo + 1;
-        } else {
-            const int t = L.cols[pos];
-            L.cols[pos] = L.cols[hi];
-            L.cols[hi] = t;
-            ++hi;
+// A run of tie events: for i = 0 .. n-1 in order, swap cols[pos_i] with
+// cols[h0 + i] (pos_i = ev[k0 + i], strictly increasing, pos_i >= h0 + i).
+// The result, computed for all events at once: cols[h0 + i] receives the
+// original cols[pos_i]; a position pos_i >= h0 + n receives what was at h0 + i
+// when event i ran -- the original element there, unless h0 + i was an
+// earlier event's position pos_j (j < i), in which case it is what event j
+// received, and so on down the chain.  Leaves emap all -1.
+__device__ void apply_tie_run(LargeLds &L, int k0, int n, int h0) {
+    const int lane = lane_id();
+    for (int i = lane; i < n; i += 64)
+        L.emap[L.ev[k0 + i] & 0x7fffffff] = i;
+    lds_sync();
+    constexpr int kPer = kMaxLargeK / 64;
+    int a[kPer], b[kPer];
+#pragma unroll
+    for (int t = 0; t < kPer; ++t) {
+        const int i = t * 64 + lane;
+        if (i < n) {
+            const int pos = L.ev[k0 + i] & 0x7fffffff;
+            a[t] = L.cols[pos];
+            if (pos >= h0 + n) {
+                int h = h0 + i;
+                int j = L.emap[h];
+                while (j >= 0 && j < i) {  // j strictly falls: at most i steps
+                    h = h0 + j;
+                    j = L.emap[h];
+                }
+                b[t] = L.cols[h];
+            }
         }
+    }
+    lds_sync();
+#pragma unroll
+    for (int t = 0; t < kPer; ++t) {
+        const int i = t * 64 + lane;
+        if (i < n) {
+            const int pos = L.ev[k0 + i] & 0x7fffffff;
+            L.cols[h0 + i] = a[t];
+            if (pos >= h0 + n)
+                L.cols[pos] = b[t];
+        }
+    }
+    lds_sync();
+    for (int i = lane; i < n; i += 64)
+        L.emap[L.ev[k0 + i] & 0x7fffffff] = -1;
+    lds_sync();
+}
+
+// Replays find_dense's swap events in order: bit 31 set = a new running
+// minimum (swap with lo, hi back to lo + 1), clear = a tie (swap with hi, then
+// hi + 1).  Each new minimum is one swap; each run of ties in between goes
+// through apply_tie_run.  Returns hi (uniform).
+__device__ int replay_find_events(LargeLds &L, int n_ev, int lo) {
+    const int lane = lane_id();
+    int hi = lo + 1;
+    int k = 0;
+    while (k < n_ev) {
+        const int e = L.ev[k];
+        if (e < 0) {
+            const int pos = e & 0x7fffffff;
+            lds_sync();
+            if (lane == 0) {
+                const int t = L.cols[pos];
+                L.cols[pos] = L.cols[lo];
+                L.cols[lo] = t;
+            }
+            lds_sync();
+            hi = lo + 1;
+            ++k;
+            continue;
+        }
+        // the run of ties up to the next new minimum
+        int r = n_ev;
+        for (int base = k; base < n_ev; base += 64) {
+            const int q = base + lane;
+            const uint64_t recm = ballot(q < n_ev && L.ev[q] < 0);
+            if (recm) {
+                r = base + first_lane(recm);
+                break;
+            }
+        }
+        apply_tie_run(L, k, r - k, hi);
+        hi += r - k;
+        k = r;
     }
     return hi;
 }
@@ -106,18 +186,26 @@ __device__ bool large_solve(const int K, const int E, LargeLds &L, const CostVie
             ymin[e] = 0;
         }
         const int rows_real = C.N < K ? C.N : K;
-        for (int i = 0; i < rows_real; ++i) {
+        // four rows' loads in flight per pass; rows still fold in order
+        constexpr int R = 4;
+        for (int i = 0; i < rows_real; i += R) {
+            float c[R][kMaxChunks];
 #pragma unroll
-            for (int e = 0; e < kMaxChunks; ++e) {
-                const int j = e * 64 + lane;
-                if (e < E && j < K) {
-                    const float c = C.at(i, j);
-                    if (c < vmin[e]) {
-                        vmin[e] = c;
-                        ymin[e] = i;
+            for (int q = 0; q < R; ++q)
+#pragma unroll
+                for (int e = 0; e < kMaxChunks; ++e) {
+                    const int j = e * 64 + lane;
+                    c[q][e] = (i + q < rows_real && e < E && j < K) ? C.at(i + q, j) : finf();
+                }
+#pragma unroll
+            for (int q = 0; q < R; ++q)
+#pragma unroll
+                for (int e = 0; e < kMaxChunks; ++e) {
+                    if (c[q][e] < vmin[e]) {
+                        vmin[e] = c[q][e];
+                        ymin[e] = i + q;
                     }
                 }
-            }
         }
         // padding rows (all 0): the first one wins where 0 is a strict new minimum
 #pragma unroll
@@ -132,6 +220,7 @@ __device__ bool large_solve(const int K, const int E, LargeLds &L, const CostVie
                 L.y[j] = ymin[e];
                 L.x[j] = -1;   // K rows == K columns
                 L.ev[j] = 0;   // claim counts
+                L.emap[j] = -1;
             }
         }
     }
@@ -170,16 +259,18 @@ __device__ bool large_solve(const int K, const int E, LargeLds &L, const CostVie
             t &= t - 1;
             const int own = L.x[i];
             // mn = LARGE, then `if (c < mn) mn = c` over j != own in order
+            float cr[kMaxChunks];
+            load_row(C, i, E, K, cr);
             int best = kKeyNone;
-            for (int e2 = 0; e2 < E; ++e2) {
+#pragma unroll
+            for (int e2 = 0; e2 < kMaxChunks; ++e2) {
                 const int j = e2 * 64 + lane;
-                float r = finf();
-                if (j < K && j != own)
-                    r = C.at(i, j) - L.v[j];
-                if (j < K)
+                if (e2 < E && j < K) {
+                    const float r = j != own ? cr[e2] - L.v[j] : finf();
                     L.rbuf[j] = r;
-                if (j < K && j != own)
-                    best = min(best, fkey(r));
+                    if (j != own)
+                        best = min(best, fkey(r));
+                }
             }
             best = uniform_i(wave_min_key(best));
             lds_sync();
@@ -212,11 +303,14 @@ __device__ bool large_solve(const int K, const int E, LargeLds &L, const CostVie
             const int fi = L.fr[cur];
             ++cur;
             // reduced costs of row fi, lane-local two-minimum by (value, column)
+            float cr[kMaxChunks];
+            load_row(C, fi, E, K, cr);
             int a = kKeyNone, bk = kKeyNone;
-            for (int e = 0; e < E; ++e) {
+#pragma unroll
+            for (int e = 0; e < kMaxChunks; ++e) {
                 const int j = e * 64 + lane;
-                if (j < K) {
-                    const float r = C.at(fi, j) - L.v[j];
+                if (e < E && j < K) {
+                    const float r = cr[e] - L.v[j];
                     L.rbuf[j] = r;
                     const int k = fkey(r);
                     if (k < a) {
@@ -348,11 +442,14 @@ __device__ bool large_solve(const int K, const int E, LargeLds &L, const CostVie
     // ---- augmentation (ca_dense / find_path_dense, jonker_dense_flat.h:75-122,237-258) ----
     for (int f = 0; f < n_free; ++f) {
         const int start = L.fr[f];
-        for (int e = 0; e < E; ++e) {
+        float cr[kMaxChunks];
+        load_row(C, start, E, K, cr);
+#pragma unroll
+        for (int e = 0; e < kMaxChunks; ++e) {
             const int j = e * 64 + lane;
-            if (j < K) {
+            if (e < E && j < K) {
                 L.cols[j] = j;
-                L.d[j] = C.at(start, j) - L.v[j];
+                L.d[j] = cr[e] - L.v[j];
                 L.pred[j] = start;
             }
         }
@@ -379,11 +476,7 @@ __device__ bool large_solve(const int K, const int E, LargeLds &L, const CostVie
                     carry = min(carry, readlane_i(incl, 63));
                 }
                 lds_sync();
-                int h = 0;
-                if (lane == 0)
-                    h = replay_find_events(L, n_ev, lo);
-                hi = readlane_i(h, 0);
-                lds_sync();
+                hi = replay_find_events(L, n_ev, lo);
                 // the LAST unassigned column of the tied block wins
                 int last = -1;
                 for (int base = lo; base < hi; base += 64) {
@@ -408,14 +501,32 @@ __device__ bool large_solve(const int K, const int E, LargeLds &L, const CostVie
                 const float hq = C.at(iq, jq) - L.v[jq] - level;
                 int n_ev = 0;
                 const int base0 = shi;
-                for (int base = base0; base < K; base += 64) {
+                // gather row iq at the columns of positions [shi, K), all
+                // loads in flight together
+                int jg[kMaxChunks];
+                float cg[kMaxChunks];
+#pragma unroll
+                for (int e = 0; e < kMaxChunks; ++e) {
+                    const int p = base0 + e * 64 + lane;
+                    jg[e] = p < K ? L.cols[p] : 0;
+                }
+#pragma unroll
+                for (int e = 0; e < kMaxChunks; ++e) {
+                    const int p = base0 + e * 64 + lane;
+                    cg[e] = p < K ? C.at(iq, jg[e]) : 0.f;
+                }
+#pragma unroll
+                for (int e = 0; e < kMaxChunks; ++e) {
+                    const int base = base0 + e * 64;
+                    if (base >= K)
+                        break;
                     const int p = base + lane;
                     int jp = 0;
                     float r = 0.f, dp = 0.f;
                     bool better = false;
                     if (p < K) {
-                        jp = L.cols[p];
-                        r = C.at(iq, jp) - L.v[jp] - hq;
+                        jp = jg[e];
+                        r = cg[e] - L.v[jp] - hq;
                         dp = L.d[jp];
                         better = r < dp;
                     }
@@ -440,19 +551,9 @@ __device__ bool large_solve(const int K, const int E, LargeLds &L, const CostVie
                 lds_sync();
                 if (early)
                     break;
-                int h = 0;
-                if (lane == 0) {
-                    h = shi;
-                    for (int k = 0; k < n_ev; ++k) {
-                        const int pos = L.ev[k];
-                        const int t = L.cols[pos];
-                        L.cols[pos] = L.cols[h];
-                        L.cols[h] = t;
-                        ++h;
-                    }
-                }
-                shi = readlane_i(h, 0);
-                lds_sync();
+                if (n_ev > 0)
+                    apply_tie_run(L, 0, n_ev, shi);
+                shi += n_ev;
             }
             if (!early) {
                 lo = slo;
