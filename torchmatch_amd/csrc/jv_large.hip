@@ -41,6 +41,16 @@ struct LargeLds {
     int32_t cols[kMaxLargeK];
     int32_t ev[kMaxLargeK];  // claims in the column reduction, swap events later
     int32_t emap[kMaxLargeK];  // position -> index in the current tie run, else -1
+    // Row cache of the augmenting row reduction: for row i, the three columns
+    // that were its smallest reduced costs when it was last scanned (ascending
+    // column order), their costs, and tau = the fourth smallest reduced cost
+    // of that scan (-inf: never scanned).  Duals only fall in that phase, so
+    // every other reduced cost of the row is still >= tau; when the second
+    // smallest cached value (with the current duals) is < tau, the two cached
+    // minima are the row's two minima, first column on ties.
+    int32_t cq[3][kMaxLargeK];
+    float cg[3][kMaxLargeK];
+    float ctau[kMaxLargeK];
 };
 
 // The virtually padded K x K tile: 0 outside (N, M), +inf -> sentinel.
@@ -293,6 +303,10 @@ __device__ bool large_solve(const int K, const int E, LargeLds &L, const CostVie
 
     // ---- augmenting row reduction (carr_dense, jonker_dense_flat.h:178-235) ----
     const uint32_t rr_limit = 4u * (uint32_t)K * (uint32_t)K + 64u;
+    for (int i = lane; i < K; i += 64)
+        L.ctau[i] = -finf();
+    float *cbuf = reinterpret_cast<float *>(L.ev);  // row costs of the last scan
+    lds_sync();
     for (int round = 0; n_free > 0 && round < 2; ++round) {
         uint32_t cur = 0, rr = 0;
         int still = 0;
@@ -302,17 +316,47 @@ __device__ bool large_solve(const int K, const int E, LargeLds &L, const CostVie
                 return false;
             const int fi = L.fr[cur];
             ++cur;
+            int j1 = -1, j2 = -1;
+            float u1 = 0.f, u2 = 0.f;
+            bool hit = false;
+            {
+                const float tau = L.ctau[fi];
+                if (tau > -finf()) {
+                    const int q0 = L.cq[0][fi], q1 = L.cq[1][fi], q2 = L.cq[2][fi];
+                    const float r0 = L.cg[0][fi] - L.v[q0];
+                    const float r1 = L.cg[1][fi] - L.v[q1];
+                    const float r2 = L.cg[2][fi] - L.v[q2];
+                    const float t1 = fminf(fminf(r0, r1), r2);
+                    const float t2 = __builtin_amdgcn_fmed3f(r0, r1, r2);
+                    if (t2 < tau && t2 < kLarge) {
+                        // u2 < LARGE: the reference's (LARGE, -1) start slot
+                        // cannot win
+                        hit = true;
+                        const bool e0 = r0 == t1, e1 = r1 == t1;
+                        j1 = e0 ? q0 : (e1 ? q1 : q2);
+                        j2 = e0 ? (r2 < r1 ? q2 : q1)
+                                : (e1 ? (r2 < r0 ? q2 : q0) : (r1 < r0 ? q1 : q0));
+                        u1 = t1;
+                        u2 = t2;
+                    }
+                }
+            }
+            if (!hit) {
             // reduced costs of row fi, lane-local two-minimum by (value, column)
             float cr[kMaxChunks];
+            int kk[kMaxChunks];
             load_row(C, fi, E, K, cr);
             int a = kKeyNone, bk = kKeyNone;
 #pragma unroll
             for (int e = 0; e < kMaxChunks; ++e) {
                 const int j = e * 64 + lane;
+                kk[e] = kKeyNone;
                 if (e < E && j < K) {
                     const float r = cr[e] - L.v[j];
                     L.rbuf[j] = r;
+                    cbuf[j] = cr[e];
                     const int k = fkey(r);
+                    kk[e] = k;
                     if (k < a) {
                         bk = a;
                         a = k;
@@ -332,8 +376,6 @@ __device__ bool large_solve(const int K, const int E, LargeLds &L, const CostVie
             }
             lds_sync();
             const float r0 = L.rbuf[0];
-            int j1 = -1, j2 = -1;
-            float u1, u2;
             if (!(r0 <= kLarge)) {
                 // the reference seeds (v1, j1) with column 0; beyond LARGE that
                 // seed changes the outcome: run its scan verbatim
@@ -399,6 +441,49 @@ __device__ bool large_solve(const int K, const int E, LargeLds &L, const CostVie
                     else
                         j2 = -1;
                 }
+                if (j2 >= 0) {
+                    // refill row fi's cache: the third smallest (value, column)
+                    // after j1, j2 and the fourth smallest value
+                    int a3 = kKeyNone, b3 = kKeyNone;
+#pragma unroll
+                    for (int e = 0; e < kMaxChunks; ++e) {
+                        const int j = e * 64 + lane;
+                        const int k = (j != j1 && j != j2) ? kk[e] : kKeyNone;
+                        if (k < a3) {
+                            b3 = a3;
+                            a3 = k;
+                        } else if (k < b3) {
+                            b3 = k;
+                        }
+                    }
+                    int p3, p4;
+                    wave_min2_key(a3, p3, p4);
+                    const int k3 = uniform_i(p3);
+                    const int k4 = min(uniform_i(p4), uniform_i(wave_min_key(b3)));
+                    if (k3 != kKeyNone) {
+                        int j3 = -1;
+#pragma unroll
+                        for (int e = 0; e < kMaxChunks; ++e) {
+                            const int j = e * 64 + lane;
+                            const uint64_t m3 = ballot(j != j1 && j != j2 && kk[e] == k3);
+                            if (j3 < 0 && m3)
+                                j3 = e * 64 + first_lane(m3);
+                        }
+                        const int lo12 = min(j1, j2), hi12 = max(j1, j2);
+                        const int s0 = min(lo12, j3), s2 = max(hi12, j3);
+                        const int s1 = j1 + j2 + j3 - s0 - s2;
+                        if (lane == 0) {
+                            L.cq[0][fi] = s0;
+                            L.cq[1][fi] = s1;
+                            L.cq[2][fi] = s2;
+                            L.cg[0][fi] = cbuf[s0];
+                            L.cg[1][fi] = cbuf[s1];
+                            L.cg[2][fi] = cbuf[s2];
+                            L.ctau[fi] = k4 == kKeyNone ? finf() : key_to_float(k4);
+                        }
+                    }
+                }
+            }
             }
             int jsel = j1;
             int i0 = L.y[j1];
