@@ -79,6 +79,24 @@ __device__ __forceinline__ void load_row(const CostView &C, int i, int E, int K,
     }
 }
 
+// Raw costs of a real row (i < N) for a prefetch: no use of the loaded values
+// here, so nothing waits for them until the row is scanned.
+__device__ __forceinline__ void load_row_raw(const CostView &C, int i, int E, int K,
+                                             float (&raw)[kMaxChunks]) {
+    const int lane = lane_id();
+    const float *src = C.src + (int64_t)i * C.M;
+#pragma unroll
+    for (int e = 0; e < kMaxChunks; ++e) {
+        const int j = e * 64 + lane;
+        raw[e] = (e < E && j < K && j < C.M) ? src[j] : 0.f;
+    }
+}
+
+// The padded-tile view of raw row costs: +inf -> sentinel, columns >= M -> 0.
+__device__ __forceinline__ float fix_cost(const CostView &C, float raw, int j) {
+    return j >= C.M ? 0.f : (isfinite(raw) ? raw : C.sentinel);
+}
+
 __device__ __forceinline__ void lds_sync() { __syncthreads(); }
 
 // A run of tie events: for i = 0 .. n-1 in order, swap cols[pos_i] with
@@ -181,6 +199,163 @@ __device__ __forceinline__ int append_events(LargeLds &L, int n_ev, uint64_t mas
         L.ev[slot] = (base + lane) | (rec ? (int)tag_mask_rec : 0);
     }
     return n_ev + __builtin_popcountll(mask);
+}
+
+// One row's two-minimum by a full scan (reference order: first column on
+// ties, the (LARGE, -1) start slot of the second minimum, column 0 as the
+// first seed), from registers `pf` when they hold row fi, else loaded.  When
+// `refill` is set and the result is within LARGE, the row cache of fi is
+// refilled from the same scan.
+__device__ void scan_row(LargeLds &L, const CostView &C, int fi, int E, int K,
+                         const float (&pf)[kMaxChunks], int pf_row, float *cbuf, bool refill,
+                         int &j1, int &j2, float &u1, float &u2) {
+    const int lane = lane_id();
+    float cr[kMaxChunks];
+    if (pf_row == fi) {
+#pragma unroll
+        for (int e = 0; e < kMaxChunks; ++e)
+            cr[e] = fix_cost(C, pf[e], e * 64 + lane);
+    } else {
+        load_row(C, fi, E, K, cr);
+    }
+    // reduced costs, lane-local two-minimum of keys
+    int kk[kMaxChunks];
+    int a = kKeyNone, bk = kKeyNone;
+#pragma unroll
+    for (int e = 0; e < kMaxChunks; ++e) {
+        const int j = e * 64 + lane;
+        kk[e] = kKeyNone;
+        if (e < E && j < K) {
+            const float r = cr[e] - L.v[j];
+            L.rbuf[j] = r;
+            cbuf[j] = cr[e];
+            const int k = fkey(r);
+            kk[e] = k;
+            if (k < a) {
+                bk = a;
+                a = k;
+            } else if (k < bk) {
+                bk = k;
+            }
+        }
+    }
+    int k1, k2;
+    {
+        int p1, p2;
+        wave_min2_key(a, p1, p2);
+        // the multiset two-minimum of the per-lane pairs: merge with b
+        const int bmin = uniform_i(wave_min_key(bk));
+        k1 = uniform_i(p1);
+        k2 = min(uniform_i(p2), bmin);
+    }
+    lds_sync();
+    const float r0 = L.rbuf[0];
+    j1 = -1;
+    j2 = -1;
+    if (!(r0 <= kLarge)) {
+        // the reference seeds (v1, j1) with column 0; beyond LARGE that seed
+        // changes the outcome: run its scan verbatim
+        float w1 = r0, w2 = kLarge;
+        int i1 = 0, i2 = -1;
+        if (lane == 0) {
+            for (int j = 1; j < K; ++j) {
+                const float r = L.rbuf[j];
+                if (!(r < w2))
+                    continue;
+                if (r >= w1) {
+                    w2 = r;
+                    i2 = j;
+                } else {
+                    w2 = w1;
+                    i2 = i1;
+                    w1 = r;
+                    i1 = j;
+                }
+            }
+        }
+        j1 = readlane_i(i1, 0);
+        j2 = readlane_i(i2, 0);
+        u1 = readlane_f(w1, 0);
+        u2 = readlane_f(w2, 0);
+        return;
+    }
+    // first column (in index order) at k1; second: the next one at k1 if
+    // k2 == k1, else the first at k2
+    int found = 0;
+#pragma unroll
+    for (int e = 0; e < kMaxChunks; ++e) {
+        if (found < 2) {
+            uint64_t m1 = ballot(kk[e] == k1);
+            if (found == 0 && m1) {
+                j1 = e * 64 + first_lane(m1);
+                m1 &= m1 - 1;
+                found = 1;
+            }
+            if (k2 == k1 && found == 1 && m1) {
+                j2 = e * 64 + first_lane(m1);
+                found = 2;
+            }
+        }
+    }
+    if (k2 != k1 && k2 != kKeyNone) {
+#pragma unroll
+        for (int e = 0; e < kMaxChunks; ++e) {
+            const uint64_t m2 = ballot(kk[e] == k2);
+            if (j2 < 0 && m2)
+                j2 = e * 64 + first_lane(m2);
+        }
+    }
+    u1 = L.rbuf[j1];
+    u2 = kLarge;
+    if (j2 >= 0) {
+        const float w = L.rbuf[j2];
+        if (w < kLarge)
+            u2 = w;
+        else
+            j2 = -1;
+    }
+    if (!refill || j2 < 0)
+        return;
+    // refill: the third smallest (value, column) after j1, j2 and the fourth
+    // smallest value
+    int a3 = kKeyNone, b3 = kKeyNone;
+#pragma unroll
+    for (int e = 0; e < kMaxChunks; ++e) {
+        const int j = e * 64 + lane;
+        const int k = (j != j1 && j != j2) ? kk[e] : kKeyNone;
+        if (k < a3) {
+            b3 = a3;
+            a3 = k;
+        } else if (k < b3) {
+            b3 = k;
+        }
+    }
+    int p3, p4;
+    wave_min2_key(a3, p3, p4);
+    const int k3 = uniform_i(p3);
+    const int k4 = min(uniform_i(p4), uniform_i(wave_min_key(b3)));
+    if (k3 == kKeyNone)
+        return;
+    int j3 = -1;
+#pragma unroll
+    for (int e = 0; e < kMaxChunks; ++e) {
+        const int j = e * 64 + lane;
+        const uint64_t m3 = ballot(j != j1 && j != j2 && kk[e] == k3);
+        if (j3 < 0 && m3)
+            j3 = e * 64 + first_lane(m3);
+    }
+    const int lo12 = min(j1, j2), hi12 = max(j1, j2);
+    const int s0 = min(lo12, j3), s2 = max(hi12, j3);
+    const int s1 = j1 + j2 + j3 - s0 - s2;
+    if (lane == 0) {
+        L.cq[0][fi] = s0;
+        L.cq[1][fi] = s1;
+        L.cq[2][fi] = s2;
+        L.cg[0][fi] = cbuf[s0];
+        L.cg[1][fi] = cbuf[s1];
+        L.cg[2][fi] = cbuf[s2];
+        L.ctau[fi] = k4 == kKeyNone ? finf() : key_to_float(k4);
+    }
 }
 
 __device__ bool large_solve(const int K, const int E, LargeLds &L, const CostView &C) {
@@ -307,6 +482,14 @@ __device__ bool large_solve(const int K, const int E, LargeLds &L, const CostVie
         L.ctau[i] = -finf();
     float *cbuf = reinterpret_cast<float *>(L.ev);  // row costs of the last scan
     lds_sync();
+    // Rows >= N of the padded tile are all 0, so their reduced costs are -v:
+    // one two-minimum serves every such row until a dual changes.
+    int pad_j1 = -1, pad_j2 = -1;
+    float pad_u1 = 0.f, pad_u2 = 0.f;
+    bool pad_valid = false;
+    // the next row's raw costs, loaded while the current step finishes
+    float pf[kMaxChunks];
+    int pf_row = -1;
     for (int round = 0; n_free > 0 && round < 2; ++round) {
         uint32_t cur = 0, rr = 0;
         int still = 0;
@@ -316,10 +499,17 @@ __device__ bool large_solve(const int K, const int E, LargeLds &L, const CostVie
                 return false;
             const int fi = L.fr[cur];
             ++cur;
+            const bool pad_row = fi >= C.N;
             int j1 = -1, j2 = -1;
             float u1 = 0.f, u2 = 0.f;
-            bool hit = false;
-            {
+            bool known = false;
+            if (pad_row && pad_valid) {
+                j1 = pad_j1;
+                j2 = pad_j2;
+                u1 = pad_u1;
+                u2 = pad_u2;
+                known = true;
+            } else if (!pad_row) {
                 const float tau = L.ctau[fi];
                 if (tau > -finf()) {
                     const int q0 = L.cq[0][fi], q1 = L.cq[1][fi], q2 = L.cq[2][fi];
@@ -331,7 +521,7 @@ __device__ bool large_solve(const int K, const int E, LargeLds &L, const CostVie
                     if (t2 < tau && t2 < kLarge) {
                         // u2 < LARGE: the reference's (LARGE, -1) start slot
                         // cannot win
-                        hit = true;
+                        known = true;
                         const bool e0 = r0 == t1, e1 = r1 == t1;
                         j1 = e0 ? q0 : (e1 ? q1 : q2);
                         j2 = e0 ? (r2 < r1 ? q2 : q1)
@@ -341,163 +531,42 @@ __device__ bool large_solve(const int K, const int E, LargeLds &L, const CostVie
                     }
                 }
             }
-            if (!hit) {
-            // reduced costs of row fi, lane-local two-minimum by (value, column)
-            float cr[kMaxChunks];
-            int kk[kMaxChunks];
-            load_row(C, fi, E, K, cr);
-            int a = kKeyNone, bk = kKeyNone;
-#pragma unroll
-            for (int e = 0; e < kMaxChunks; ++e) {
-                const int j = e * 64 + lane;
-                kk[e] = kKeyNone;
-                if (e < E && j < K) {
-                    const float r = cr[e] - L.v[j];
-                    L.rbuf[j] = r;
-                    cbuf[j] = cr[e];
-                    const int k = fkey(r);
-                    kk[e] = k;
-                    if (k < a) {
-                        bk = a;
-                        a = k;
-                    } else if (k < bk) {
-                        bk = k;
-                    }
-                }
-            }
-            int k1, k2;
-            {
-                int p1, p2;
-                wave_min2_key(a, p1, p2);
-                // the multiset two-minimum of the per-lane pairs: merge with b
-                const int bmin = uniform_i(wave_min_key(bk));
-                k1 = uniform_i(p1);
-                k2 = min(uniform_i(p2), bmin);
-            }
-            lds_sync();
-            const float r0 = L.rbuf[0];
-            if (!(r0 <= kLarge)) {
-                // the reference seeds (v1, j1) with column 0; beyond LARGE that
-                // seed changes the outcome: run its scan verbatim
-                float w1 = r0, w2 = kLarge;
-                int i1 = 0, i2 = -1;
-                if (lane == 0) {
-                    for (int j = 1; j < K; ++j) {
-                        const float r = L.rbuf[j];
-                        if (!(r < w2))
-                            continue;
-                        if (r >= w1) {
-                            w2 = r;
-                            i2 = j;
-                        } else {
-                            w2 = w1;
-                            i2 = i1;
-                            w1 = r;
-                            i1 = j;
-                        }
-                    }
-                }
-                j1 = readlane_i(i1, 0);
-                j2 = readlane_i(i2, 0);
-                u1 = readlane_f(w1, 0);
-                u2 = readlane_f(w2, 0);
-            } else {
-                // first column (in index order) at k1; second: the next one at
-                // k1 if k2 == k1, else the first at k2
-                int found = 0;
-                for (int e = 0; e < E && found < 2; ++e) {
-                    const int j = e * 64 + lane;
-                    const int k = j < K ? fkey(L.rbuf[j]) : kKeyNone;
-                    uint64_t m1 = ballot(k == k1);
-                    if (found == 0 && m1) {
-                        j1 = e * 64 + first_lane(m1);
-                        m1 &= m1 - 1;
-                        found = 1;
-                    }
-                    if (k2 == k1) {
-                        if (found == 1 && m1) {
-                            j2 = e * 64 + first_lane(m1);
-                            found = 2;
-                        }
-                    }
-                }
-                if (k2 != k1 && k2 != kKeyNone) {
-                    for (int e = 0; e < E; ++e) {
-                        const int j = e * 64 + lane;
-                        const int k = j < K ? fkey(L.rbuf[j]) : kKeyNone;
-                        const uint64_t m2 = ballot(k == k2);
-                        if (m2) {
-                            j2 = e * 64 + first_lane(m2);
-                            break;
-                        }
-                    }
-                }
-                u1 = L.rbuf[j1];
-                u2 = kLarge;
-                if (j2 >= 0) {
-                    const float w = L.rbuf[j2];
-                    if (w < kLarge)
-                        u2 = w;
-                    else
-                        j2 = -1;
-                }
-                if (j2 >= 0) {
-                    // refill row fi's cache: the third smallest (value, column)
-                    // after j1, j2 and the fourth smallest value
-                    int a3 = kKeyNone, b3 = kKeyNone;
-#pragma unroll
-                    for (int e = 0; e < kMaxChunks; ++e) {
-                        const int j = e * 64 + lane;
-                        const int k = (j != j1 && j != j2) ? kk[e] : kKeyNone;
-                        if (k < a3) {
-                            b3 = a3;
-                            a3 = k;
-                        } else if (k < b3) {
-                            b3 = k;
-                        }
-                    }
-                    int p3, p4;
-                    wave_min2_key(a3, p3, p4);
-                    const int k3 = uniform_i(p3);
-                    const int k4 = min(uniform_i(p4), uniform_i(wave_min_key(b3)));
-                    if (k3 != kKeyNone) {
-                        int j3 = -1;
-#pragma unroll
-                        for (int e = 0; e < kMaxChunks; ++e) {
-                            const int j = e * 64 + lane;
-                            const uint64_t m3 = ballot(j != j1 && j != j2 && kk[e] == k3);
-                            if (j3 < 0 && m3)
-                                j3 = e * 64 + first_lane(m3);
-                        }
-                        const int lo12 = min(j1, j2), hi12 = max(j1, j2);
-                        const int s0 = min(lo12, j3), s2 = max(hi12, j3);
-                        const int s1 = j1 + j2 + j3 - s0 - s2;
-                        if (lane == 0) {
-                            L.cq[0][fi] = s0;
-                            L.cq[1][fi] = s1;
-                            L.cq[2][fi] = s2;
-                            L.cg[0][fi] = cbuf[s0];
-                            L.cg[1][fi] = cbuf[s1];
-                            L.cg[2][fi] = cbuf[s2];
-                            L.ctau[fi] = k4 == kKeyNone ? finf() : key_to_float(k4);
-                        }
-                    }
-                }
-            }
+            if (!known)
+                scan_row(L, C, fi, E, K, pf, pf_row, cbuf, !pad_row, j1, j2, u1, u2);
+            if (pad_row && !pad_valid) {
+                pad_j1 = j1;
+                pad_j2 = j2;
+                pad_u1 = u1;
+                pad_u2 = u2;
+                pad_valid = true;
             }
             int jsel = j1;
             int i0 = L.y[j1];
             const float vj1 = L.v[j1];
             const float lowered = vj1 - (u2 - u1);
             const bool lowers = lowered < vj1;
+            const bool cap = rr < cur * (uint32_t)K;
+            if (cap && !lowers && i0 >= 0 && j2 >= 0) {
+                jsel = j2;
+                i0 = L.y[j2];
+            }
+            // the row the next step takes: the displaced owner when it goes
+            // back to the front, else the next queued row; load it now
+            {
+                const int nxt = (cap && lowers && i0 >= 0)
+                                    ? i0
+                                    : (cur < (uint32_t)n_free ? L.fr[cur] : -1);
+                if (nxt >= 0 && nxt < C.N && nxt != pf_row) {
+                    load_row_raw(C, nxt, E, K, pf);
+                    pf_row = nxt;
+                }
+            }
             lds_sync();
-            if (rr < cur * (uint32_t)K) {
+            if (cap) {
                 if (lowers) {
                     if (lane == 0)
                         L.v[j1] = lowered;
-                } else if (i0 >= 0 && j2 >= 0) {
-                    jsel = j2;
-                    i0 = L.y[j2];
+                    pad_valid = false;
                 }
                 if (i0 >= 0) {
                     if (lowers) {
