@@ -66,35 +66,37 @@ struct CostView {
     }
 };
 
-// Row i of the padded tile into registers, lane l holding columns l, l + 64,
-// ...: every load is issued before any is used, so a row costs one memory
-// latency rather than one per 64-column chunk.
-__device__ __forceinline__ void load_row(const CostView &C, int i, int E, int K,
-                                         float (&cr)[kMaxChunks]) {
-    const int lane = lane_id();
-#pragma unroll
-    for (int e = 0; e < kMaxChunks; ++e) {
-        const int j = e * 64 + lane;
-        cr[e] = (e < E && j < K) ? C.at(i, j) : 0.f;
-    }
-}
-
-// Raw costs of a real row (i < N) for a prefetch: no use of the loaded values
-// here, so nothing waits for them until the row is scanned.
-__device__ __forceinline__ void load_row_raw(const CostView &C, int i, int E, int K,
-                                             float (&raw)[kMaxChunks]) {
+// Raw costs of a real row (i < N), lane l holding columns l, l + 64, ...
+// Every lane loads every chunk (addresses clamped into the row, extra values
+// ignored by the callers), so the loads carry no branches and all of them are
+// in flight before any is used: a row costs one memory latency.
+__device__ __forceinline__ void load_row_raw(const CostView &C, int i, float (&raw)[kMaxChunks]) {
     const int lane = lane_id();
     const float *src = C.src + (int64_t)i * C.M;
 #pragma unroll
-    for (int e = 0; e < kMaxChunks; ++e) {
-        const int j = e * 64 + lane;
-        raw[e] = (e < E && j < K && j < C.M) ? src[j] : 0.f;
-    }
+    for (int e = 0; e < kMaxChunks; ++e)
+        raw[e] = src[min(e * 64 + lane, C.M - 1)];
 }
 
-// The padded-tile view of raw row costs: +inf -> sentinel, columns >= M -> 0.
+// The padded-tile view of a raw cost: +inf -> sentinel, columns >= M -> 0.
 __device__ __forceinline__ float fix_cost(const CostView &C, float raw, int j) {
     return j >= C.M ? 0.f : (isfinite(raw) ? raw : C.sentinel);
+}
+
+// Row i of the padded tile into registers (values for j >= K are unused).
+__device__ __forceinline__ void load_row(const CostView &C, int i, float (&cr)[kMaxChunks]) {
+    const int lane = lane_id();
+    if (i < C.N) {
+        float raw[kMaxChunks];
+        load_row_raw(C, i, raw);
+#pragma unroll
+        for (int e = 0; e < kMaxChunks; ++e)
+            cr[e] = fix_cost(C, raw[e], e * 64 + lane);
+    } else {
+#pragma unroll
+        for (int e = 0; e < kMaxChunks; ++e)
+            cr[e] = 0.f;
+    }
 }
 
 __device__ __forceinline__ void lds_sync() { __syncthreads(); }
@@ -216,7 +218,7 @@ __device__ void scan_row(LargeLds &L, const CostView &C, int fi, int E, int K,
         for (int e = 0; e < kMaxChunks; ++e)
             cr[e] = fix_cost(C, pf[e], e * 64 + lane);
     } else {
-        load_row(C, fi, E, K, cr);
+        load_row(C, fi, cr);
     }
     // reduced costs, lane-local two-minimum of keys
     int kk[kMaxChunks];
@@ -377,17 +379,15 @@ __device__ bool large_solve(const int K, const int E, LargeLds &L, const CostVie
             float c[R][kMaxChunks];
 #pragma unroll
             for (int q = 0; q < R; ++q)
-#pragma unroll
-                for (int e = 0; e < kMaxChunks; ++e) {
-                    const int j = e * 64 + lane;
-                    c[q][e] = (i + q < rows_real && e < E && j < K) ? C.at(i + q, j) : finf();
-                }
+                load_row_raw(C, min(i + q, rows_real - 1), c[q]);
 #pragma unroll
             for (int q = 0; q < R; ++q)
 #pragma unroll
                 for (int e = 0; e < kMaxChunks; ++e) {
-                    if (c[q][e] < vmin[e]) {
-                        vmin[e] = c[q][e];
+                    const int j = e * 64 + lane;
+                    const float cv = fix_cost(C, c[q][e], j);
+                    if (i + q < rows_real && e < E && j < K && cv < vmin[e]) {
+                        vmin[e] = cv;
                         ymin[e] = i + q;
                     }
                 }
@@ -445,7 +445,7 @@ __device__ bool large_solve(const int K, const int E, LargeLds &L, const CostVie
             const int own = L.x[i];
             // mn = LARGE, then `if (c < mn) mn = c` over j != own in order
             float cr[kMaxChunks];
-            load_row(C, i, E, K, cr);
+            load_row(C, i, cr);
             int best = kKeyNone;
 #pragma unroll
             for (int e2 = 0; e2 < kMaxChunks; ++e2) {
@@ -557,7 +557,7 @@ __device__ bool large_solve(const int K, const int E, LargeLds &L, const CostVie
                                     ? i0
                                     : (cur < (uint32_t)n_free ? L.fr[cur] : -1);
                 if (nxt >= 0 && nxt < C.N && nxt != pf_row) {
-                    load_row_raw(C, nxt, E, K, pf);
+                    load_row_raw(C, nxt, pf);
                     pf_row = nxt;
                 }
             }
@@ -597,7 +597,7 @@ __device__ bool large_solve(const int K, const int E, LargeLds &L, const CostVie
     for (int f = 0; f < n_free; ++f) {
         const int start = L.fr[f];
         float cr[kMaxChunks];
-        load_row(C, start, E, K, cr);
+        load_row(C, start, cr);
 #pragma unroll
         for (int e = 0; e < kMaxChunks; ++e) {
             const int j = e * 64 + lane;
@@ -664,10 +664,18 @@ __device__ bool large_solve(const int K, const int E, LargeLds &L, const CostVie
                     const int p = base0 + e * 64 + lane;
                     jg[e] = p < K ? L.cols[p] : 0;
                 }
+                if (iq < C.N) {
+                    const float *srow = C.src + (int64_t)iq * C.M;
 #pragma unroll
-                for (int e = 0; e < kMaxChunks; ++e) {
-                    const int p = base0 + e * 64 + lane;
-                    cg[e] = p < K ? C.at(iq, jg[e]) : 0.f;
+                    for (int e = 0; e < kMaxChunks; ++e)
+                        cg[e] = srow[min(jg[e], C.M - 1)];
+#pragma unroll
+                    for (int e = 0; e < kMaxChunks; ++e)
+                        cg[e] = fix_cost(C, cg[e], jg[e]);
+                } else {
+#pragma unroll
+                    for (int e = 0; e < kMaxChunks; ++e)
+                        cg[e] = 0.f;
                 }
 #pragma unroll
                 for (int e = 0; e < kMaxChunks; ++e) {
