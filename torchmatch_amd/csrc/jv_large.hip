@@ -58,12 +58,6 @@ struct CostView {
     const float *src;
     int N, M;
     float sentinel;
-    __device__ __forceinline__ float at(int i, int j) const {
-        if (i >= N || j >= M)
-            return 0.f;
-        const float c = src[(int64_t)i * M + j];
-        return isfinite(c) ? c : sentinel;
-    }
 };
 
 // Raw costs of a real row (i < N), lane l holding columns l, l + 64, ...
@@ -594,10 +588,18 @@ __device__ bool large_solve(const int K, const int E, LargeLds &L, const CostVie
     }
 
     // ---- augmentation (ca_dense / find_path_dense, jonker_dense_flat.h:75-122,237-258) ----
+    // the next path's start row is loaded while this path is searched
+    float nx[kMaxChunks];
+    if (n_free > 0 && L.fr[0] < C.N)
+        load_row_raw(C, L.fr[0], nx);
     for (int f = 0; f < n_free; ++f) {
         const int start = L.fr[f];
         float cr[kMaxChunks];
-        load_row(C, start, cr);
+#pragma unroll
+        for (int e = 0; e < kMaxChunks; ++e)
+            cr[e] = start < C.N ? fix_cost(C, nx[e], e * 64 + lane) : 0.f;
+        if (f + 1 < n_free && L.fr[f + 1] < C.N)
+            load_row_raw(C, L.fr[f + 1], nx);
 #pragma unroll
         for (int e = 0; e < kMaxChunks; ++e) {
             const int j = e * 64 + lane;
@@ -616,20 +618,59 @@ __device__ bool large_solve(const int K, const int E, LargeLds &L, const CostVie
                 // find_dense over positions [lo, K): classify each position
                 // against the running minimum of the positions before it
                 n_ready = lo;
+                // the next chunk's key is read while this chunk is classified
+                auto chunk_key = [&](int base) {
+                    const int p = base + lane;
+                    const float dv = L.d[L.cols[min(p, K - 1)]];
+                    return p < K ? fkey(dv) : kKeyNone;
+                };
                 int carry = kKeyNone;
                 int n_ev = 0;
+                int last_rec = -1;  // index in ev of the last new minimum
+                int dk_next = chunk_key(lo);
+#pragma unroll 1
                 for (int base = lo; base < K; base += 64) {
                     const int p = base + lane;
-                    const int dk = p < K ? fkey(L.d[L.cols[p]]) : kKeyNone;
+                    const int dk = dk_next;
+                    dk_next = chunk_key(base + 64);
                     const int incl = wave_prefix_min_key(dk);
                     const int before = min(carry, wave_shift_up_key(incl));
                     const bool later = p > lo && p < K;
                     const uint64_t rec = ballot(later && dk < before);
                     const uint64_t tie = ballot(later && dk == before);
-                    n_ev = append_events(L, n_ev, rec | tie, base, 0x80000000u, rec);
+                    const uint64_t evm = rec | tie;
+                    if (rec) {
+                        const int lr = last_lane(rec);
+                        const uint64_t upto = lr == 63 ? ~0ull : ((2ull << lr) - 1);
+                        last_rec = n_ev + __builtin_popcountll(evm & upto) - 1;
+                    }
+                    n_ev = append_events(L, n_ev, evm, base, 0x80000000u, rec);
                     carry = min(carry, readlane_i(incl, 63));
                 }
                 lds_sync();
+                if (lo == 0) {
+                    // First search of the path: cols[] is still the identity,
+                    // so without replaying the swaps the tied block is, in
+                    // order, the column of the last new minimum (column 0 if
+                    // none) followed by the ties recorded after it.  If one of
+                    // them is unassigned the path ends here and cols[] is
+                    // never read again (the next path resets it).
+                    const int c_lo = last_rec >= 0 ? (L.ev[last_rec] & 0x7fffffff) : 0;
+                    int found = -1;
+                    for (int top = n_ev; top > last_rec + 1 && found < 0; top -= 64) {
+                        const int k = top - 64 + lane;
+                        const bool ok = k > last_rec && k < top && L.y[L.ev[max(k, 0)]] < 0;
+                        const uint64_t open = ballot(ok);
+                        if (open)
+                            found = L.ev[top - 64 + last_lane(open)];
+                    }
+                    if (found < 0 && L.y[c_lo] < 0)
+                        found = c_lo;
+                    if (found >= 0) {
+                        final_j = found;
+                        break;
+                    }
+                }
                 hi = replay_find_events(L, n_ev, lo);
                 // the LAST unassigned column of the tied block wins
                 int last = -1;
@@ -652,11 +693,10 @@ __device__ bool large_solve(const int K, const int E, LargeLds &L, const CostVie
                 const int jq = L.cols[q];
                 const int iq = L.y[jq];
                 const float level = L.d[jq];
-                const float hq = C.at(iq, jq) - L.v[jq] - level;
                 int n_ev = 0;
                 const int base0 = shi;
-                // gather row iq at the columns of positions [shi, K), all
-                // loads in flight together
+                // gather row iq at column jq and at the columns of positions
+                // [shi, K), all loads in flight together
                 int jg[kMaxChunks];
                 float cg[kMaxChunks];
 #pragma unroll
@@ -664,11 +704,14 @@ __device__ bool large_solve(const int K, const int E, LargeLds &L, const CostVie
                     const int p = base0 + e * 64 + lane;
                     jg[e] = p < K ? L.cols[p] : 0;
                 }
+                float cq = 0.f;
                 if (iq < C.N) {
                     const float *srow = C.src + (int64_t)iq * C.M;
+                    cq = srow[min(jq, C.M - 1)];
 #pragma unroll
                     for (int e = 0; e < kMaxChunks; ++e)
                         cg[e] = srow[min(jg[e], C.M - 1)];
+                    cq = fix_cost(C, cq, jq);
 #pragma unroll
                     for (int e = 0; e < kMaxChunks; ++e)
                         cg[e] = fix_cost(C, cg[e], jg[e]);
@@ -677,6 +720,7 @@ __device__ bool large_solve(const int K, const int E, LargeLds &L, const CostVie
                     for (int e = 0; e < kMaxChunks; ++e)
                         cg[e] = 0.f;
                 }
+                const float hq = cq - L.v[jq] - level;
 #pragma unroll
                 for (int e = 0; e < kMaxChunks; ++e) {
                     const int base = base0 + e * 64;
