@@ -64,6 +64,11 @@ def test_schemas_match_reference():
         "transport::unbalanced_sinkhorn(Tensor cost, float eps, SymInt n_iter, float rho, "
         "Tensor a, Tensor b, Tensor? mask=None, float? scaling=None) -> Tensor"
     )
+    assert str(torch.ops.transport.sinkhorn_divergence.default._schema) == (
+        "transport::sinkhorn_divergence(Tensor cost, float eps, SymInt n_iter, Tensor a, "
+        "Tensor b, Tensor? mask=None, float? scaling=None, Tensor? cost_aa=None, "
+        "Tensor? cost_bb=None) -> Tensor"
+    )
 
 
 def test_no_host_fallback():
@@ -91,3 +96,6 @@ def test_fake_kernels():
             c, 0.1, 3, 1.0, torch.empty(5, 7), torch.empty(5, 9)
         )
         assert plan.shape == (5, 7, 9)
+        div = torch.ops.transport.sinkhorn_divergence(c, 0.1, 3, torch.empty(5, 7),
+                                                      torch.empty(5, 9))
+        assert div.shape == (5,)

@@ -4,8 +4,10 @@ Python surface mirrored from the reference:
 
 * :func:`log_sinkhorn_plan`  -- ``transport/matrix/_log_sinkhorn.py:136-221``
 * :func:`unbalanced_sinkhorn_plan` -- ``transport/matrix/_unbalanced_sinkhorn.py:30-103``
-* ops ``transport::log_sinkhorn`` (``_log_sinkhorn.py:224-266``) and
-  ``transport::unbalanced_sinkhorn`` (``_unbalanced_sinkhorn.py:106-153``),
+* :func:`sinkhorn_divergence` -- ``transport/matrix/_sinkhorn_divergence.py:56-128``
+* ops ``transport::log_sinkhorn`` (``_log_sinkhorn.py:224-266``),
+  ``transport::unbalanced_sinkhorn`` (``_unbalanced_sinkhorn.py:106-153``) and
+  ``transport::sinkhorn_divergence`` (``_sinkhorn_divergence.py:131-173``),
   same schemas (inferred from the same Python signatures), same fakes.
 
 The iteration itself runs in the gfx950 kernels of ``csrc/sinkhorn.hip`` via
@@ -113,6 +115,61 @@ def unbalanced_sinkhorn_plan(  # noqa: PLR0913
     return log_plan.to(cost.dtype)
 
 
+def _potentials(cost, a, b, eps, n_iter, scaling):
+    """(f, g) of ``log_sinkhorn_plan(..., return_potentials=True)`` without
+    writing the plan (the divergence reads only the potentials)."""
+    schedule = build_eps_schedule(cost=cost, reg=eps, n_iter=n_iter, scaling=scaling)
+    b_size, rows, cols = cost.shape
+    if b_size == 0:
+        return cost.new_empty(b_size, rows), cost.new_empty(b_size, cols)
+    _require_device(cost, a, b, "sinkhorn_divergence")
+    _, log_u, log_v = _run(cost, a, b, schedule, 0.0, write_plan=False)
+    final_eps = schedule[-1]
+    return (-final_eps * log_u).to(cost.dtype), (-final_eps * log_v).to(cost.dtype)
+
+
+def _expand_self_cost(c_self, ref: torch.Tensor, b: int, k: int) -> torch.Tensor:
+    """``c_self`` broadcast to (b, k, k), or zeros (``_sinkhorn_divergence.py:44-53``)."""
+    if c_self is None:
+        return torch.zeros(b, k, k, device=ref.device, dtype=ref.dtype)
+    c_self = c_self.to(device=ref.device, dtype=ref.dtype)
+    if c_self.ndim == 2:
+        c_self = c_self.unsqueeze(0)
+    return c_self.expand(b, -1, -1)
+
+
+def sinkhorn_divergence(  # noqa: PLR0913
+    cost: torch.Tensor,
+    *,
+    eps: float,
+    n_iter: int,
+    a: torch.Tensor,
+    b: torch.Tensor,
+    scaling: float | None = None,
+    cost_aa: torch.Tensor | None = None,
+    cost_bb: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """``S_eps(a, b) = OT(a, b) - OT(a, a)/2 - OT(b, b)/2``, each OT the dual
+    value ``<a, f> + <b, g>`` of a converged kernel run (B,).
+
+    With ``f = -eps * log_u`` the dual inner product is minus the OT cost, so
+    the combination is negated, as ``_sinkhorn_divergence.py:125-128`` does.
+    Missing self-costs are zero matrices (the entropic-bias-only variant).
+    """
+    batch = cost.size(0)
+    n = a.size(-1)
+    m = b.size(-1)
+
+    def ot(c, p, q):
+        f, g = _potentials(c, p, q, eps, n_iter, scaling)
+        return (p * f).sum(dim=-1) + (q * g).sum(dim=-1)
+
+    ot_ab = ot(cost, a, b)
+    ot_aa = ot(_expand_self_cost(cost_aa, cost, batch, n), a, a)
+    ot_bb = ot(_expand_self_cost(cost_bb, cost, batch, m), b, b)
+    return -(ot_ab - 0.5 * ot_aa - 0.5 * ot_bb)
+
+
 # ---- op registrations ------------------------------------------------------------
 
 
@@ -192,6 +249,47 @@ def _unbalanced_sinkhorn_fake(  # noqa: PLR0913
     return cost.new_empty(cost.size(0), cost.size(1), cost.size(2))
 
 
+def _sinkhorn_divergence_impl(  # noqa: PLR0913
+    cost: torch.Tensor,
+    eps: float,
+    n_iter: int,
+    a: torch.Tensor,
+    b: torch.Tensor,
+    mask: torch.Tensor | None = None,
+    scaling: float | None = None,
+    cost_aa: torch.Tensor | None = None,
+    cost_bb: torch.Tensor | None = None,
+) -> torch.Tensor:
+    validate_cost(cost)
+    if cost.ndim != 3:
+        msg = (
+            "torch.ops.transport.sinkhorn_divergence: cost.ndim must be 3, "
+            f"got {cost.ndim}"
+        )
+        raise ValueError(msg)
+    cost = fuse_mask_into_cost(cost, mask)
+    return sinkhorn_divergence(
+        cost, eps=eps, n_iter=n_iter, a=a, b=b, scaling=scaling,
+        cost_aa=cost_aa, cost_bb=cost_bb,
+    )
+
+
+def _sinkhorn_divergence_fake(  # noqa: PLR0913
+    cost: torch.Tensor,
+    eps: float,
+    n_iter: int,
+    a: torch.Tensor,
+    b: torch.Tensor,
+    mask: torch.Tensor | None = None,
+    scaling: float | None = None,
+    cost_aa: torch.Tensor | None = None,
+    cost_bb: torch.Tensor | None = None,
+) -> torch.Tensor:
+    del eps, n_iter, a, b, mask, scaling, cost_aa, cost_bb
+    torch._check(cost.dim() == 3, lambda: "cost must be 3D (B, N, M)")
+    return cost.new_empty(cost.size(0))
+
+
 def _register(name: str, impl, fake) -> None:
     qualname = f"transport::{name}"
     if _has_op("transport", name):
@@ -206,3 +304,4 @@ def _register(name: str, impl, fake) -> None:
 
 _register("log_sinkhorn", _log_sinkhorn_impl, _log_sinkhorn_fake)
 _register("unbalanced_sinkhorn", _unbalanced_sinkhorn_impl, _unbalanced_sinkhorn_fake)
+_register("sinkhorn_divergence", _sinkhorn_divergence_impl, _sinkhorn_divergence_fake)

@@ -1,8 +1,9 @@
 """``solve`` for the cost-matrix face (mirrors ``transport/matrix/_solve.py:98-264``).
 
-``LOG_SINKHORN`` (and ``AUTO``) and ``UNBALANCED_SINKHORN`` run the gfx950
-kernel on device tensors.  ``SINKHORN_DIVERGENCE`` and ``EXACT_EMD`` are
-reference backends outside this package and raise ``NotImplementedError``.
+``LOG_SINKHORN`` (and ``AUTO``), ``UNBALANCED_SINKHORN`` and
+``SINKHORN_DIVERGENCE`` run the gfx950 kernel on device tensors.
+``EXACT_EMD`` is a reference backend outside this package and raises
+``NotImplementedError``.
 """
 
 from __future__ import annotations
@@ -13,6 +14,7 @@ import torch
 
 from torchmatch_amd.transport.matrix._sinkhorn import (
     log_sinkhorn_plan,
+    sinkhorn_divergence,
     unbalanced_sinkhorn_plan,
 )
 from torchmatch_amd.transport.matrix._validate import (
@@ -66,8 +68,7 @@ def solve(  # noqa: PLR0913, PLR0911
     """Log transport plan of ``cost`` (or ``(log_plan, f, g)`` with ``unpack``)."""
     backend = _coerce_backend(backend)
     validate_cost(cost)
-    if backend in (Backend.SINKHORN_DIVERGENCE, Backend.EXACT_EMD):
-        del cost_aa, cost_bb
+    if backend == Backend.EXACT_EMD:
         msg = f"torchmatch_amd.transport.matrix.solve: backend {backend.value!r} is not provided"
         raise NotImplementedError(msg)
 
@@ -82,6 +83,14 @@ def solve(  # noqa: PLR0913, PLR0911
         if isinstance(x, tuple):
             return tuple(t.squeeze(0) for t in x) if squeeze_batch else x
         return x.squeeze(0) if squeeze_batch else x
+
+    if backend == Backend.SINKHORN_DIVERGENCE:
+        # self-costs are used as given (2-D ones broadcast over the batch)
+        result = sinkhorn_divergence(
+            cost, eps=reg, n_iter=n_iter, a=a_, b=b_, scaling=scaling,
+            cost_aa=cost_aa, cost_bb=cost_bb,
+        )
+        return result.squeeze(0) if squeeze_batch else result
 
     if backend in (Backend.AUTO, Backend.LOG_SINKHORN):
         res = log_sinkhorn_plan(

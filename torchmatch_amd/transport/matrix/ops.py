@@ -8,6 +8,7 @@ import torch
 import torchmatch_amd.transport.matrix._sinkhorn  # noqa: F401  (registers the ops)
 
 log_sinkhorn = torch.ops.transport.log_sinkhorn
+sinkhorn_divergence = torch.ops.transport.sinkhorn_divergence
 unbalanced_sinkhorn = torch.ops.transport.unbalanced_sinkhorn
 
-__all__ = ["log_sinkhorn", "unbalanced_sinkhorn"]
+__all__ = ["log_sinkhorn", "sinkhorn_divergence", "unbalanced_sinkhorn"]
