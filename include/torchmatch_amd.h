@@ -16,6 +16,10 @@
  *                           (compute_inf_sentinel, rewrite_inf_to_sentinel);
  *                           results follow the CPU op
  *                           assignment/cpu/ops.cpp:176-289 bit for bit.
+ *   tm_jv_unpack_i64        the unpack loop of solve_batch_unpacked,
+ *                           assignment/cpu/ops.cpp:291-417 (the device side of
+ *                           assignment::jonker_dense_batch_unpacked), which
+ *                           assignment/_solve.py:124-164 restates in torch.
  *   tm_sinkhorn_f32         sources/torchmatch/transport/matrix/_log_sinkhorn.py:136-221
  *                           (log_sinkhorn_plan) and
  *                           transport/matrix/_unbalanced_sinkhorn.py:30-103
@@ -83,6 +87,20 @@ int tm_jv_dense_batch_f32(const float *costs, int64_t B, int32_t N, int32_t M, i
  * cuda_common.cuh:241-249).  Returns TM_OK, TM_ERR_NAN, TM_ERR_NEG_INF,
  * TM_ERR_INTERNAL or TM_ERR_HIP. */
 int tm_jv_check_status(const uint32_t *d_status, hipStream_t stream);
+
+/* Unpack B packed mappings (the `out` of tm_jv_dense_batch_f32: row -> column
+ * in [0, M) or -1) into the tuple of assignment::jonker_dense_batch_unpacked:
+ *   matches         device, (B, N, 2) int64: (row, col) of matched rows in row
+ *                   order, -1 after n_matches[b] pairs
+ *   unmatched_rows  device, (B, N) int64: unmatched rows, increasing, then -1
+ *   unmatched_cols  device, (B, M) int64: columns no row took, increasing,
+ *                   then -1
+ *   n_matches       device, (B,) int64
+ * Same contents as the reference CPU op (ops.cpp:387-414, -1 padding as its
+ * at::full(-1) leaves).  M <= 4096. */
+int tm_jv_unpack_i64(const int64_t *packed, int64_t B, int32_t N, int32_t M, int64_t *matches,
+                     int64_t *unmatched_rows, int64_t *unmatched_cols, int64_t *n_matches,
+                     hipStream_t stream);
 
 /* ---- log-domain Sinkhorn (transport::log_sinkhorn / unbalanced_sinkhorn) */
 

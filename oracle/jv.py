@@ -146,3 +146,35 @@ def ref_jv_dense_batch(costs, threads: int = 0) -> np.ndarray:
 
 def default_threads() -> int:
     return len(os.sched_getaffinity(0))
+
+
+def unpack_packed(packed, m: int):
+    """The reference CPU op's unpack of packed (B, N) mappings into
+    (matches (B, N, 2), unmatched_rows (B, N), unmatched_cols (B, M),
+    n_matches (B,)), -1 padded -- a plain-loop restatement of
+    assignment/cpu/ops.cpp:387-414 (solve_batch_unpacked)."""
+    packed = np.asarray(packed, dtype=np.int64)
+    b, n = packed.shape
+    matches = np.full((b, n, 2), -1, dtype=np.int64)
+    ur = np.full((b, n), -1, dtype=np.int64)
+    uc = np.full((b, m), -1, dtype=np.int64)
+    nm = np.zeros(b, dtype=np.int64)
+    for k in range(b):
+        used = [False] * m
+        cnt = nur = 0
+        for i in range(n):
+            j = int(packed[k, i])
+            if 0 <= j < m:
+                matches[k, cnt] = (i, j)
+                cnt += 1
+                used[j] = True
+            else:
+                ur[k, nur] = i
+                nur += 1
+        nm[k] = cnt
+        nuc = 0
+        for j in range(m):
+            if not used[j]:
+                uc[k, nuc] = j
+                nuc += 1
+    return matches, ur, uc, nm

@@ -56,6 +56,10 @@ def test_invalid_arguments_rejected_without_gpu_work():
 def test_schemas_match_reference():
     assert str(torch.ops.assignment.jonker_dense_batch.default._schema) == \
         "assignment::jonker_dense_batch(Tensor costs) -> Tensor"
+    assert str(torch.ops.assignment.jonker_dense_batch_unpacked.default._schema) == (
+        "assignment::jonker_dense_batch_unpacked(Tensor costs) -> "
+        "(Tensor, Tensor, Tensor, Tensor)"
+    )
     assert str(torch.ops.transport.log_sinkhorn.default._schema) == (
         "transport::log_sinkhorn(Tensor cost, float eps, SymInt n_iter, Tensor a, Tensor b, "
         "Tensor? mask=None, float? scaling=None) -> Tensor"
@@ -90,6 +94,8 @@ def test_fake_kernels():
         c = torch.empty(5, 7, 9)
         out = torch.ops.assignment.jonker_dense_batch(c)
         assert out.shape == (5, 7) and out.dtype == torch.long
+        shapes = [t.shape for t in torch.ops.assignment.jonker_dense_batch_unpacked(c)]
+        assert shapes == [(5, 7, 2), (5, 7), (5, 9), (5,)]
         plan = torch.ops.transport.log_sinkhorn(c, 0.1, 3, torch.empty(5, 7), torch.empty(5, 9))
         assert plan.shape == (5, 7, 9)
         plan = torch.ops.transport.unbalanced_sinkhorn(

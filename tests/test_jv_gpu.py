@@ -204,6 +204,43 @@ def test_solve_dispatch_and_unpack(device):
     assert torchmatch_amd.assignment.resolve_backend(cost.to(device)) == "jonker_dense_batch"
 
 
+@pytest.mark.parametrize(("b", "n", "m", "p_inf"), [
+    (64, 64, 64, 0.0), (32, 40, 64, 0.5), (16, 64, 30, 0.3), (8, 500, 768, 0.2),
+    (4, 1, 1, 0.0), (3, 1000, 900, 0.9),
+])
+def test_unpacked_op_matches_cpu_format(b, n, m, p_inf, device):
+    """assignment::jonker_dense_batch_unpacked on device: all four tensors equal
+    the reference CPU op's (ops.cpp:291-417, restated in oracle.jv.unpack_packed)
+    for the oracle's mapping of the same costs."""
+    cost = workloads.jv_rect_masked(B=b, N=n, M=m, p_inf=p_inf, seed=n + m)
+    print(f"unpacked {(b, n, m, p_inf)}", flush=True)
+    want = jv.unpack_packed(jv.jv_dense_batch(cost.numpy()), m)
+    got = torch.ops.assignment.jonker_dense_batch_unpacked(cost.to(device))
+    for g, w in zip(got, want):
+        np.testing.assert_array_equal(g.cpu().numpy(), w)
+    via_solve = torchmatch_amd.assignment.solve(cost.to(device), unpack=True)
+    for g, w in zip(via_solve, want):
+        np.testing.assert_array_equal(g.cpu().numpy(), w)
+
+
+def test_unpack_c_abi_direct(device):
+    lib = _native.lib()
+    packed = torch.tensor([[2, -1, 0], [-1, -1, -1], [0, 1, 2]], dtype=torch.int64,
+                          device=device)
+    outs = [torch.empty(3, 3, 2, dtype=torch.int64, device=device),
+            torch.empty(3, 3, dtype=torch.int64, device=device),
+            torch.empty(3, 4, dtype=torch.int64, device=device),
+            torch.empty(3, dtype=torch.int64, device=device)]
+    rc = lib.tm_jv_unpack_i64(packed.data_ptr(), 3, 3, 4, *[t.data_ptr() for t in outs],
+                              torch.cuda.current_stream().cuda_stream)
+    assert rc == _native.TM_OK
+    torch.cuda.synchronize()
+    for g, w in zip(outs, jv.unpack_packed(packed.cpu().numpy(), 4)):
+        np.testing.assert_array_equal(g.cpu().numpy(), w)
+    assert lib.tm_jv_unpack_i64(packed.data_ptr(), 3, 3, 5000, *[t.data_ptr() for t in outs],
+                                None) == _native.TM_ERR_UNSUPPORTED_SHAPE
+
+
 _GUARD_SCRIPT = textwrap.dedent(
     """
     import sys

@@ -155,6 +155,36 @@ def test_bench_relaxation_count():
     assert (counts[:, 0] >= 64 * 64).all()
 
 
+def test_unpack_restatement_known_cases():
+    """Hand-worked unpacks (ops.cpp:387-414): row order of matches, increasing
+    unmatched rows / columns, -1 padding."""
+    packed = np.array([[2, -1, 0], [-1, -1, -1], [0, 1, 2]])
+    matches, ur, uc, nm = jv.unpack_packed(packed, 4)
+    np.testing.assert_array_equal(nm, [2, 0, 3])
+    np.testing.assert_array_equal(matches[0], [[0, 2], [2, 0], [-1, -1]])
+    np.testing.assert_array_equal(ur[0], [1, -1, -1])
+    np.testing.assert_array_equal(uc[0], [1, 3, -1, -1])
+    np.testing.assert_array_equal(matches[1], [[-1, -1]] * 3)
+    np.testing.assert_array_equal(ur[1], [0, 1, 2])
+    np.testing.assert_array_equal(uc[1], [0, 1, 2, 3])
+    np.testing.assert_array_equal(matches[2], [[0, 0], [1, 1], [2, 2]])
+    np.testing.assert_array_equal(uc[2], [3, -1, -1, -1])
+
+
+def test_unpack_restatement_invariants():
+    """On real solves: every row is matched or unmatched exactly once, every
+    column used at most once, and n_matches counts the non-negative entries."""
+    c = workloads.jv_rect_masked(B=4, N=30, M=45, p_inf=0.6, seed=3).numpy()
+    packed = jv.jv_dense_batch(c)
+    matches, ur, uc, nm = jv.unpack_packed(packed, c.shape[2])
+    for k in range(c.shape[0]):
+        rows = set(matches[k, : nm[k], 0]) | set(ur[k, : 30 - nm[k]])
+        assert rows == set(range(30))
+        cols = list(matches[k, : nm[k], 1]) + list(uc[k, : 45 - nm[k]])
+        assert sorted(cols) == list(range(45))
+        assert nm[k] == (packed[k] >= 0).sum()
+
+
 def test_torch_input_roundtrip():
     c = torch.rand(4, 6, 6, generator=torch.Generator().manual_seed(0))
     assert jv.jv_dense_batch(c.numpy()).shape == (4, 6)

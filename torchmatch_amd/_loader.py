@@ -22,6 +22,9 @@ OPS_SO = _PKG / "_C.so"
 CABI_SO = _PKG / "lib" / "libtorchmatch_amd.so"
 
 JONKER_DENSE_BATCH_SCHEMA = "jonker_dense_batch(Tensor costs) -> Tensor"
+JONKER_DENSE_BATCH_UNPACKED_SCHEMA = (
+    "jonker_dense_batch_unpacked(Tensor costs) -> (Tensor, Tensor, Tensor, Tensor)"
+)
 
 _state: dict[str, object] = {"loaded": False, "libs": []}
 
@@ -39,16 +42,30 @@ def _has_op(namespace: str, name: str) -> bool:
 
 
 def _ensure_assignment_schema() -> None:
-    if _has_op("assignment", "jonker_dense_batch"):
-        return
-    lib = torch.library.Library("assignment", "FRAGMENT")  # noqa: TOR901
-    lib.define(JONKER_DENSE_BATCH_SCHEMA)
-    _state["libs"].append(lib)  # keep the registration alive
+    if not _has_op("assignment", "jonker_dense_batch"):
+        lib = torch.library.Library("assignment", "FRAGMENT")  # noqa: TOR901
+        lib.define(JONKER_DENSE_BATCH_SCHEMA)
+        _state["libs"].append(lib)  # keep the registration alive
 
-    @torch.library.register_fake("assignment::jonker_dense_batch", lib=lib)
-    def _fake(costs: torch.Tensor) -> torch.Tensor:
-        torch._check(costs.dim() == 3, lambda: "costs must be 3D (B, N, M)")
-        return costs.new_empty(costs.size(0), costs.size(1), dtype=torch.long)
+        @torch.library.register_fake("assignment::jonker_dense_batch", lib=lib)
+        def _fake(costs: torch.Tensor) -> torch.Tensor:
+            torch._check(costs.dim() == 3, lambda: "costs must be 3D (B, N, M)")
+            return costs.new_empty(costs.size(0), costs.size(1), dtype=torch.long)
+
+    if not _has_op("assignment", "jonker_dense_batch_unpacked"):
+        lib = torch.library.Library("assignment", "FRAGMENT")  # noqa: TOR901
+        lib.define(JONKER_DENSE_BATCH_UNPACKED_SCHEMA)
+        _state["libs"].append(lib)
+
+        # same shapes as the reference fake, assignment/_loader.py:172-189
+        @torch.library.register_fake("assignment::jonker_dense_batch_unpacked", lib=lib)
+        def _fake_unpacked(costs: torch.Tensor):
+            torch._check(costs.dim() == 3, lambda: "costs must be 3D (B, N, M)")
+            b, n, m = costs.shape
+            return (costs.new_empty(b, n, 2, dtype=torch.long),
+                    costs.new_empty(b, n, dtype=torch.long),
+                    costs.new_empty(b, m, dtype=torch.long),
+                    costs.new_empty(b, dtype=torch.long))
 
 
 def load() -> None:

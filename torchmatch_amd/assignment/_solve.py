@@ -124,6 +124,10 @@ def _dispatch_jonker(cost: torch.Tensor, *, unpack: bool):
             f"max(N, M) <= {jv_max_k()}, got shape {tuple(cost.shape)}"
         )
         raise ValueError(msg)
+    if unpack and not squeeze:
+        # the device unpack, as the reference's native-unpack path
+        # (assignment/_solve.py:207-209) returns the CPU op's tuple
+        return torch.ops.assignment.jonker_dense_batch_unpacked(batch.contiguous())
     packed = torch.ops.assignment.jonker_dense_batch(batch.contiguous())
     if squeeze:
         packed = packed[0]

@@ -106,6 +106,31 @@ at::Tensor jonker_dense_batch_hip(const at::Tensor &costs) {
     return out;
 }
 
+// CUDA-key kernel of assignment::jonker_dense_batch_unpacked: the solve above,
+// then the device unpack (tm_jv_unpack_i64) into the tuple the reference CPU op
+// returns (assignment/cpu/ops.cpp:291-417, registered at :504).
+std::tuple<at::Tensor, at::Tensor, at::Tensor, at::Tensor>
+jonker_dense_batch_unpacked_hip(const at::Tensor &costs) {
+    const at::Tensor packed = jonker_dense_batch_hip(costs);
+    const c10::DeviceGuard guard(costs.device());
+    const int64_t B = costs.size(0), N = costs.size(1), M = costs.size(2);
+    const auto lopts = costs.options().dtype(at::kLong);
+    auto matches = at::empty({B, N, 2}, lopts);
+    auto ur = at::empty({B, N}, lopts);
+    auto uc = at::empty({B, M}, lopts);
+    auto nm = at::zeros({B}, lopts);
+    if (B == 0 || N == 0 || M == 0) {
+        // the CPU op's empty-shape return (ops.cpp:310-316)
+        return {matches, ur, uc, nm};
+    }
+    const int rc = tm_jv_unpack_i64(packed.data_ptr<int64_t>(), B, (int32_t)N, (int32_t)M,
+                                    matches.data_ptr<int64_t>(), ur.data_ptr<int64_t>(),
+                                    uc.data_ptr<int64_t>(), nm.data_ptr<int64_t>(),
+                                    current_stream(costs));
+    check_rc(rc, "jonker_dense_batch_unpacked");
+    return {matches, ur, uc, nm};
+}
+
 // torchmatch_amd::sinkhorn -- device Sinkhorn over a precomputed epsilon
 // schedule.  Returns (log_plan, log_u, log_v); log_plan is empty when
 // write_plan is false.
@@ -147,6 +172,7 @@ sinkhorn_hip(const at::Tensor &cost, const at::Tensor &a, const at::Tensor &b,
 
 TORCH_LIBRARY_IMPL(assignment, CUDA, m) {
     m.impl("jonker_dense_batch", &jonker_dense_batch_hip);
+    m.impl("jonker_dense_batch_unpacked", &jonker_dense_batch_unpacked_hip);
 }
 
 TORCH_LIBRARY(torchmatch_amd, m) {
