@@ -20,8 +20,16 @@
  *                           assignment/cpu/ops.cpp:291-417 (the device side of
  *                           assignment::jonker_dense_batch_unpacked), which
  *                           assignment/_solve.py:124-164 restates in torch.
- *   tm_sinkhorn_f32         sources/torchmatch/transport/matrix/_log_sinkhorn.py:136-221
- *                           (log_sinkhorn_plan) and
+ *   tm_sinkhorn_prepare_f32 transport/matrix/_validate.py:58-63,108-110,149-156
+ *                           (validate_cost's NaN / -inf checks, the marginal
+ *                           sign checks, fuse_mask_into_cost),
+ *                           transport/matrix/_schedule.py:68-69 (largest
+ *                           finite cost) and _log_sinkhorn.py:36-46
+ *                           (_inf_row_col_masks), fused into one pass.
+ *   tm_sinkhorn_read_stats  the host readbacks (`.any()`, `.item()`) of
+ *                           those checks, one synchronisation for all.
+ *   tm_sinkhorn_iterate_f32 sources/torchmatch/transport/matrix/_log_sinkhorn.py:136-221
+ *   tm_sinkhorn_f32         (log_sinkhorn_plan) and
  *                           transport/matrix/_unbalanced_sinkhorn.py:30-103
  *                           (unbalanced_sinkhorn_plan).
  */
@@ -104,20 +112,62 @@ int tm_jv_unpack_i64(const int64_t *packed, int64_t B, int32_t N, int32_t M, int
 
 /* ---- log-domain Sinkhorn (transport::log_sinkhorn / unbalanced_sinkhorn) */
 
-/* Device workspace tm_sinkhorn_f32 needs. */
+/* Flag bits tm_sinkhorn_read_stats reports. */
+enum {
+    TM_SK_FLAG_NAN = 1u,          /* the cost holds NaN (before the mask) */
+    TM_SK_FLAG_NEG_INF = 2u,      /* the cost holds -inf (before the mask) */
+    TM_SK_FLAG_A_NEG = 4u,        /* a holds a negative entry */
+    TM_SK_FLAG_B_NEG = 8u,        /* b holds a negative entry */
+    TM_SK_FLAG_ANY_FINITE = 16u   /* the masked cost holds a finite entry */
+};
+
+/* Device workspace the Sinkhorn calls below need. */
 size_t tm_sinkhorn_workspace_bytes(int64_t B, int64_t N, int64_t M);
 
-/* Run the log-domain Sinkhorn iteration of the reference on a (B, N, M)
- * float32 cost and write the log transport plan.
- *   cost       device (B, N, M); +inf = forbidden pair; no NaN / -inf
- *   a, b       device marginals (B, N) and (B, M), non-negative
+/* First half of a solve: one pass over the (B, N, M) float32 cost and the
+ * marginals, all on `stream`, no host synchronisation.
+ *   cost       device (B, N, M); +inf = forbidden pair
+ *   keep       device (B, N, M) bytes or NULL: pairs with keep == 0 are
+ *              forbidden (the cost is read as +inf there), i.e. the
+ *              reference's fuse_mask_into_cost (transport/matrix/
+ *              _validate.py:149-156) without materialising the fused cost
+ *   a, b       device marginals (B, N) and (B, M)
+ *   k_eps      > 0: also write the log kernel -C/k_eps into the workspace
+ *              (pass the same value to tm_sinkhorn_iterate_f32); 0: do not
+ * The pass also records what the reference's validation and schedule read
+ * from the cost (transport/matrix/_validate.py:58-63, 108-110 and
+ * _schedule.py:68-69): NaN / -inf in the cost, negative marginal entries and
+ * the largest finite (masked) cost.  tm_sinkhorn_read_stats fetches them. */
+int tm_sinkhorn_prepare_f32(const float *cost, const uint8_t *keep, const float *a,
+                            const float *b, int64_t B, int64_t N, int64_t M, float k_eps,
+                            void *workspace, size_t workspace_bytes, hipStream_t stream);
+
+/* Copy the statistics of the last tm_sinkhorn_prepare_f32 on `workspace` to
+ * the host and synchronise `stream` (the only host sync of a solve).
+ * *flags receives TM_SK_FLAG_* bits, *max_finite the largest finite masked
+ * cost (-inf when TM_SK_FLAG_ANY_FINITE is clear). */
+int tm_sinkhorn_read_stats(const void *workspace, int64_t B, int64_t N, int64_t M,
+                           uint32_t *flags, float *max_finite, hipStream_t stream);
+
+/* Second half: the log-domain Sinkhorn iteration of the reference over the
+ * workspace tm_sinkhorn_prepare_f32 filled (same cost, keep, B, N, M), and
+ * the log transport plan.
  *   eps_sched  HOST array of n_iter float64 epsilons (the reference schedule)
  *   rho        <= 0: balanced (log_sinkhorn); > 0: unbalanced with KL
  *              penalty rho (damping 1 / (1 + eps / rho) per step)
+ *   k_eps      the k_eps given to tm_sinkhorn_prepare_f32
  *   log_plan   device (B, N, M) output, may be NULL to skip the plan
  *   log_u, log_v  device (B, N), (B, M) outputs: the final scaling
- *              potentials (f = -eps * log_u, g = -eps * log_v)
- *   workspace  device, >= tm_sinkhorn_workspace_bytes(B, N, M) */
+ *              potentials (f = -eps * log_u, g = -eps * log_v) */
+int tm_sinkhorn_iterate_f32(const float *cost, const uint8_t *keep, int64_t B, int64_t N,
+                            int64_t M, const double *eps_sched, int32_t n_iter, double rho,
+                            float k_eps, float *log_plan, float *log_u, float *log_v,
+                            void *workspace, size_t workspace_bytes, hipStream_t stream);
+
+/* Both halves without a mask and without reading the statistics back: the
+ * cost must hold no NaN / -inf and the marginals must be non-negative.
+ *   a, b       device marginals (B, N) and (B, M)
+ *   other arguments as tm_sinkhorn_iterate_f32 */
 int tm_sinkhorn_f32(const float *cost, const float *a, const float *b, int64_t B, int64_t N,
                     int64_t M, const double *eps_sched, int32_t n_iter, double rho,
                     float *log_plan, float *log_u, float *log_v, void *workspace,

@@ -45,6 +45,28 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "tm_sinkhorn_workspace_bytes": (
         ctypes.c_size_t, [ctypes.c_int64, ctypes.c_int64, ctypes.c_int64]
     ),
+    "tm_sinkhorn_prepare_f32": (
+        ctypes.c_int,
+        [
+            _VP, _VP, _VP, _VP, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64,
+            ctypes.c_float, _VP, ctypes.c_size_t, _VP,
+        ],
+    ),
+    "tm_sinkhorn_read_stats": (
+        ctypes.c_int,
+        [
+            _VP, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64,
+            ctypes.POINTER(ctypes.c_uint32), ctypes.POINTER(ctypes.c_float), _VP,
+        ],
+    ),
+    "tm_sinkhorn_iterate_f32": (
+        ctypes.c_int,
+        [
+            _VP, _VP, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64,
+            ctypes.POINTER(ctypes.c_double), ctypes.c_int32, ctypes.c_double, ctypes.c_float,
+            _VP, _VP, _VP, _VP, ctypes.c_size_t, _VP,
+        ],
+    ),
     "tm_sinkhorn_f32": (
         ctypes.c_int,
         [

@@ -36,6 +36,7 @@
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdint.h>
+#include <string.h>
 
 #include "jv_batch.h"
 #include "wave.h"
@@ -112,7 +113,7 @@ __device__ __forceinline__ float update_potential(float lse, float log_marg, flo
 struct SinkhornLayout {
     int64_t B, N, M;
     int n_chunk, rows_per_chunk, n_strip;
-    size_t off_k, off_logmu, off_lognu, off_infrow, off_infcol, off_colpart, total;
+    size_t off_k, off_logmu, off_lognu, off_infrow, off_infcol, off_colpart, off_stats, total;
 };
 
 __host__ __device__ inline size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
@@ -148,21 +149,49 @@ SinkhornLayout make_layout(int64_t B, int64_t N, int64_t M) {
     L.off_colpart = off;
     if (L.n_chunk > 1)
         off = align_up(off + sizeof(float2) * (size_t)B * L.n_chunk * (size_t)M, 256);
+    L.off_stats = off;
+    off += 256;
     L.total = off;
     return L;
 }
 
-// ---- elementwise preparation ----------------------------------------------------
+// ---- preparation: one pass over the cost ----------------------------------------
 
-// K = -C / e (IEEE division, as torch's `-cost / step_eps` in float32).
+constexpr int kPrepWaves = 4;                                // waves per prepare block
+constexpr int kPrepRowsPerWave = 8;                          // rows a wave keeps in flight
+constexpr int kPrepRows = kPrepWaves * kPrepRowsPerWave;     // rows per block and group
+constexpr uint32_t kFlagNan = TM_SK_FLAG_NAN, kFlagNegInf = TM_SK_FLAG_NEG_INF;
+constexpr uint32_t kFlagANeg = TM_SK_FLAG_A_NEG, kFlagBNeg = TM_SK_FLAG_B_NEG;
+
+// Order-preserving key of a float: f < g  <=>  key(f) < key(g); every float
+// that is not a negative NaN maps above 0, so 0 means "no value".
+__device__ __forceinline__ uint32_t order_key(float f) {
+    const uint32_t u = __float_as_uint(f);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+// K = -C'/e (IEEE division, as torch's `-cost / step_eps` in float32), where
+// C' = C, or with a keep mask C' = keep ? C : +inf (torch's
+// `cost.masked_fill(~mask, inf)`), so masked pairs hold -inf.  Float4 steps
+// when `vec` (C and K 16-byte aligned, keep 4-byte aligned), else scalar.
+template <bool MASK>
 __global__ void __launch_bounds__(kMapBlock)
-sk_log_kernel(const float *__restrict__ C, float *__restrict__ K, int64_t n, float eps) {
+sk_log_kernel(const float *__restrict__ C, const uint8_t *__restrict__ keep,
+              float *__restrict__ K, int64_t n, float eps, int vec) {
     const int64_t stride = (int64_t)gridDim.x * kMapBlock;
-    const int64_t n4 = n / 4;
+    const int64_t n4 = vec ? n / 4 : 0;
     const float4 *c4 = reinterpret_cast<const float4 *>(C);
+    const uint32_t *kp4 = reinterpret_cast<const uint32_t *>(keep);
     float4 *k4 = reinterpret_cast<float4 *>(K);
     for (int64_t k = (int64_t)blockIdx.x * kMapBlock + threadIdx.x; k < n4; k += stride) {
-        const float4 c = c4[k];
+        float4 c = c4[k];
+        if (MASK) {
+            const uint32_t kp = kp4[k];
+            c.x = (kp & 0xffu) ? c.x : f_inf();
+            c.y = (kp & 0xff00u) ? c.y : f_inf();
+            c.z = (kp & 0xff0000u) ? c.z : f_inf();
+            c.w = (kp & 0xff000000u) ? c.w : f_inf();
+        }
         float4 r;
         r.x = -c.x / eps;
         r.y = -c.y / eps;
@@ -171,15 +200,20 @@ sk_log_kernel(const float *__restrict__ C, float *__restrict__ K, int64_t n, flo
         k4[k] = r;
     }
     for (int64_t k = n4 * 4 + (int64_t)blockIdx.x * kMapBlock + threadIdx.x; k < n; k += stride)
-        K[k] = -C[k] / eps;
+        K[k] = -((MASK && keep[k] == 0) ? f_inf() : C[k]) / eps;
 }
 
-// log of the marginals (torch `a.log()`), n elements.
+// log of a marginal (torch `a.log()`), n elements; sets `neg_flag` in
+// stats[0] when an element is negative (the reference's `(a < 0).any()`).
 __global__ void __launch_bounds__(kMapBlock)
-sk_log_marginal(const float *__restrict__ x, float *__restrict__ y, int64_t n) {
+sk_log_marginal(const float *__restrict__ x, float *__restrict__ y, int64_t n,
+                uint32_t *__restrict__ stats, uint32_t neg_flag) {
     const int64_t k = (int64_t)blockIdx.x * kMapBlock + threadIdx.x;
+    const float v = k < n ? x[k] : 0.f;
     if (k < n)
-        y[k] = logf(x[k]);
+        y[k] = logf(v);
+    if (ballot(v < 0.f) != 0 && lane_id() == 0)
+        atomicOr(&stats[0], neg_flag);
 }
 
 __global__ void __launch_bounds__(kMapBlock)
@@ -189,35 +223,151 @@ sk_fill(float *__restrict__ y, int64_t n, float value) {
         y[k] = value;
 }
 
-// inf_row[b, i] = all_j C[b, i, j] == +inf (one wave per row).
-__global__ void __launch_bounds__(256)
-sk_inf_rows(const float *__restrict__ C, uint8_t *__restrict__ inf_row, int64_t rows,
-            int64_t M) {
-    const int64_t r = (int64_t)blockIdx.x * 4 + threadIdx.x / 64;
-    if (r >= rows)
-        return;
-    const float *row = C + r * M;
-    bool all_inf = true;
-    for (int64_t j = lane_id(); j < M; j += 64)
-        all_inf = all_inf && (row[j] == f_inf());
-    const bool any_finite = ballot(!all_inf) != 0;
-    if (lane_id() == 0)
-        inf_row[r] = any_finite ? 0 : 1;
+// Start state of sk_prepare: every row and column flagged all-+inf, stats 0.
+__global__ void __launch_bounds__(kMapBlock)
+sk_reset_flags(uint8_t *__restrict__ inf_row, int64_t n_row, uint8_t *__restrict__ inf_col,
+               int64_t n_col, uint32_t *__restrict__ stats) {
+    const int64_t k = (int64_t)blockIdx.x * kMapBlock + threadIdx.x;
+    if (k < n_row)
+        inf_row[k] = 1;
+    if (k < n_col)
+        inf_col[k] = 1;
+    if (k < 2)
+        stats[k] = 0;
 }
 
-// inf_col[b, j] = all_i C[b, i, j] == +inf (one thread per column; runs once).
-__global__ void __launch_bounds__(kMapBlock)
-sk_inf_cols(const float *__restrict__ C, uint8_t *__restrict__ inf_col, int64_t B, int64_t N,
-            int64_t M) {
-    const int64_t t = (int64_t)blockIdx.x * kMapBlock + threadIdx.x;
-    if (t >= B * M)
+// One pass over the cost C (B, N, M) and the optional keep mask:
+//   K         = -C'/e when e > 0 (as sk_log_kernel), C' = keep ? C : +inf
+//   inf_row   cleared to 0 for each row of C' that holds a value other than
+//             +inf (the reference's `(cost == inf).all(dim=2)`, negated)
+//   inf_col   the same for columns
+//   stats[0] |= kFlagNan / kFlagNegInf for NaN / -inf in C itself (the cost
+//             is validated before the mask is fused into it)
+//   stats[1]  = max(stats[1], order_key(largest finite C'))
+// Block (x, y, z) covers the 64*CW columns from x*64*CW and `groups` groups
+// of kPrepRows rows from y*groups*kPrepRows, of batch z.  Lanes own CW
+// consecutive columns (4 with float4 loads, else 1); wave w reads rows
+// w*8 .. w*8+7 of a group with all eight loads in flight (row indexes clamped
+// to N-1, the surplus rows ignored).  A row flag is one byte store per wave;
+// column flags are OR-ed over the waves in LDS and stored once per block; the
+// stats words see at most one atomic each per block.  Flags are only ever
+// cleared, so stores from different blocks cannot conflict.
+template <bool VEC, bool MASK>
+__global__ void __launch_bounds__(kPrepWaves * 64)
+sk_prepare(const float *__restrict__ C, const uint8_t *__restrict__ keep,
+           float *__restrict__ K, uint8_t *__restrict__ inf_row, uint8_t *__restrict__ inf_col,
+           uint32_t *__restrict__ stats, int64_t N, int64_t M, int groups, float e) {
+    constexpr int CW = VEC ? 4 : 1;
+    __shared__ uint32_t col_any[kPrepWaves][64];
+    __shared__ float blk_max[kPrepWaves];
+    __shared__ uint32_t blk_flags[kPrepWaves];
+    const int lane = lane_id();
+    const int w = (int)(threadIdx.x >> 6);
+    const int64_t b = blockIdx.z;
+    const int64_t c0 = ((int64_t)blockIdx.x * 64 + lane) * CW;
+    const bool col_ok = c0 < M;
+    const int64_t cc = col_ok ? c0 : 0;  // column the loads use
+    const bool write_k = e > 0.f;
+    uint32_t any_col = 0;  // bit q: column c0 + q holds a C' value other than +inf
+    bool nan = false, ninf = false;
+    float vmax = -f_inf();
+    for (int g = 0; g < groups; ++g) {
+        const int64_t r0 =
+            ((int64_t)blockIdx.y * groups + g) * kPrepRows + (int64_t)w * kPrepRowsPerWave;
+        if (r0 >= N)
+            break;
+        float v[kPrepRowsPerWave][CW];
+        uint32_t kp[kPrepRowsPerWave];
+#pragma unroll
+        for (int k = 0; k < kPrepRowsPerWave; ++k) {
+            const int64_t r = r0 + k < N ? r0 + k : N - 1;
+            const int64_t off = (b * N + r) * M + cc;
+            if constexpr (VEC) {
+                const float4 t = *reinterpret_cast<const float4 *>(C + off);
+                v[k][0] = t.x;
+                v[k][1] = t.y;
+                v[k][2] = t.z;
+                v[k][3] = t.w;
+                kp[k] = MASK ? *reinterpret_cast<const uint32_t *>(keep + off) : ~0u;
+            } else {
+                v[k][0] = C[off];
+                kp[k] = MASK ? (uint32_t)keep[off] : ~0u;
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < kPrepRowsPerWave; ++k) {
+            const int64_t r = r0 + k;
+            if (r >= N)
+                break;
+            bool row_any = false;
+            float kv[CW];
+#pragma unroll
+            for (int q = 0; q < CW; ++q) {
+                const float x = col_ok ? v[k][q] : f_inf();
+                nan = nan || x != x;
+                ninf = ninf || x == -f_inf();
+                const bool kept = !MASK || ((kp[k] >> (8 * q)) & 0xffu) != 0;
+                const float y = kept ? x : f_inf();
+                if (y != f_inf()) {
+                    any_col |= 1u << q;
+                    row_any = true;
+                }
+                if (__builtin_isfinite(y))
+                    vmax = fmaxf(vmax, y);
+                kv[q] = -y / e;
+            }
+            if (write_k && col_ok) {
+                const int64_t off = (b * N + r) * M + c0;
+                if constexpr (VEC)
+                    *reinterpret_cast<float4 *>(K + off) = make_float4(kv[0], kv[1], kv[2], kv[3]);
+                else
+                    K[off] = kv[0];
+            }
+            if (ballot(row_any) != 0 && lane == 0)
+                inf_row[b * N + r] = 0;
+        }
+    }
+    const uint32_t fl = (ballot(nan) != 0 ? kFlagNan : 0u) | (ballot(ninf) != 0 ? kFlagNegInf : 0u);
+    const float wm = wave_max(vmax);
+    col_any[w][lane] = any_col;
+    if (lane == 0) {
+        blk_max[w] = wm;
+        blk_flags[w] = fl;
+    }
+    __syncthreads();
+    if (w != 0)
         return;
-    const int64_t b = t / M, j = t % M;
-    const float *col = C + b * N * M + j;
-    bool all_inf = true;
-    for (int64_t i = 0; i < N && all_inf; ++i)
-        all_inf = col[i * M] == f_inf();
-    inf_col[t] = all_inf ? 1 : 0;
+    uint32_t a = 0;
+#pragma unroll
+    for (int k = 0; k < kPrepWaves; ++k)
+        a |= col_any[k][lane];
+    if (col_ok && a != 0) {
+        uint8_t *dst = inf_col + b * M + c0;
+        if (VEC && a == 0xfu) {
+            *reinterpret_cast<uint32_t *>(dst) = 0u;
+        } else {
+#pragma unroll
+            for (int q = 0; q < CW; ++q)
+                if ((a >> q) & 1u)
+                    dst[q] = 0;
+        }
+    }
+    if (lane == 0) {
+        float m = blk_max[0];
+        uint32_t f = blk_flags[0];
+#pragma unroll
+        for (int k = 1; k < kPrepWaves; ++k) {
+            m = fmaxf(m, blk_max[k]);
+            f |= blk_flags[k];
+        }
+        if (f != 0)
+            atomicOr(&stats[0], f);
+        if (m > -f_inf()) {
+            const uint32_t key = order_key(m);
+            if (key > __hip_atomic_load(&stats[1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
+                atomicMax(&stats[1], key);
+        }
+    }
 }
 
 // ---- row sweep: log_u -------------------------------------------------------------
@@ -517,16 +667,17 @@ sk_col_merge(const float2 *__restrict__ colpart, const float *__restrict__ log_n
 
 // ---- final plan -------------------------------------------------------------------
 
-// log_plan[b,i,j] = (log_u[b,i] + (-C[b,i,j] / e)) + log_v[b,j]; M % 4 == 0 path
-// with float4 rows, generic path otherwise.
+// log_plan[b,i,j] = (log_u[b,i] + K[b,i,j]) + log_v[b,j], K holding -C'/e_final
+// from the last step (the reference's `(log_u + (-cost / eps)) + log_v`, the
+// same float32 division); float4 rows when M % 4 == 0, generic otherwise.
 __global__ void __launch_bounds__(kMapBlock)
-sk_plan4(const float *__restrict__ C, const float *__restrict__ log_u,
+sk_plan4(const float *__restrict__ K, const float *__restrict__ log_u,
          const float *__restrict__ log_v, float *__restrict__ plan, int64_t B, int64_t N,
-         int64_t M, float eps) {
+         int64_t M) {
     const int64_t m4 = M / 4;
     const int64_t n4 = B * N * m4;
     const int64_t stride = (int64_t)gridDim.x * kMapBlock;
-    const float4 *c4 = reinterpret_cast<const float4 *>(C);
+    const float4 *k4 = reinterpret_cast<const float4 *>(K);
     float4 *p4 = reinterpret_cast<float4 *>(plan);
     for (int64_t k = (int64_t)blockIdx.x * kMapBlock + threadIdx.x; k < n4; k += stride) {
         const int64_t row = k / m4;
@@ -534,27 +685,27 @@ sk_plan4(const float *__restrict__ C, const float *__restrict__ log_u,
         const int64_t b = row / N;
         const float u = log_u[row];
         const float4 v = reinterpret_cast<const float4 *>(log_v + b * M)[q];
-        const float4 c = c4[k];
+        const float4 c = k4[k];
         float4 o;
-        o.x = (u + (-c.x / eps)) + v.x;
-        o.y = (u + (-c.y / eps)) + v.y;
-        o.z = (u + (-c.z / eps)) + v.z;
-        o.w = (u + (-c.w / eps)) + v.w;
+        o.x = (u + c.x) + v.x;
+        o.y = (u + c.y) + v.y;
+        o.z = (u + c.z) + v.z;
+        o.w = (u + c.w) + v.w;
         p4[k] = o;
     }
 }
 
 __global__ void __launch_bounds__(kMapBlock)
-sk_plan(const float *__restrict__ C, const float *__restrict__ log_u,
+sk_plan(const float *__restrict__ K, const float *__restrict__ log_u,
         const float *__restrict__ log_v, float *__restrict__ plan, int64_t B, int64_t N,
-        int64_t M, float eps) {
+        int64_t M) {
     const int64_t n = B * N * M;
     const int64_t stride = (int64_t)gridDim.x * kMapBlock;
     for (int64_t k = (int64_t)blockIdx.x * kMapBlock + threadIdx.x; k < n; k += stride) {
         const int64_t row = k / M;
         const int64_t j = k - row * M;
         const int64_t b = row / N;
-        plan[k] = (log_u[row] + (-C[k] / eps)) + log_v[b * M + j];
+        plan[k] = (log_u[row] + K[k]) + log_v[b * M + j];
     }
 }
 
@@ -576,21 +727,150 @@ extern "C" size_t tm_sinkhorn_workspace_bytes(int64_t B, int64_t N, int64_t M) {
     return make_layout(B, N, M).total;
 }
 
-extern "C" int tm_sinkhorn_f32(const float *cost, const float *a, const float *b, int64_t B,
-                               int64_t N, int64_t M, const double *eps_sched, int32_t n_iter,
-                               double rho, float *log_plan, float *log_u, float *log_v,
-                               void *workspace, size_t workspace_bytes, hipStream_t stream) {
-    if (B < 0 || N < 0 || M < 0 || n_iter < 1 || eps_sched == nullptr)
+namespace {
+
+#define TM_LAUNCH(...)                                                                    \
+    do {                                                                                  \
+        hipLaunchKernelGGL(__VA_ARGS__);                                                  \
+        if (hipGetLastError() != hipSuccess)                                              \
+            return TM_ERR_LAUNCH;                                                         \
+    } while (0)
+
+// Shape limits of the launch grids below.
+bool shape_supported(const SinkhornLayout &L) {
+    return L.n_strip <= 0x7fffffff && L.n_chunk <= 65535 && L.B <= 65535 &&
+           L.B * L.N <= 0x7fffffff;
+}
+
+int launch_log_kernel(const float *cost, const uint8_t *keep, float *K, int64_t nK, float e,
+                      hipStream_t stream) {
+    const int vec = ((uintptr_t)cost % 16) == 0 && ((uintptr_t)K % 16) == 0 &&
+                    ((uintptr_t)keep % 4) == 0;
+    const dim3 grid(grid_for(nK / 4 + 1, kMapBlock, 8192));
+    if (keep != nullptr)
+        TM_LAUNCH(sk_log_kernel<true>, grid, dim3(kMapBlock), 0, stream, cost, keep, K, nK, e,
+                  vec);
+    else
+        TM_LAUNCH(sk_log_kernel<false>, grid, dim3(kMapBlock), 0, stream, cost, keep, K, nK, e,
+                  vec);
+    return TM_OK;
+}
+
+} // namespace
+
+extern "C" int tm_sinkhorn_prepare_f32(const float *cost, const uint8_t *keep, const float *a,
+                                       const float *b, int64_t B, int64_t N, int64_t M,
+                                       float k_eps, void *workspace, size_t workspace_bytes,
+                                       hipStream_t stream) {
+    if (B < 0 || N < 0 || M < 0 || !(k_eps >= 0.f))
+        return TM_ERR_INVALID_ARGUMENT;
+    if (B == 0 || N == 0 || M == 0)
+        return TM_OK;
+    if (cost == nullptr || a == nullptr || b == nullptr)
+        return TM_ERR_INVALID_ARGUMENT;
+    const SinkhornLayout L = make_layout(B, N, M);
+    if (workspace == nullptr || workspace_bytes < L.total)
+        return TM_ERR_WORKSPACE;
+    // prepare grid: y = row blocks of kPrepRows * groups rows (<= 65535)
+    const int64_t row_groups = (N + kPrepRows - 1) / kPrepRows;
+    const int64_t groups = (row_groups + 65534) / 65535;
+    if (!shape_supported(L) || groups > 0x7fffffff)
+        return TM_ERR_UNSUPPORTED_SHAPE;
+    char *ws = static_cast<char *>(workspace);
+    float *K = reinterpret_cast<float *>(ws + L.off_k);
+    float *log_mu = reinterpret_cast<float *>(ws + L.off_logmu);
+    float *log_nu = reinterpret_cast<float *>(ws + L.off_lognu);
+    uint8_t *inf_row = reinterpret_cast<uint8_t *>(ws + L.off_infrow);
+    uint8_t *inf_col = reinterpret_cast<uint8_t *>(ws + L.off_infcol);
+    uint32_t *stats = reinterpret_cast<uint32_t *>(ws + L.off_stats);
+
+    const int64_t n_flags = B * N > B * M ? B * N : B * M;
+    TM_LAUNCH(sk_reset_flags, dim3(grid_for(n_flags, kMapBlock, 1 << 30)), dim3(kMapBlock), 0,
+              stream, inf_row, B * N, inf_col, B * M, stats);
+    TM_LAUNCH(sk_log_marginal, dim3(grid_for(B * N, kMapBlock, 1 << 30)), dim3(kMapBlock), 0,
+              stream, a, log_mu, B * N, stats, kFlagANeg);
+    TM_LAUNCH(sk_log_marginal, dim3(grid_for(B * M, kMapBlock, 1 << 30)), dim3(kMapBlock), 0,
+              stream, b, log_nu, B * M, stats, kFlagBNeg);
+
+    const bool vec = (M % 4) == 0 && ((uintptr_t)cost % 16) == 0 && ((uintptr_t)keep % 4) == 0;
+    const int cw = vec ? 4 : 1;
+    const dim3 grid((unsigned)((M + 64 * cw - 1) / (64 * cw)),
+                    (unsigned)((row_groups + groups - 1) / groups), (unsigned)B);
+    const dim3 block(kPrepWaves * 64);
+    const int g = (int)groups;
+    if (vec && keep != nullptr)
+        TM_LAUNCH((sk_prepare<true, true>), grid, block, 0, stream, cost, keep, K, inf_row,
+                  inf_col, stats, N, M, g, k_eps);
+    else if (vec)
+        TM_LAUNCH((sk_prepare<true, false>), grid, block, 0, stream, cost, keep, K, inf_row,
+                  inf_col, stats, N, M, g, k_eps);
+    else if (keep != nullptr)
+        TM_LAUNCH((sk_prepare<false, true>), grid, block, 0, stream, cost, keep, K, inf_row,
+                  inf_col, stats, N, M, g, k_eps);
+    else
+        TM_LAUNCH((sk_prepare<false, false>), grid, block, 0, stream, cost, keep, K, inf_row,
+                  inf_col, stats, N, M, g, k_eps);
+    return TM_OK;
+}
+
+extern "C" int tm_sinkhorn_read_stats(const void *workspace, int64_t B, int64_t N, int64_t M,
+                                      uint32_t *flags, float *max_finite, hipStream_t stream) {
+    if (flags == nullptr || max_finite == nullptr || B < 0 || N < 0 || M < 0)
+        return TM_ERR_INVALID_ARGUMENT;
+    *flags = 0;
+    *max_finite = -INFINITY;
+    if (B == 0 || N == 0 || M == 0)
+        return TM_OK;
+    if (workspace == nullptr)
+        return TM_ERR_INVALID_ARGUMENT;
+    const SinkhornLayout L = make_layout(B, N, M);
+    uint32_t words[2] = {0, 0};
+    if (hipMemcpyAsync(words, static_cast<const char *>(workspace) + L.off_stats, sizeof(words),
+                       hipMemcpyDeviceToHost, stream) != hipSuccess)
+        return TM_ERR_HIP;
+    if (hipStreamSynchronize(stream) != hipSuccess)
+        return TM_ERR_HIP;
+    *flags = words[0];
+    if (words[1] != 0) {
+        const uint32_t k = words[1];
+        const uint32_t u = (k & 0x80000000u) ? (k & 0x7fffffffu) : ~k;
+        float f;
+        memcpy(&f, &u, sizeof(f));
+        *max_finite = f;
+        *flags |= TM_SK_FLAG_ANY_FINITE;
+    }
+    return TM_OK;
+}
+
+extern "C" int tm_sinkhorn_iterate_f32(const float *cost, const uint8_t *keep, int64_t B,
+                                       int64_t N, int64_t M, const double *eps_sched,
+                                       int32_t n_iter, double rho, float k_eps, float *log_plan,
+                                       float *log_u, float *log_v, void *workspace,
+                                       size_t workspace_bytes, hipStream_t stream) {
+    if (B < 0 || N < 0 || M < 0 || n_iter < 1 || eps_sched == nullptr || !(k_eps >= 0.f))
         return TM_ERR_INVALID_ARGUMENT;
     for (int32_t s = 0; s < n_iter; ++s)
         if (!(eps_sched[s] > 0.0))
             return TM_ERR_INVALID_ARGUMENT;
-    if (B == 0 || N == 0 || M == 0)
+    if (B == 0)
         return TM_OK;
+    if (N == 0 || M == 0) {
+        // no pair: every row and column is "all +inf", the potentials keep
+        // their start value 0 (log_plan is empty)
+        if (N > 0 && log_u != nullptr)
+            TM_LAUNCH(sk_fill, dim3(grid_for(B * N, kMapBlock, 1 << 30)), dim3(kMapBlock), 0,
+                      stream, log_u, B * N, 0.f);
+        if (M > 0 && log_v != nullptr)
+            TM_LAUNCH(sk_fill, dim3(grid_for(B * M, kMapBlock, 1 << 30)), dim3(kMapBlock), 0,
+                      stream, log_v, B * M, 0.f);
+        return TM_OK;
+    }
+    if (cost == nullptr || log_u == nullptr || log_v == nullptr)
+        return TM_ERR_INVALID_ARGUMENT;
     const SinkhornLayout L = make_layout(B, N, M);
     if (workspace == nullptr || workspace_bytes < L.total)
         return TM_ERR_WORKSPACE;
-    if (L.n_strip > 0x7fffffff || L.n_chunk > 65535 || B > 65535 || B * N > 0x7fffffff)
+    if (!shape_supported(L))
         return TM_ERR_UNSUPPORTED_SHAPE;
     char *ws = static_cast<char *>(workspace);
     float *K = reinterpret_cast<float *>(ws + L.off_k);
@@ -601,38 +881,24 @@ extern "C" int tm_sinkhorn_f32(const float *cost, const float *a, const float *b
     float2 *colpart = reinterpret_cast<float2 *>(ws + L.off_colpart);
     const bool unbalanced = rho > 0.0;
     const int64_t nK = B * N * M;
-    const bool vec = (M % 4) == 0 && ((uintptr_t)cost % 16) == 0 && ((uintptr_t)log_v % 16) == 0;
+    const bool vec = (M % 4) == 0 && ((uintptr_t)log_v % 16) == 0;
 
-#define TM_LAUNCH(...)                                                                    \
-    do {                                                                                  \
-        hipLaunchKernelGGL(__VA_ARGS__);                                                  \
-        if (hipGetLastError() != hipSuccess)                                              \
-            return TM_ERR_LAUNCH;                                                         \
-    } while (0)
-
-    TM_LAUNCH(sk_log_marginal, dim3(grid_for(B * N, kMapBlock, 1 << 30)), dim3(kMapBlock), 0,
-              stream, a, log_mu, B * N);
-    TM_LAUNCH(sk_log_marginal, dim3(grid_for(B * M, kMapBlock, 1 << 30)), dim3(kMapBlock), 0,
-              stream, b, log_nu, B * M);
     TM_LAUNCH(sk_fill, dim3(grid_for(B * N, kMapBlock, 1 << 30)), dim3(kMapBlock), 0, stream,
               log_u, B * N, 0.f);
     TM_LAUNCH(sk_fill, dim3(grid_for(B * M, kMapBlock, 1 << 30)), dim3(kMapBlock), 0, stream,
               log_v, B * M, 0.f);
-    TM_LAUNCH(sk_inf_rows, dim3(grid_for(B * N, 4, 1 << 30)), dim3(256), 0, stream, cost,
-              inf_row, B * N, M);
-    TM_LAUNCH(sk_inf_cols, dim3(grid_for(B * M, kMapBlock, 1 << 30)), dim3(kMapBlock), 0,
-              stream, cost, inf_col, B, N, M);
 
-    const int map_grid = grid_for(nK / 4 + 1, kMapBlock, 8192);
     const int64_t waves_per_batch = (N + kRowsPerWave - 1) / kRowsPerWave;
     const int64_t row_waves = B * waves_per_batch;
     const dim3 row_grid((unsigned)((row_waves + kRowWaves - 1) / kRowWaves));
     const dim3 col_grid((unsigned)L.n_strip, (unsigned)L.n_chunk, (unsigned)B);
-    float cur_eps = -1.f;
+    float cur_eps = k_eps > 0.f ? k_eps : -1.f;  // the epsilon K currently holds
     for (int32_t s = 0; s < n_iter; ++s) {
         const float e = (float)eps_sched[s];
         if (e != cur_eps) {
-            TM_LAUNCH(sk_log_kernel, dim3(map_grid), dim3(kMapBlock), 0, stream, cost, K, nK, e);
+            const int rc = launch_log_kernel(cost, keep, K, nK, e, stream);
+            if (rc != TM_OK)
+                return rc;
             cur_eps = e;
         }
         const float damp = unbalanced ? (float)(1.0 / (1.0 + eps_sched[s] / rho)) : 1.f;
@@ -672,14 +938,32 @@ extern "C" int tm_sinkhorn_f32(const float *cost, const float *a, const float *b
                       unbalanced ? 1 : 0);
     }
     if (log_plan != nullptr) {
-        const float ef = (float)eps_sched[n_iter - 1];
         if (vec && ((uintptr_t)log_plan % 16) == 0)
             TM_LAUNCH(sk_plan4, dim3(grid_for(nK / 4, kMapBlock, 8192)), dim3(kMapBlock), 0,
-                      stream, cost, log_u, log_v, log_plan, B, N, M, ef);
+                      stream, K, log_u, log_v, log_plan, B, N, M);
         else
             TM_LAUNCH(sk_plan, dim3(grid_for(nK, kMapBlock, 8192)), dim3(kMapBlock), 0, stream,
-                      cost, log_u, log_v, log_plan, B, N, M, ef);
+                      K, log_u, log_v, log_plan, B, N, M);
     }
-#undef TM_LAUNCH
     return TM_OK;
+}
+
+#undef TM_LAUNCH
+
+extern "C" int tm_sinkhorn_f32(const float *cost, const float *a, const float *b, int64_t B,
+                               int64_t N, int64_t M, const double *eps_sched, int32_t n_iter,
+                               double rho, float *log_plan, float *log_u, float *log_v,
+                               void *workspace, size_t workspace_bytes, hipStream_t stream) {
+    if (B < 0 || N < 0 || M < 0 || n_iter < 1 || eps_sched == nullptr)
+        return TM_ERR_INVALID_ARGUMENT;
+    for (int32_t s = 0; s < n_iter; ++s)
+        if (!(eps_sched[s] > 0.0))
+            return TM_ERR_INVALID_ARGUMENT;
+    const float k_eps = (float)eps_sched[0];
+    const int rc = tm_sinkhorn_prepare_f32(cost, nullptr, a, b, B, N, M, k_eps, workspace,
+                                           workspace_bytes, stream);
+    if (rc != TM_OK)
+        return rc;
+    return tm_sinkhorn_iterate_f32(cost, nullptr, B, N, M, eps_sched, n_iter, rho, k_eps,
+                                   log_plan, log_u, log_v, workspace, workspace_bytes, stream);
 }

@@ -7,9 +7,10 @@
 // the device kernel exactly where the reference's CUDA extension adds its own
 // (assignment/cuda/dispatch.cu:181-186).
 //
-// The private `torchmatch_amd::sinkhorn` op is what the Python custom ops
-// `transport::log_sinkhorn` / `transport::unbalanced_sinkhorn` call for
-// device tensors.
+// The private `torchmatch_amd::sinkhorn_prepare` / `sinkhorn_iterate` ops are
+// what the Python custom ops `transport::log_sinkhorn`,
+// `transport::unbalanced_sinkhorn` and `transport::sinkhorn_divergence` call
+// for device tensors.
 #include <ATen/ATen.h>
 #include <c10/core/DeviceGuard.h>
 #include <c10/hip/HIPStream.h>
@@ -131,40 +132,90 @@ jonker_dense_batch_unpacked_hip(const at::Tensor &costs) {
     return {matches, ur, uc, nm};
 }
 
-// torchmatch_amd::sinkhorn -- device Sinkhorn over a precomputed epsilon
-// schedule.  Returns (log_plan, log_u, log_v); log_plan is empty when
-// write_plan is false.
-std::tuple<at::Tensor, at::Tensor, at::Tensor>
-sinkhorn_hip(const at::Tensor &cost, const at::Tensor &a, const at::Tensor &b,
-             at::ArrayRef<double> eps_sched, double rho, bool write_plan) {
+void check_keep(const at::Tensor &cost, const c10::optional<at::Tensor> &keep) {
+    if (!keep.has_value())
+        return;
+    TORCH_CHECK(keep->is_cuda() && keep->device() == cost.device(),
+                "sinkhorn: keep must be on the cost's device");
+    TORCH_CHECK(keep->scalar_type() == at::kBool, "sinkhorn: keep must be a bool tensor");
+    TORCH_CHECK(keep->sizes() == cost.sizes() && keep->is_contiguous(),
+                "sinkhorn: keep must be contiguous with the cost's shape");
+}
+
+const uint8_t *keep_ptr(const c10::optional<at::Tensor> &keep) {
+    return keep.has_value() ? reinterpret_cast<const uint8_t *>(keep->data_ptr<bool>()) : nullptr;
+}
+
+// torchmatch_amd::sinkhorn_prepare -- the one pass over cost, keep mask and
+// marginals that a device Sinkhorn solve starts with.  Returns the workspace
+// (device bytes, handed to sinkhorn_iterate) and, when read_stats, a CPU
+// float64 tensor (flags, largest finite masked cost) read back with one
+// synchronisation; an empty tensor otherwise.
+std::tuple<at::Tensor, at::Tensor>
+sinkhorn_prepare_hip(const at::Tensor &cost, const c10::optional<at::Tensor> &keep,
+                     const at::Tensor &a, const at::Tensor &b, double k_eps, bool read_stats) {
     TORCH_CHECK(cost.is_cuda() && a.is_cuda() && b.is_cuda(),
                 "sinkhorn: cost, a and b must be CUDA tensors");
     TORCH_CHECK(cost.dim() == 3, "sinkhorn: cost must be 3D (B, N, M)");
     TORCH_CHECK(cost.scalar_type() == at::kFloat && a.scalar_type() == at::kFloat &&
                     b.scalar_type() == at::kFloat,
                 "sinkhorn: the gfx950 kernels compute in float32");
+    TORCH_CHECK(cost.is_contiguous() && a.is_contiguous() && b.is_contiguous(),
+                "sinkhorn: cost, a and b must be contiguous");
     const int64_t B = cost.size(0), N = cost.size(1), M = cost.size(2);
     TORCH_CHECK(a.dim() == 2 && a.size(0) == B && a.size(1) == N, "sinkhorn: a must be (B, N)");
     TORCH_CHECK(b.dim() == 2 && b.size(0) == B && b.size(1) == M, "sinkhorn: b must be (B, M)");
-    TORCH_CHECK(!eps_sched.empty(), "sinkhorn: empty epsilon schedule");
+    check_keep(cost, keep);
     const c10::DeviceGuard guard(cost.device());
-    const at::Tensor c = cost.contiguous(), ac = a.contiguous(), bc = b.contiguous();
+    const size_t ws_bytes = tm_sinkhorn_workspace_bytes(B, N, M);
+    auto ws = at::empty({(int64_t)ws_bytes}, cost.options().dtype(at::kByte));
+    const hipStream_t stream = current_stream(cost);
+    if (read_stats)
+        check_not_capturing(stream, "the transport Sinkhorn input check");
+    int rc = tm_sinkhorn_prepare_f32(cost.data_ptr<float>(), keep_ptr(keep), a.data_ptr<float>(),
+                                     b.data_ptr<float>(), B, N, M, (float)k_eps, ws.data_ptr(),
+                                     ws_bytes, stream);
+    check_rc(rc, "sinkhorn_prepare");
+    at::Tensor stats = at::empty({0}, at::TensorOptions().dtype(at::kDouble));
+    if (read_stats) {
+        uint32_t flags = 0;
+        float max_finite = 0.f;
+        rc = tm_sinkhorn_read_stats(ws.data_ptr(), B, N, M, &flags, &max_finite, stream);
+        TORCH_CHECK(rc == TM_OK, "sinkhorn_prepare: reading the statistics back failed: ",
+                    hipGetErrorString(hipGetLastError()));
+        stats = at::empty({2}, at::TensorOptions().dtype(at::kDouble));
+        stats.data_ptr<double>()[0] = (double)flags;
+        stats.data_ptr<double>()[1] = (double)max_finite;
+    }
+    return {ws, stats};
+}
+
+// torchmatch_amd::sinkhorn_iterate -- device Sinkhorn over a precomputed
+// epsilon schedule on a workspace from sinkhorn_prepare (same cost and keep).
+// Returns (log_plan, log_u, log_v); log_plan is empty when write_plan is false.
+std::tuple<at::Tensor, at::Tensor, at::Tensor>
+sinkhorn_iterate_hip(const at::Tensor &cost, const c10::optional<at::Tensor> &keep,
+                     const at::Tensor &ws, at::ArrayRef<double> eps_sched, double rho,
+                     double k_eps, bool write_plan) {
+    TORCH_CHECK(cost.is_cuda() && ws.is_cuda(), "sinkhorn: cost and workspace must be CUDA tensors");
+    TORCH_CHECK(cost.dim() == 3 && cost.scalar_type() == at::kFloat && cost.is_contiguous(),
+                "sinkhorn: cost must be a contiguous float32 (B, N, M) tensor");
+    TORCH_CHECK(!eps_sched.empty(), "sinkhorn: empty epsilon schedule");
+    check_keep(cost, keep);
+    const int64_t B = cost.size(0), N = cost.size(1), M = cost.size(2);
+    const c10::DeviceGuard guard(cost.device());
     auto log_u = at::empty({B, N}, cost.options());
     auto log_v = at::empty({B, M}, cost.options());
     at::Tensor log_plan = write_plan ? at::empty({B, N, M}, cost.options())
                                      : at::empty({0}, cost.options());
     if (B == 0)
         return {log_plan, log_u, log_v};
-    const size_t ws_bytes = tm_sinkhorn_workspace_bytes(B, N, M);
-    auto ws = at::empty({(int64_t)ws_bytes}, cost.options().dtype(at::kByte));
-    const hipStream_t stream = current_stream(cost);
-    const int rc = tm_sinkhorn_f32(c.data_ptr<float>(), ac.data_ptr<float>(),
-                                   bc.data_ptr<float>(), B, N, M, eps_sched.data(),
-                                   (int32_t)eps_sched.size(), rho,
-                                   write_plan ? log_plan.data_ptr<float>() : nullptr,
-                                   log_u.data_ptr<float>(), log_v.data_ptr<float>(),
-                                   ws.data_ptr(), ws_bytes, stream);
-    check_rc(rc, "sinkhorn");
+    const int rc = tm_sinkhorn_iterate_f32(
+        cost.data_ptr<float>(), keep_ptr(keep), B, N, M, eps_sched.data(),
+        (int32_t)eps_sched.size(), rho, (float)k_eps,
+        write_plan ? log_plan.data_ptr<float>() : nullptr, log_u.data_ptr<float>(),
+        log_v.data_ptr<float>(), ws.data_ptr(), (size_t)ws.numel(), current_stream(cost));
+    check_rc(rc, "sinkhorn_iterate");
     return {log_plan, log_u, log_v};
 }
 
@@ -176,8 +227,13 @@ TORCH_LIBRARY_IMPL(assignment, CUDA, m) {
 }
 
 TORCH_LIBRARY(torchmatch_amd, m) {
-    m.def("sinkhorn(Tensor cost, Tensor a, Tensor b, float[] eps_sched, float rho, "
-          "bool write_plan) -> (Tensor, Tensor, Tensor)");
+    m.def("sinkhorn_prepare(Tensor cost, Tensor? keep, Tensor a, Tensor b, float k_eps, "
+          "bool read_stats) -> (Tensor, Tensor)");
+    m.def("sinkhorn_iterate(Tensor cost, Tensor? keep, Tensor ws, float[] eps_sched, "
+          "float rho, float k_eps, bool write_plan) -> (Tensor, Tensor, Tensor)");
 }
 
-TORCH_LIBRARY_IMPL(torchmatch_amd, CUDA, m) { m.impl("sinkhorn", &sinkhorn_hip); }
+TORCH_LIBRARY_IMPL(torchmatch_amd, CUDA, m) {
+    m.impl("sinkhorn_prepare", &sinkhorn_prepare_hip);
+    m.impl("sinkhorn_iterate", &sinkhorn_iterate_hip);
+}

@@ -10,10 +10,17 @@ Python surface mirrored from the reference:
   ``transport::sinkhorn_divergence`` (``_sinkhorn_divergence.py:131-173``),
   same schemas (inferred from the same Python signatures), same fakes.
 
-The iteration itself runs in the gfx950 kernels of ``csrc/sinkhorn.hip`` via
-``torch.ops.torchmatch_amd.sinkhorn``; this module only validates, builds the
-epsilon schedule and shapes the results.  The kernels compute in float32
-(float64 input is solved in float32 and the result cast back).  Device
+The work runs in the gfx950 kernels of ``csrc/sinkhorn.hip`` via two private
+ops: ``torchmatch_amd::sinkhorn_prepare`` (one pass over cost, mask and
+marginals: the log kernel for the first step, the all-+inf row / column
+flags, and what the reference's validation and schedule read from the cost,
+NaN / -inf, negative marginals, the largest finite cost, fetched with one
+host synchronisation) and ``torchmatch_amd::sinkhorn_iterate``.  A mask is
+fused in the kernels (the fused cost is never materialised).  This module
+raises the reference's errors from the returned flags, builds the epsilon
+schedule and shapes the results.  The kernels compute in float32 (float64
+input is validated by torch in float64, solved in float32 and the result
+cast back).  Device
 tensors only: there is no host or torch-eager fallback.  Autograd through the
 kernel is not provided (the reference's ``solve`` differentiates through
 torch eager code instead).
@@ -25,8 +32,15 @@ import torch
 
 from torchmatch_amd._loader import _has_op
 from torchmatch_amd._loader import load as _load
-from torchmatch_amd.transport.matrix._schedule import build_eps_schedule
-from torchmatch_amd.transport.matrix._validate import fuse_mask_into_cost, validate_cost
+from torchmatch_amd.transport.matrix._schedule import build_eps_schedule, schedule_from_max
+from torchmatch_amd.transport.matrix._validate import (
+    FLAG_ANY_FINITE,
+    fuse_mask_into_cost,
+    kernel_keep_mask,
+    raise_for_flags,
+    validate_cost,
+    validate_cost_meta,
+)
 
 _load()
 
@@ -45,19 +59,114 @@ def _require_device(cost: torch.Tensor, a: torch.Tensor, b: torch.Tensor, who: s
         raise NotImplementedError(msg)
 
 
-def _run(
+def _device_checkable(cost: torch.Tensor, a: torch.Tensor, b: torch.Tensor) -> bool:
+    """True when the device pass can run the value checks itself: it reads the
+    float32 cost as given (a float64 cost is checked in float64 by torch)."""
+    return (
+        cost.dtype == torch.float32
+        and cost.device.type == "cuda"
+        and a.device.type == "cuda"
+        and b.device.type == "cuda"
+        and not (cost.requires_grad or a.requires_grad or b.requires_grad)
+    )
+
+
+def _torch_marginal_signs(a: torch.Tensor, b: torch.Tensor) -> None:
+    raise_for_flags(
+        (4 if bool((a < 0).any()) else 0) | (8 if bool((b < 0).any()) else 0),
+        cost=False, marginals=True,
+    )
+
+
+def _device_solve(  # noqa: PLR0913
     cost: torch.Tensor,
     a: torch.Tensor,
     b: torch.Tensor,
-    schedule: list[float],
-    rho: float,
     *,
+    eps: float,
+    n_iter: int,
+    scaling: float | None,
+    rho: float,
+    who: str,
+    mask: torch.Tensor | None = None,
+    check_cost: bool = False,
+    check_marginals: bool = False,
+    before_schedule=None,
     write_plan: bool = True,
-) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+):
+    """One solve: the preparation pass (mask fusion, validation, largest
+    finite cost), the schedule, then the iteration.  Returns
+    ``(schedule, log_plan, log_u, log_v)``; log_plan is None without
+    ``write_plan``.
+
+    The checks raise in the reference's order: cost NaN / -inf
+    (``_validate.py:58-63``), negative marginals (``:108-110``), then
+    ``before_schedule`` (the callers' rho checks), then the schedule's own
+    argument checks (``_schedule.py:45-66``).  On the device path all value
+    checks and the schedule's largest finite cost come from one pass and one
+    host synchronisation; the synchronisation is skipped when nothing needs
+    it (no checks and no epsilon scaling)."""
+    keep = None
+    if mask is not None and _device_checkable(cost, a, b):
+        keep = kernel_keep_mask(cost, mask)
+    device_checks = _device_checkable(cost, a, b) and (mask is None or keep is not None)
+    if not device_checks:
+        if check_cost:
+            validate_cost(cost)
+        if check_marginals:
+            _torch_marginal_signs(a, b)
+        cost = fuse_mask_into_cost(cost, mask)
+        if before_schedule is not None:
+            before_schedule()
+        schedule = build_eps_schedule(cost=cost, reg=eps, n_iter=n_iter, scaling=scaling)
+        b_size, rows, cols = cost.shape
+        if b_size == 0:
+            plan = cost.new_empty(b_size, rows, cols) if write_plan else None
+            return schedule, plan, cost.new_empty(b_size, rows), cost.new_empty(b_size, cols)
+        _require_device(cost, a, b, who)
     c32 = cost.to(torch.float32).contiguous()
     a32 = a.to(torch.float32).contiguous()
     b32 = b.to(torch.float32).contiguous()
-    return torch.ops.torchmatch_amd.sinkhorn(c32, a32, b32, schedule, float(rho), write_plan)
+    if device_checks:
+        # K for the first step is written by the same pass when the schedule
+        # is known before it (no scaling)
+        k_eps = float(eps) if (scaling is None and eps > 0 and n_iter >= 1) else 0.0
+        read = check_cost or check_marginals or scaling is not None
+        ws, stats = torch.ops.torchmatch_amd.sinkhorn_prepare(c32, keep, a32, b32, k_eps, read)
+        max_finite = None
+        if read:
+            flags = int(stats[0].item())
+            raise_for_flags(flags, cost=check_cost, marginals=check_marginals)
+            if flags & FLAG_ANY_FINITE:
+                max_finite = float(stats[1].item())
+        if before_schedule is not None:
+            before_schedule()
+        schedule = schedule_from_max(reg=eps, n_iter=n_iter, scaling=scaling,
+                                     max_finite=max_finite)
+    else:
+        k_eps = float(schedule[0])
+        ws, _ = torch.ops.torchmatch_amd.sinkhorn_prepare(c32, None, a32, b32, k_eps, False)
+    log_plan, log_u, log_v = torch.ops.torchmatch_amd.sinkhorn_iterate(
+        c32, keep, ws, schedule, float(rho), k_eps, write_plan
+    )
+    return schedule, (log_plan if write_plan else None), log_u, log_v
+
+
+def _log_sinkhorn(  # noqa: PLR0913
+    cost, *, eps, n_iter, a, b, scaling=None, return_potentials=False, mask=None,
+    check_cost=False, check_marginals=False,
+):
+    schedule, log_plan, log_u, log_v = _device_solve(
+        cost, a, b, eps=eps, n_iter=n_iter, scaling=scaling, rho=0.0, who="log_sinkhorn",
+        mask=mask, check_cost=check_cost, check_marginals=check_marginals,
+    )
+    log_plan = log_plan.to(cost.dtype)
+    if return_potentials:
+        final_eps = schedule[-1]
+        f = (-final_eps * log_u).to(cost.dtype)
+        g = (-final_eps * log_v).to(cost.dtype)
+        return log_plan, f, g
+    return log_plan
 
 
 def log_sinkhorn_plan(  # noqa: PLR0913
@@ -71,22 +180,35 @@ def log_sinkhorn_plan(  # noqa: PLR0913
     return_potentials: bool = False,
 ):
     """Log plan (B, N, M), or ``(log_plan, f, g)`` with ``f = -eps_final * log_u``."""
-    schedule = build_eps_schedule(cost=cost, reg=eps, n_iter=n_iter, scaling=scaling)
-    b_size, rows, cols = cost.shape
-    if b_size == 0:
-        empty_plan = cost.new_empty(b_size, rows, cols)
-        if return_potentials:
-            return empty_plan, cost.new_empty(b_size, rows), cost.new_empty(b_size, cols)
-        return empty_plan
-    _require_device(cost, a, b, "log_sinkhorn")
-    log_plan, log_u, log_v = _run(cost, a, b, schedule, 0.0)
-    log_plan = log_plan.to(cost.dtype)
-    if return_potentials:
-        final_eps = schedule[-1]
-        f = (-final_eps * log_u).to(cost.dtype)
-        g = (-final_eps * log_v).to(cost.dtype)
-        return log_plan, f, g
-    return log_plan
+    return _log_sinkhorn(cost, eps=eps, n_iter=n_iter, a=a, b=b, scaling=scaling,
+                         return_potentials=return_potentials)
+
+
+def _rho_check(rho: float, msg: str):
+    def check() -> None:
+        if rho <= 0:
+            raise ValueError(msg)
+    return check
+
+
+def _solve_rho_message(rho: float) -> str:
+    return (
+        "torchmatch.transport.matrix.solve: rho must be positive for "
+        f"UNBALANCED_SINKHORN, got {rho}"
+    )
+
+
+def _unbalanced_sinkhorn(  # noqa: PLR0913
+    cost, *, eps, n_iter, rho, a, b, scaling=None, mask=None, check_cost=False,
+    check_marginals=False,
+):
+    _, log_plan, _, _ = _device_solve(
+        cost, a, b, eps=eps, n_iter=n_iter, scaling=scaling, rho=float(rho),
+        who="unbalanced_sinkhorn", mask=mask, check_cost=check_cost,
+        check_marginals=check_marginals,
+        before_schedule=_rho_check(rho, _solve_rho_message(rho)),
+    )
+    return log_plan.to(cost.dtype)
 
 
 def unbalanced_sinkhorn_plan(  # noqa: PLR0913
@@ -101,29 +223,18 @@ def unbalanced_sinkhorn_plan(  # noqa: PLR0913
 ) -> torch.Tensor:
     """Unbalanced (KL-penalised) log plan (B, N, M)."""
     if rho <= 0:
-        msg = (
-            "torchmatch.transport.matrix.solve: rho must be positive for "
-            f"UNBALANCED_SINKHORN, got {rho}"
-        )
-        raise ValueError(msg)
-    schedule = build_eps_schedule(cost=cost, reg=eps, n_iter=n_iter, scaling=scaling)
-    b_size, rows, cols = cost.shape
-    if b_size == 0:
-        return cost.new_empty(b_size, rows, cols)
-    _require_device(cost, a, b, "unbalanced_sinkhorn")
-    log_plan, _, _ = _run(cost, a, b, schedule, float(rho))
-    return log_plan.to(cost.dtype)
+        raise ValueError(_solve_rho_message(rho))
+    return _unbalanced_sinkhorn(cost, eps=eps, n_iter=n_iter, rho=rho, a=a, b=b,
+                                scaling=scaling)
 
 
-def _potentials(cost, a, b, eps, n_iter, scaling):
+def _potentials(cost, a, b, eps, n_iter, scaling, **checks):
     """(f, g) of ``log_sinkhorn_plan(..., return_potentials=True)`` without
     writing the plan (the divergence reads only the potentials)."""
-    schedule = build_eps_schedule(cost=cost, reg=eps, n_iter=n_iter, scaling=scaling)
-    b_size, rows, cols = cost.shape
-    if b_size == 0:
-        return cost.new_empty(b_size, rows), cost.new_empty(b_size, cols)
-    _require_device(cost, a, b, "sinkhorn_divergence")
-    _, log_u, log_v = _run(cost, a, b, schedule, 0.0, write_plan=False)
+    schedule, _, log_u, log_v = _device_solve(
+        cost, a, b, eps=eps, n_iter=n_iter, scaling=scaling, rho=0.0,
+        who="sinkhorn_divergence", write_plan=False, **checks,
+    )
     final_eps = schedule[-1]
     return (-final_eps * log_u).to(cost.dtype), (-final_eps * log_v).to(cost.dtype)
 
@@ -136,6 +247,24 @@ def _expand_self_cost(c_self, ref: torch.Tensor, b: int, k: int) -> torch.Tensor
     if c_self.ndim == 2:
         c_self = c_self.unsqueeze(0)
     return c_self.expand(b, -1, -1)
+
+
+def _sinkhorn_divergence(  # noqa: PLR0913
+    cost, *, eps, n_iter, a, b, scaling=None, cost_aa=None, cost_bb=None, mask=None,
+    check_cost=False, check_marginals=False,
+):
+    batch = cost.size(0)
+    n = a.size(-1)
+    m = b.size(-1)
+
+    def ot(c, p, q, **checks):
+        f, g = _potentials(c, p, q, eps, n_iter, scaling, **checks)
+        return (p * f).sum(dim=-1) + (q * g).sum(dim=-1)
+
+    ot_ab = ot(cost, a, b, mask=mask, check_cost=check_cost, check_marginals=check_marginals)
+    ot_aa = ot(_expand_self_cost(cost_aa, cost, batch, n), a, a)
+    ot_bb = ot(_expand_self_cost(cost_bb, cost, batch, m), b, b)
+    return -(ot_ab - 0.5 * ot_aa - 0.5 * ot_bb)
 
 
 def sinkhorn_divergence(  # noqa: PLR0913
@@ -156,18 +285,18 @@ def sinkhorn_divergence(  # noqa: PLR0913
     the combination is negated, as ``_sinkhorn_divergence.py:125-128`` does.
     Missing self-costs are zero matrices (the entropic-bias-only variant).
     """
-    batch = cost.size(0)
-    n = a.size(-1)
-    m = b.size(-1)
+    return _sinkhorn_divergence(cost, eps=eps, n_iter=n_iter, a=a, b=b, scaling=scaling,
+                                cost_aa=cost_aa, cost_bb=cost_bb)
 
-    def ot(c, p, q):
-        f, g = _potentials(c, p, q, eps, n_iter, scaling)
-        return (p * f).sum(dim=-1) + (q * g).sum(dim=-1)
 
-    ot_ab = ot(cost, a, b)
-    ot_aa = ot(_expand_self_cost(cost_aa, cost, batch, n), a, a)
-    ot_bb = ot(_expand_self_cost(cost_bb, cost, batch, m), b, b)
-    return -(ot_ab - 0.5 * ot_aa - 0.5 * ot_bb)
+def _check_op_cost(cost: torch.Tensor, op: str, hint: str = "") -> None:
+    """``validate_cost`` then ``cost.ndim == 3`` as the ops check them; the
+    value half of validate_cost is left to the device pass for 3-D costs."""
+    if cost.ndim != 3:
+        validate_cost(cost)
+        msg = f"torch.ops.transport.{op}: cost.ndim must be 3, got {cost.ndim}{hint}"
+        raise ValueError(msg)
+    validate_cost_meta(cost)
 
 
 # ---- op registrations ------------------------------------------------------------
@@ -182,16 +311,12 @@ def _log_sinkhorn_impl(  # noqa: PLR0913
     mask: torch.Tensor | None = None,
     scaling: float | None = None,
 ) -> torch.Tensor:
-    validate_cost(cost)
-    if cost.ndim != 3:
-        msg = (
-            "torch.ops.transport.log_sinkhorn: cost.ndim must be 3, got "
-            f"{cost.ndim}. Call torchmatch.transport.matrix.solve(...) for "
-            "2-D ergonomic dispatch."
-        )
-        raise ValueError(msg)
-    cost = fuse_mask_into_cost(cost, mask)
-    return log_sinkhorn_plan(cost, eps=eps, n_iter=n_iter, a=a, b=b, scaling=scaling)
+    _check_op_cost(
+        cost, "log_sinkhorn",
+        ". Call torchmatch.transport.matrix.solve(...) for 2-D ergonomic dispatch.",
+    )
+    return _log_sinkhorn(cost, eps=eps, n_iter=n_iter, a=a, b=b, scaling=scaling, mask=mask,
+                         check_cost=True)
 
 
 def _log_sinkhorn_fake(  # noqa: PLR0913
@@ -218,20 +343,15 @@ def _unbalanced_sinkhorn_impl(  # noqa: PLR0913
     mask: torch.Tensor | None = None,
     scaling: float | None = None,
 ) -> torch.Tensor:
-    validate_cost(cost)
-    if cost.ndim != 3:
-        msg = (
-            "torch.ops.transport.unbalanced_sinkhorn: cost.ndim must be 3, "
-            f"got {cost.ndim}"
-        )
-        raise ValueError(msg)
-    if rho <= 0:
-        msg = "torch.ops.transport.unbalanced_sinkhorn: rho must be positive"
-        raise ValueError(msg)
-    cost = fuse_mask_into_cost(cost, mask)
-    return unbalanced_sinkhorn_plan(
-        cost, eps=eps, n_iter=n_iter, rho=rho, a=a, b=b, scaling=scaling
+    _check_op_cost(cost, "unbalanced_sinkhorn")
+    _, log_plan, _, _ = _device_solve(
+        cost, a, b, eps=eps, n_iter=n_iter, scaling=scaling, rho=float(rho),
+        who="unbalanced_sinkhorn", mask=mask, check_cost=True,
+        before_schedule=_rho_check(
+            rho, "torch.ops.transport.unbalanced_sinkhorn: rho must be positive"
+        ),
     )
+    return log_plan.to(cost.dtype)
 
 
 def _unbalanced_sinkhorn_fake(  # noqa: PLR0913
@@ -260,17 +380,10 @@ def _sinkhorn_divergence_impl(  # noqa: PLR0913
     cost_aa: torch.Tensor | None = None,
     cost_bb: torch.Tensor | None = None,
 ) -> torch.Tensor:
-    validate_cost(cost)
-    if cost.ndim != 3:
-        msg = (
-            "torch.ops.transport.sinkhorn_divergence: cost.ndim must be 3, "
-            f"got {cost.ndim}"
-        )
-        raise ValueError(msg)
-    cost = fuse_mask_into_cost(cost, mask)
-    return sinkhorn_divergence(
-        cost, eps=eps, n_iter=n_iter, a=a, b=b, scaling=scaling,
-        cost_aa=cost_aa, cost_bb=cost_bb,
+    _check_op_cost(cost, "sinkhorn_divergence")
+    return _sinkhorn_divergence(
+        cost, eps=eps, n_iter=n_iter, a=a, b=b, scaling=scaling, cost_aa=cost_aa,
+        cost_bb=cost_bb, mask=mask, check_cost=True,
     )
 
 

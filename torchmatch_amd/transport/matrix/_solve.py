@@ -13,14 +13,15 @@ from enum import Enum
 import torch
 
 from torchmatch_amd.transport.matrix._sinkhorn import (
-    log_sinkhorn_plan,
-    sinkhorn_divergence,
-    unbalanced_sinkhorn_plan,
+    _device_checkable,
+    _log_sinkhorn,
+    _sinkhorn_divergence,
+    _unbalanced_sinkhorn,
 )
 from torchmatch_amd.transport.matrix._validate import (
     coerce_marginals,
-    fuse_mask_into_cost,
     validate_cost,
+    validate_cost_meta,
 )
 
 __all__ = ["Backend", "marginal_error", "solve"]
@@ -67,17 +68,30 @@ def solve(  # noqa: PLR0913, PLR0911
 ):
     """Log transport plan of ``cost`` (or ``(log_plan, f, g)`` with ``unpack``)."""
     backend = _coerce_backend(backend)
-    validate_cost(cost)
+    validate_cost_meta(cost)
     if backend == Backend.EXACT_EMD:
+        validate_cost(cost)
         msg = f"torchmatch_amd.transport.matrix.solve: backend {backend.value!r} is not provided"
         raise NotImplementedError(msg)
 
     squeeze_batch = cost.ndim == 2
-    if squeeze_batch:
-        cost = cost.unsqueeze(0)
-    a_, b_ = coerce_marginals(cost, a, b)
-    mask_to_fuse = mask.unsqueeze(0) if (squeeze_batch and mask is not None) else mask
-    cost = fuse_mask_into_cost(cost, mask_to_fuse)
+    cost3 = cost.unsqueeze(0) if squeeze_batch else cost
+    # the value checks of validate_cost and of the marginals run in the
+    # kernels' preparation pass when it reads the values as given (float32 on
+    # the device); otherwise torch runs them here, in the reference's order
+    try:
+        a_, b_ = coerce_marginals(cost3, a, b, check_sign=False)
+    except ValueError:
+        validate_cost(cost)
+        coerce_marginals(cost3, a, b)
+        raise
+    device_checks = _device_checkable(cost3, a_, b_)
+    if not device_checks:
+        validate_cost(cost)
+        coerce_marginals(cost3, a_, b_)
+    cost = cost3
+    mask_ = mask.unsqueeze(0) if (squeeze_batch and mask is not None) else mask
+    checks = {"mask": mask_, "check_cost": device_checks, "check_marginals": device_checks}
 
     def _out(x):
         if isinstance(x, tuple):
@@ -86,22 +100,22 @@ def solve(  # noqa: PLR0913, PLR0911
 
     if backend == Backend.SINKHORN_DIVERGENCE:
         # self-costs are used as given (2-D ones broadcast over the batch)
-        result = sinkhorn_divergence(
+        result = _sinkhorn_divergence(
             cost, eps=reg, n_iter=n_iter, a=a_, b=b_, scaling=scaling,
-            cost_aa=cost_aa, cost_bb=cost_bb,
+            cost_aa=cost_aa, cost_bb=cost_bb, **checks,
         )
         return result.squeeze(0) if squeeze_batch else result
 
     if backend in (Backend.AUTO, Backend.LOG_SINKHORN):
-        res = log_sinkhorn_plan(
+        res = _log_sinkhorn(
             cost, eps=reg, n_iter=n_iter, a=a_, b=b_, scaling=scaling,
-            return_potentials=unpack,
+            return_potentials=unpack, **checks,
         )
         return _out(res)
 
     # UNBALANCED_SINKHORN
-    log_plan = unbalanced_sinkhorn_plan(
-        cost, eps=reg, n_iter=n_iter, rho=rho, a=a_, b=b_, scaling=scaling
+    log_plan = _unbalanced_sinkhorn(
+        cost, eps=reg, n_iter=n_iter, rho=rho, a=a_, b=b_, scaling=scaling, **checks
     )
     if not unpack:
         return _out(log_plan)
