@@ -16,6 +16,11 @@
  *                           (compute_inf_sentinel, rewrite_inf_to_sentinel);
  *                           results follow the CPU op
  *                           assignment/cpu/ops.cpp:176-289 bit for bit.
+ *   tm_jv_compact_batch_f32 the CPU op assignment::jonker_compact_batch
+ *                           (assignment/cpu/ops.cpp:431-433 with
+ *                           jonker_compact_core.h:20-301), which has no
+ *                           device counterpart in the reference; results
+ *                           follow it bit for bit.
  *   tm_jv_unpack_i64        the unpack loop of solve_batch_unpacked,
  *                           assignment/cpu/ops.cpp:291-417 (the device side of
  *                           assignment::jonker_dense_batch_unpacked), which
@@ -89,6 +94,17 @@ size_t tm_jv_workspace_bytes(int64_t B, int32_t N, int32_t M);
 int tm_jv_dense_batch_f32(const float *costs, int64_t B, int32_t N, int32_t M, int64_t *out,
                           void *workspace, size_t workspace_bytes, uint32_t *d_status,
                           hipStream_t stream);
+
+/* Largest K = max(N, M) tm_jv_compact_batch_f32 accepts. */
+int32_t tm_jv_compact_max_k(void);
+
+/* Solve B problems like tm_jv_dense_batch_f32 (same arguments, workspace,
+ * status words and sentinel / padding rules) with the solver of
+ * assignment::jonker_compact_batch instead: out is identical to that CPU op's
+ * mapping, whose tie rules differ from the dense solver's. */
+int tm_jv_compact_batch_f32(const float *costs, int64_t B, int32_t N, int32_t M, int64_t *out,
+                            void *workspace, size_t workspace_bytes, uint32_t *d_status,
+                            hipStream_t stream);
 
 /* Copy the two status words to the host and synchronise `stream` (the only
  * host sync of the JV path, mirroring the reference's validation readback,

@@ -5,10 +5,11 @@ may import this module.  It loads:
 
 * ``oracle/libjv_oracle.so`` -- the C restatement in ``jv_oracle.c`` of the
   reference's float32 ``jonker_dense_batch`` (ops.cpp:67-93,176-289,
-  jonker_dense_core.cpp:15-60, jonker_dense_flat.h:27-274);
+  jonker_dense_core.cpp:15-60, jonker_dense_flat.h:27-274) and
+  ``jonker_compact_batch`` (ops.cpp:431-433, jonker_compact_core.h:20-301);
 * ``oracle/_ref/libjv_ref.so`` -- the reference's own ``jonker_dense_core.cpp``
-  compiled by ``oracle/Makefile`` (absent where the reference was never
-  checked out and nothing prebuilt travelled along).
+  and ``jonker_compact_core.h`` compiled by ``oracle/Makefile`` (absent where
+  the reference was never checked out and nothing prebuilt travelled along).
 
 Error codes follow ``jv_oracle.c``: 1 = NaN in the input, 2 = -inf.
 """
@@ -57,6 +58,8 @@ def oracle_lib() -> ctypes.CDLL:
         _F32P, ctypes.c_int64, ctypes.c_int32, ctypes.c_int32, _I64P, _I64P,
     ]
     lib.jvo_dense_batch_counted.restype = ctypes.c_int
+    lib.jvo_compact_batch.argtypes = lib.jvo_dense_batch.argtypes
+    lib.jvo_compact_batch.restype = ctypes.c_int
     lib.jvo_sentinel.argtypes = [_F32P, ctypes.c_int64, ctypes.c_int32, _F32P]
     lib.jvo_sentinel.restype = ctypes.c_int
     return lib
@@ -72,6 +75,8 @@ def ref_lib() -> ctypes.CDLL:
         _F32P, ctypes.c_int64, ctypes.c_int32, ctypes.c_int32, _I64P, ctypes.c_int,
     ]
     lib.ref_jv_dense_batch_f32.restype = ctypes.c_int
+    lib.ref_jv_compact_batch_f32.argtypes = lib.ref_jv_dense_batch_f32.argtypes
+    lib.ref_jv_compact_batch_f32.restype = ctypes.c_int
     return lib
 
 
@@ -97,6 +102,18 @@ def jv_dense_batch(costs, threads: int = 0) -> np.ndarray:
     b, n, m = arr.shape
     out = np.empty((b, n), dtype=np.int64)
     rc = oracle_lib().jvo_dense_batch(
+        arr.ctypes.data_as(_F32P), b, n, m, out.ctypes.data_as(_I64P), threads
+    )
+    _raise(rc)
+    return out
+
+
+def jv_compact_batch(costs, threads: int = 0) -> np.ndarray:
+    """Oracle ``jonker_compact_batch``: (B, N, M) float32 -> (B, N) int64."""
+    arr = _prep(costs)
+    b, n, m = arr.shape
+    out = np.empty((b, n), dtype=np.int64)
+    rc = oracle_lib().jvo_compact_batch(
         arr.ctypes.data_as(_F32P), b, n, m, out.ctypes.data_as(_I64P), threads
     )
     _raise(rc)
@@ -138,6 +155,19 @@ def ref_jv_dense_batch(costs, threads: int = 0) -> np.ndarray:
     b, n, m = arr.shape
     out = np.empty((b, n), dtype=np.int64)
     rc = ref_lib().ref_jv_dense_batch_f32(
+        arr.ctypes.data_as(_F32P), b, n, m, out.ctypes.data_as(_I64P), threads
+    )
+    _raise(rc)
+    return out
+
+
+def ref_jv_compact_batch(costs, threads: int = 0) -> np.ndarray:
+    """The reference's compact solver (header compiled from its own source)
+    behind the same batch driver."""
+    arr = _prep(costs)
+    b, n, m = arr.shape
+    out = np.empty((b, n), dtype=np.int64)
+    rc = ref_lib().ref_jv_compact_batch_f32(
         arr.ctypes.data_as(_F32P), b, n, m, out.ctypes.data_as(_I64P), threads
     )
     _raise(rc)

@@ -1,5 +1,6 @@
 /*
- * jv_oracle.c -- CPU restatement of torchmatch's float32 `jonker_dense_batch`.
+ * jv_oracle.c -- CPU restatement of torchmatch's float32 `jonker_dense_batch`
+ * and `jonker_compact_batch`.
  *
  * TEST INFRASTRUCTURE ONLY.  This file is the parity checker for the HIP
  * kernels in torchmatch_amd/csrc; nothing in the product links, loads or
@@ -18,6 +19,10 @@
  *   jonker_dense_flat.h:178-235  carr_dense     -> jvo_row_reduction()
  *   jonker_dense_flat.h:237-258  ca_dense       -> jvo_augment()
  *   jonker_dense_flat.h:260-274  jonker_internal_flat -> jvo_square()
+ *   jonker_compact_core.h:20-43  find_umins_regular -> jvoc_two_min()
+ *   jonker_compact_core.h:51-252 jonker_compact_kernel -> jvoc_square()
+ *   ops.cpp:431-433, jonker_compact_core.h:279-301
+ *                                jonker_compact_batch -> jvo_compact_batch()
  *
  * Every float32 expression keeps the reference's operand order and every
  * comparison keeps its strictness, because the int64 row->col mapping must
@@ -312,6 +317,215 @@ static void jvo_square(uint32_t n, const float *c, jvo_scratch *s, jvo_counts *c
         jvo_augment(n, c, (uint32_t)n_free, s, cnt);
 }
 
+/* ---- jonker_compact_batch: the square JV of jonker_compact_core.h ---------- */
+
+#define JVOC_FLT_MAX 3.402823466e38f /* numeric_limits<float>::max() */
+
+/* find_umins_regular (jonker_compact_core.h:20-43): the smallest reduced
+ * cost of row i and the next one in (value, index) order.  Column 0 seeds
+ * the minimum; the second minimum starts at FLT_MAX, so an entry that is not
+ * below it never becomes j2 (j2 stays -1 when nothing qualifies). */
+static void jvoc_two_min(uint32_t n, const float *row, const float *v, float *u1, float *u2,
+                         int32_t *j1, int32_t *j2) {
+    float lo1 = row[0] - v[0], lo2 = JVOC_FLT_MAX;
+    int32_t a = 0, b = -1;
+    for (uint32_t j = 1; j < n; ++j) {
+        const float h = row[j] - v[j];
+        if (!(h < lo2))
+            continue;
+        if (h >= lo1) {
+            lo2 = h;
+            b = (int32_t)j;
+        } else {
+            lo2 = lo1;
+            b = a;
+            lo1 = h;
+            a = (int32_t)j;
+        }
+    }
+    *u1 = lo1;
+    *u2 = lo2;
+    *j1 = a;
+    *j2 = b;
+}
+
+/* jonker_compact_kernel<int32_t, float> (jonker_compact_core.h:51-252) on a
+ * square n x n tile.  x = rowsol, y = colsol; free_rows doubles as the
+ * per-row claim counter of the column reduction, as in the reference
+ * (:99).  There is no iteration cap in the reference's augmenting row
+ * reduction, and none here. */
+static void jvoc_square(uint32_t n, const float *c, jvo_scratch *s, jvo_counts *cnt) {
+    int32_t *x = s->x, *y = s->y, *fr = s->free_rows, *pred = s->pred, *cols = s->cols;
+    float *v = s->v, *d = s->d;
+    int64_t relax = 0, paths = 0, scans = 0;
+
+    /* column reduction, last column first (:73-96): column minimum, first
+     * row on ties; the first column (in that order) to reach a row keeps it */
+    for (uint32_t i = 0; i < n; ++i)
+        fr[i] = 0;
+    for (int32_t j = (int32_t)n - 1; j >= 0; --j) {
+        float m = c[j];
+        int32_t im = 0;
+        for (uint32_t i = 1; i < n; ++i)
+            if (c[(size_t)i * n + j] < m) {
+                m = c[(size_t)i * n + j];
+                im = (int32_t)i;
+            }
+        v[j] = m;
+        if (++fr[im] == 1) {
+            x[im] = j;
+            y[j] = im;
+        } else {
+            y[j] = -1;
+        }
+    }
+    relax += (int64_t)n * n;
+
+    /* reduction transfer (:98-117): unclaimed rows become free (in row
+     * order); a row claimed exactly once lowers its column's dual by its
+     * smallest other reduced cost.  fr[] is read at i and written at
+     * n_free <= i, so the claim counts are consumed before being overwritten. */
+    uint32_t n_free = 0;
+    for (uint32_t i = 0; i < n; ++i) {
+        const int32_t claims = fr[i];
+        if (claims == 0) {
+            fr[n_free++] = (int32_t)i;
+        } else if (claims == 1) {
+            const float *row = c + (size_t)i * n;
+            const int32_t jx = x[i];
+            float m = JVOC_FLT_MAX;
+            for (uint32_t j = 0; j < n; ++j)
+                if ((int32_t)j != jx && row[j] - v[j] < m)
+                    m = row[j] - v[j];
+            v[jx] = v[jx] - m;
+            relax += n - 1;
+        }
+    }
+
+    /* augmenting row reduction, two rounds (:119-166).  A row whose best
+     * column's dual can be lowered takes that column and its previous owner
+     * is processed next (pushed back at the read position); otherwise it
+     * takes the second-best column and the displaced owner waits for the
+     * next round (appended at n_free, behind the read position). */
+    for (int round = 0; round < 2; ++round) {
+        const uint32_t n_prev = n_free;
+        uint32_t k = 0;
+        n_free = 0;
+        while (k < n_prev) {
+            const int32_t i = fr[k++];
+            float u1, u2;
+            int32_t j1, j2;
+            jvoc_two_min(n, c + (size_t)i * n, v, &u1, &u2, &j1, &j2);
+            relax += n;
+            int32_t i0 = y[j1];
+            const float lowered = v[j1] - (u2 - u1);
+            const int lowers = lowered < v[j1];
+            if (lowers) {
+                v[j1] = lowered;
+            } else if (i0 >= 0) {
+                j1 = j2;
+                i0 = y[j2];
+            }
+            x[i] = j1;
+            y[j1] = i;
+            if (i0 >= 0) {
+                if (lowers)
+                    fr[--k] = i0;
+                else
+                    fr[n_free++] = i0;
+            }
+        }
+    }
+
+    /* augmentation (:168-251): one shortest-path search per free row */
+    for (uint32_t f = 0; f < n_free; ++f) {
+        const int32_t start = fr[f];
+        const float *srow = c + (size_t)start * n;
+        for (uint32_t j = 0; j < n; ++j) {
+            d[j] = srow[j] - v[j];
+            pred[j] = start;
+            cols[j] = (int32_t)j;
+        }
+        relax += n;
+        ++paths;
+        uint32_t low = 0, up = 0;
+        int32_t last = 0, end = -1;
+        float level = 0.0f;
+        while (end < 0) {
+            if (up == low) {
+                /* gather every column at the new minimum into [low, up):
+                 * a smaller d restarts the group at low, an equal one
+                 * joins it (:185-199) */
+                last = (int32_t)low - 1;
+                level = d[cols[up++]];
+                for (uint32_t k = up; k < n; ++k) {
+                    const int32_t j = cols[k];
+                    const float h = d[j];
+                    if (h <= level) {
+                        if (h < level) {
+                            up = low;
+                            level = h;
+                        }
+                        cols[k] = cols[up];
+                        cols[up++] = j;
+                    }
+                }
+                /* the first unassigned column of the group ends the path
+                 * (:200-206) */
+                for (uint32_t k = low; k < up; ++k)
+                    if (y[cols[k]] < 0) {
+                        end = cols[k];
+                        break;
+                    }
+            }
+            if (end >= 0)
+                break;
+            /* scan the row of the next column of the group (:209-233) */
+            const int32_t jq = cols[low++];
+            const int32_t iq = y[jq];
+            const float *row = c + (size_t)iq * n;
+            const float h = row[jq] - v[jq] - level;
+            ++scans;
+            relax += 1 + (int64_t)(n - up);
+            for (uint32_t k = up; k < n; ++k) {
+                const int32_t j = cols[k];
+                const float r = row[j] - v[j] - h;
+                if (!(r < d[j]))
+                    continue;
+                pred[j] = iq;
+                if (r == level) {
+                    if (y[j] < 0) {
+                        end = j;
+                        break;
+                    }
+                    cols[k] = cols[up];
+                    cols[up++] = j;
+                }
+                d[j] = r;
+            }
+        }
+        /* duals of the columns finished before the last group (:236-239) */
+        for (int32_t k = 0; k <= last; ++k) {
+            const int32_t j = cols[k];
+            v[j] = v[j] + d[j] - level;
+        }
+        /* flip the assignment along the predecessors (:241-250) */
+        int32_t i;
+        do {
+            i = pred[end];
+            y[end] = i;
+            const int32_t j = end;
+            end = x[i];
+            x[i] = j;
+        } while (i != start);
+    }
+    if (cnt) {
+        cnt->relax += relax;
+        cnt->paths += paths;
+        cnt->scans += scans;
+    }
+}
+
 /* compute_sentinel<float> (ops.cpp:67-93), one serial pass over all cells. */
 int jvo_sentinel(const float *data, int64_t count, int32_t K, float *out) {
     float mx = -3.402823466e38f; /* numeric_limits<float>::lowest() */
@@ -352,8 +566,10 @@ static void jvo_pad(const float *src, int32_t N, int32_t M, int32_t K, float sen
         }
 }
 
+typedef void (*jvo_solver)(uint32_t, const float *, jvo_scratch *, jvo_counts *);
+
 static int jvo_batch_impl(const float *costs, int64_t B, int32_t N, int32_t M,
-                          int64_t *out, int threads, jvo_counts *counts) {
+                          int64_t *out, int threads, jvo_counts *counts, jvo_solver solve) {
     if (B == 0 || N == 0 || M == 0) {
         for (int64_t k = 0; k < B * (int64_t)N; ++k)
             out[k] = -1;
@@ -385,7 +601,7 @@ static int jvo_batch_impl(const float *costs, int64_t B, int32_t N, int32_t M,
 #endif
             for (int64_t b = 0; b < B; ++b) {
                 jvo_pad(costs + b * (int64_t)N * M, N, M, K, sentinel, tile);
-                jvo_square((uint32_t)K, tile, &s, counts ? &counts[b] : NULL);
+                solve((uint32_t)K, tile, &s, counts ? &counts[b] : NULL);
                 for (int32_t i = 0; i < N; ++i) {
                     const int32_t j = s.x[i];
                     out[b * N + i] = (j >= 0 && j < M) ? j : -1;
@@ -406,7 +622,14 @@ static int jvo_batch_impl(const float *costs, int64_t B, int32_t N, int32_t M,
  * 3 (allocation failure). */
 int jvo_dense_batch(const float *costs, int64_t B, int32_t N, int32_t M, int64_t *out,
                     int threads) {
-    return jvo_batch_impl(costs, B, N, M, out, threads, NULL);
+    return jvo_batch_impl(costs, B, N, M, out, threads, NULL, jvo_square);
+}
+
+/* jonker_compact_batch: the same batch driver (ops.cpp:431-433 runs
+ * solve_batch with the compact solver) around jvoc_square. */
+int jvo_compact_batch(const float *costs, int64_t B, int32_t N, int32_t M, int64_t *out,
+                      int threads) {
+    return jvo_batch_impl(costs, B, N, M, out, threads, NULL, jvoc_square);
 }
 
 /* Same, single-threaded, with per-problem work counters (3 int64 per problem:
@@ -416,7 +639,7 @@ int jvo_dense_batch_counted(const float *costs, int64_t B, int32_t N, int32_t M,
     jvo_counts *cnt = (jvo_counts *)calloc((size_t)(B > 0 ? B : 1), sizeof(jvo_counts));
     if (!cnt)
         return JVO_ERR_ALLOC;
-    const int rc = jvo_batch_impl(costs, B, N, M, out, 1, cnt);
+    const int rc = jvo_batch_impl(costs, B, N, M, out, 1, cnt, jvo_square);
     for (int64_t b = 0; b < B; ++b) {
         counts3[3 * b + 0] = cnt[b].relax;
         counts3[3 * b + 1] = cnt[b].paths;

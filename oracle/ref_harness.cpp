@@ -1,5 +1,6 @@
-// ref_harness.cpp -- C entry point around the reference's own compiled
-// jonker_dense_core.cpp, for building oracle/_ref/libjv_ref.so.
+// ref_harness.cpp -- C entry points around the reference's own compiled
+// jonker_dense_core.cpp and header-only jonker_compact_core.h, for building
+// oracle/_ref/libjv_ref.so.
 //
 // TEST INFRASTRUCTURE ONLY (parity checker / CPU baseline, never shipped).
 // The solve itself is the reference's code, compiled from
@@ -9,6 +10,7 @@
 // padding with +inf -> sentinel and zero padding, parallel loop over the
 // batch, padded columns -> -1).  It has no torch dependency so it loads with
 // ctypes on a box that does not have the reference checked out.
+#include "jonker_compact_core.h"
 #include "jonker_dense_core.h"
 
 #include <cmath>
@@ -44,10 +46,10 @@ int sentinel_of(const float *data, int64_t count, int K, float *out) {
     return 0;
 }
 
-} // namespace
+using SquareSolver = int (*)(const float *, int, int64_t *, int64_t *);
 
-extern "C" int ref_jv_dense_batch_f32(const float *costs, int64_t B, int32_t N,
-                                      int32_t M, int64_t *out, int threads) {
+int batch_driver(const float *costs, int64_t B, int32_t N, int32_t M, int64_t *out,
+                 int threads, SquareSolver solve) {
     if (B == 0 || N == 0 || M == 0) {
         for (int64_t k = 0; k < B * static_cast<int64_t>(N); ++k)
             out[k] = -1;
@@ -81,8 +83,7 @@ extern "C" int ref_jv_dense_batch_f32(const float *costs, int64_t B, int32_t N,
                     }
                     tile[static_cast<size_t>(i) * K + j] = val;
                 }
-            const int src_rc = match_jonker::detail::jonker_dense_solve_square_f32(
-                tile.data(), K, rtc.data(), ctr.data());
+            const int src_rc = solve(tile.data(), K, rtc.data(), ctr.data());
             int64_t *ob = out + b * N;
             for (int i = 0; i < N; ++i) {
                 const int64_t j = src_rc == 0 ? rtc[i] : -1;
@@ -92,4 +93,20 @@ extern "C" int ref_jv_dense_batch_f32(const float *costs, int64_t B, int32_t N,
     }
     (void)threads;
     return 0;
+}
+
+} // namespace
+
+extern "C" int ref_jv_dense_batch_f32(const float *costs, int64_t B, int32_t N,
+                                      int32_t M, int64_t *out, int threads) {
+    return batch_driver(costs, B, N, M, out, threads,
+                        &match_jonker::detail::jonker_dense_solve_square_f32);
+}
+
+// jonker_compact_batch (ops.cpp:431-433): the same driver around the
+// compact square solver (jonker_compact_core.h:279-301).
+extern "C" int ref_jv_compact_batch_f32(const float *costs, int64_t B, int32_t N,
+                                        int32_t M, int64_t *out, int threads) {
+    return batch_driver(costs, B, N, M, out, threads,
+                        &match_jonker::detail::jonker_compact_solve_square_f32);
 }

@@ -1,13 +1,15 @@
-"""Write the JV golden fixtures from the reference's own compiled solver.
+"""Write the JV golden fixtures from the reference's own compiled solvers.
 
 Runs in the build container only (needs oracle/_ref/libjv_ref.so, which
-oracle/Makefile compiles from the reference's jonker_dense_core.cpp):
+oracle/Makefile compiles from the reference's jonker_dense_core.cpp and
+jonker_compact_core.h):
 
     make -C oracle && python tests/golden/make_jv_golden.py
 
 Each fixture stores the workload recipe (generator + seed + shape), the
-sha256 of the float32 input bytes, and the reference int64 row->col mapping
-in the narrowest integer type that holds it.  Tests regenerate the input
+sha256 of the float32 input bytes, and the reference int64 row->col mappings
+of jonker_dense_batch ("mapping") and jonker_compact_batch ("compact") in the
+narrowest integer type that holds them.  Tests regenerate the input
 from the recipe, check the sha256, and compare mappings.
 """
 
@@ -52,9 +54,11 @@ def main() -> None:
     for name, (gen, kw) in CASES.items():
         cost = make_input(name)
         ref = jv.ref_jv_dense_batch(cost.numpy())
+        compact = jv.ref_jv_compact_batch(cost.numpy())
         m = cost.shape[2]
         dtype = np.int8 if m <= 127 else np.int16
-        np.savez_compressed(OUT / f"jv_{name}.npz", mapping=ref.astype(dtype))
+        np.savez_compressed(OUT / f"jv_{name}.npz", mapping=ref.astype(dtype),
+                            compact=compact.astype(dtype))
         index[name] = {
             "generator": gen,
             "kwargs": kw,
@@ -62,8 +66,11 @@ def main() -> None:
             "sha256": workloads.sha256(cost),
             "file": f"jv_{name}.npz",
             "unmatched": int((ref < 0).sum()),
+            "compact_unmatched": int((compact < 0).sum()),
+            "compact_differs": int((compact != ref).any(axis=1).sum()),
         }
-        print(name, cost.shape, "unmatched:", int((ref < 0).sum()))
+        print(name, cost.shape, "unmatched:", int((ref < 0).sum()),
+              "compact differs on", int((compact != ref).any(axis=1).sum()), "problems")
     (OUT / "jv_golden.json").write_text(json.dumps(index, indent=2) + "\n")
 
 

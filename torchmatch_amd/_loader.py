@@ -1,12 +1,13 @@
 """Load the in-tree native extension and make sure the op schemas exist.
 
-``_C.so`` carries the device kernels of ``assignment::jonker_dense_batch``
-(CUDA dispatch key -- ROCm tensors report device type ``"cuda"``) and the
-private ``torchmatch_amd::sinkhorn`` op.  The schema of
-``assignment::jonker_dense_batch`` is owned by whoever defines the
+``_C.so`` carries the device kernels of ``assignment::jonker_dense_batch``,
+``jonker_compact_batch`` and their ``_unpacked`` forms (CUDA dispatch key --
+ROCm tensors report device type ``"cuda"``) and the private
+``torchmatch_amd::sinkhorn_prepare`` / ``sinkhorn_iterate`` ops.  The
+schemas of the ``assignment`` ops are owned by whoever defines the
 ``assignment`` library: the reference CPU extension when it is loaded
-(``assignment/cpu/ops.cpp:486-495``), otherwise this module, with the same
-text and the same fake kernel as ``assignment/_loader.py:160-169``.
+(``assignment/cpu/ops.cpp:486-498``), otherwise this module, with the same
+texts and the same fake kernels as ``assignment/_loader.py:160-189``.
 
 There is no fallback: if the extension is missing, :func:`load` raises.
 """
@@ -21,10 +22,17 @@ _PKG = Path(__file__).resolve().parent
 OPS_SO = _PKG / "_C.so"
 CABI_SO = _PKG / "lib" / "libtorchmatch_amd.so"
 
-JONKER_DENSE_BATCH_SCHEMA = "jonker_dense_batch(Tensor costs) -> Tensor"
-JONKER_DENSE_BATCH_UNPACKED_SCHEMA = (
-    "jonker_dense_batch_unpacked(Tensor costs) -> (Tensor, Tensor, Tensor, Tensor)"
-)
+# schema texts of assignment/cpu/ops.cpp:486-498 for the batched JV ops
+BATCH_ROW_SCHEMAS = {
+    "jonker_dense_batch": "jonker_dense_batch(Tensor costs) -> Tensor",
+    "jonker_compact_batch": "jonker_compact_batch(Tensor costs) -> Tensor",
+}
+BATCH_UNPACKED_SCHEMAS = {
+    "jonker_dense_batch_unpacked":
+        "jonker_dense_batch_unpacked(Tensor costs) -> (Tensor, Tensor, Tensor, Tensor)",
+    "jonker_compact_batch_unpacked":
+        "jonker_compact_batch_unpacked(Tensor costs) -> (Tensor, Tensor, Tensor, Tensor)",
+}
 
 _state: dict[str, object] = {"loaded": False, "libs": []}
 
@@ -41,31 +49,32 @@ def _has_op(namespace: str, name: str) -> bool:
     return True
 
 
+def _row_fake(costs: torch.Tensor) -> torch.Tensor:
+    # assignment/_loader.py:160-169
+    torch._check(costs.dim() == 3, lambda: "costs must be 3D (B, N, M)")
+    return costs.new_empty(costs.size(0), costs.size(1), dtype=torch.long)
+
+
+def _unpacked_fake(costs: torch.Tensor):
+    # same shapes as the reference fake, assignment/_loader.py:172-189
+    torch._check(costs.dim() == 3, lambda: "costs must be 3D (B, N, M)")
+    b, n, m = costs.shape
+    return (costs.new_empty(b, n, 2, dtype=torch.long),
+            costs.new_empty(b, n, dtype=torch.long),
+            costs.new_empty(b, m, dtype=torch.long),
+            costs.new_empty(b, dtype=torch.long))
+
+
 def _ensure_assignment_schema() -> None:
-    if not _has_op("assignment", "jonker_dense_batch"):
-        lib = torch.library.Library("assignment", "FRAGMENT")  # noqa: TOR901
-        lib.define(JONKER_DENSE_BATCH_SCHEMA)
-        _state["libs"].append(lib)  # keep the registration alive
-
-        @torch.library.register_fake("assignment::jonker_dense_batch", lib=lib)
-        def _fake(costs: torch.Tensor) -> torch.Tensor:
-            torch._check(costs.dim() == 3, lambda: "costs must be 3D (B, N, M)")
-            return costs.new_empty(costs.size(0), costs.size(1), dtype=torch.long)
-
-    if not _has_op("assignment", "jonker_dense_batch_unpacked"):
-        lib = torch.library.Library("assignment", "FRAGMENT")  # noqa: TOR901
-        lib.define(JONKER_DENSE_BATCH_UNPACKED_SCHEMA)
-        _state["libs"].append(lib)
-
-        # same shapes as the reference fake, assignment/_loader.py:172-189
-        @torch.library.register_fake("assignment::jonker_dense_batch_unpacked", lib=lib)
-        def _fake_unpacked(costs: torch.Tensor):
-            torch._check(costs.dim() == 3, lambda: "costs must be 3D (B, N, M)")
-            b, n, m = costs.shape
-            return (costs.new_empty(b, n, 2, dtype=torch.long),
-                    costs.new_empty(b, n, dtype=torch.long),
-                    costs.new_empty(b, m, dtype=torch.long),
-                    costs.new_empty(b, dtype=torch.long))
+    for schemas, fake in ((BATCH_ROW_SCHEMAS, _row_fake),
+                          (BATCH_UNPACKED_SCHEMAS, _unpacked_fake)):
+        for name, schema in schemas.items():
+            if _has_op("assignment", name):
+                continue
+            lib = torch.library.Library("assignment", "FRAGMENT")  # noqa: TOR901
+            lib.define(schema)
+            _state["libs"].append(lib)  # keep the registration alive
+            torch.library.register_fake(f"assignment::{name}", fake, lib=lib)
 
 
 def load() -> None:

@@ -37,6 +37,11 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         ctypes.c_int,
         [_VP, ctypes.c_int64, ctypes.c_int32, ctypes.c_int32, _VP, _VP, ctypes.c_size_t, _VP, _VP],
     ),
+    "tm_jv_compact_max_k": (ctypes.c_int32, []),
+    "tm_jv_compact_batch_f32": (
+        ctypes.c_int,
+        [_VP, ctypes.c_int64, ctypes.c_int32, ctypes.c_int32, _VP, _VP, ctypes.c_size_t, _VP, _VP],
+    ),
     "tm_jv_check_status": (ctypes.c_int, [_VP, _VP]),
     "tm_jv_unpack_i64": (
         ctypes.c_int,

@@ -1,9 +1,11 @@
-// jv_batch.hip -- batched Jonker-Volgenant (dense, float32) for gfx950.
+// jv_batch.hip -- batched Jonker-Volgenant (float32) for gfx950.
 //
 // Reproduces the int64 row->col mapping of torchmatch's CPU
-// `assignment::jonker_dense_batch` bit for bit:
+// `assignment::jonker_dense_batch` bit for bit, and, for K <= 64, that of
+// `assignment::jonker_compact_batch` (section 3 below):
 //   sentinel + padding      sources/torchmatch/assignment/cpu/ops.cpp:67-93,176-289
 //   solver                  sources/torchmatch/assignment/cpu/jonker_dense_flat.h:27-274
+//   compact solver          sources/torchmatch/assignment/cpu/jonker_compact_core.h:20-252
 //
 // Launch structure (one stream, no host round trip between kernels):
 //   1. jv_stats_kernel     -- grid-stride pass over all B*N*M cells; each block
@@ -879,6 +881,444 @@ __device__ __forceinline__ bool wave_solve(const int K, WaveLds &L, float v,
     return true;
 }
 
+// ---------------------------------------------------------------------------
+// 3. compact variant (assignment::jonker_compact_batch), K <= 64
+// ---------------------------------------------------------------------------
+// jonker_compact_core.h:51-252 solves the same padded square problem as the
+// dense solver but with its own tie and ordering rules, so its mappings
+// differ on ties.  The code below follows it step by step:
+//   * column reduction from the last column, minima seeded by row 0 (on the
+//     wave path every cost is below LARGE, so the dense path's minima and
+//     claims are the same and are shared);
+//   * reduction transfer with FLT_MAX as the starting minimum;
+//   * augmenting row reduction without an iteration cap (a generous guard
+//     reports a runaway instead of spinning), the second minimum seeded by
+//     FLT_MAX, the displaced owner pushed back at the read position (lowered
+//     dual) or appended to the next round;
+//   * augmentation: the FIRST unassigned column of a new minimum group ends
+//     the path, and the finished columns' duals become (v + d) - min.
+
+constexpr float kFltMax = 3.402823466e38f;  // numeric_limits<float>::max()
+
+// Iteration guard of the compact augmenting row reduction (which has no cap
+// in the reference): far above what any input reaches in practice.
+__device__ __forceinline__ uint32_t compact_arr_guard(int K) {
+    return 64u * (uint32_t)K * (uint32_t)K + 4096u;
+}
+
+// find_umins_regular (jonker_compact_core.h:20-43) on the wave: j1 is the
+// first index of the smallest reduced cost, j2 the next column in (value,
+// index) order, u1 / u2 their values.  Valid when every reduced cost is below
+// FLT_MAX (the wave path's range guarantees it).
+__device__ __forceinline__ TwoMin compact_two_min(float r, bool live) {
+    const int key = live ? fkey(r) : kKeyNone;
+    int k1, k2;
+    wave_min2_key(key, k1, k2);
+    k1 = uniform_i(k1);
+    k2 = uniform_i(k2);
+    const uint64_t at1 = ballot(key == k1);
+    TwoMin t;
+    t.j1 = first_lane(at1);
+    t.u1 = readlane_f(r, t.j1);
+    t.j2 = -1;
+    t.u2 = kFltMax;
+    if (k2 == k1)
+        t.j2 = first_lane(at1 & (at1 - 1));
+    else if (k2 != kKeyNone)
+        t.j2 = first_lane(ballot(key == k2));
+    if (t.j2 >= 0)
+        t.u2 = readlane_f(r, t.j2);
+    return t;
+}
+
+// Wave-parallel jonker_compact_kernel<int32_t, float> on the LDS tile.  Lane j
+// holds column j (v, y), lane i row i (x) and the free list (lane k =
+// free_rows[k]); augmentation keeps the column at position p of the search
+// order in lane p (PosState), as the dense path does.  Returns false when the
+// iteration guard trips.
+__device__ __forceinline__ bool wave_solve_compact(const int K, WaveLds &L, float v, int y,
+                                                   int &x_out) {
+    const int lane = lane_id();
+    const bool live = lane < K;
+
+    // ---- column reduction (:77-96): (v, y) = this column's minimum and first
+    // arg-min row; the largest column claiming a row keeps it
+    if (live) {
+        L.xmax[lane] = -1;
+        L.claims[lane] = 0;
+    }
+    __syncthreads();
+    if (live) {
+        atomicMax(&L.xmax[y], lane);
+        atomicAdd(&L.claims[y], 1);
+    }
+    __syncthreads();
+    int x = live ? L.xmax[lane] : -1;               // lane = row
+    const bool once = live && L.claims[lane] == 1;  // claimed exactly once
+    if (live && L.xmax[y] != lane)
+        y = -1;                                     // lane = column
+    if (!live) {
+        v = finf();
+        y = -1;
+    }
+
+    // ---- reduction transfer (:98-117), rows in increasing order ----
+    int fr = 0;  // lane k holds free_rows[k]
+    int n_free = 0;
+    {
+        uint64_t m = ballot(live && x < 0);
+        while (m) {
+            const int row = first_lane(m);
+            m &= m - 1;
+            if (lane == n_free)
+                fr = row;
+            ++n_free;
+        }
+        const int max_key = fkey(kFltMax);
+        uint64_t t = ballot(once);
+        while (t) {
+            const int i = first_lane(t);
+            t &= t - 1;
+            const int own = readlane_i(x, i);
+            const float r = L.c[i * kTile + lane] - v;
+            const int key = (live && lane != own) ? fkey(r) : kKeyNone;
+            const int kmin = uniform_i(wave_min_key(key));
+            float mn = kFltMax;
+            if (kmin < max_key)
+                mn = readlane_f(r, first_lane(ballot(key == kmin)));
+            if (lane == own)
+                v = v - mn;
+        }
+    }
+
+    // ---- augmenting row reduction (:119-166) ----
+    const uint32_t guard = compact_arr_guard(K);
+    uint32_t steps = 0;
+    for (int round = 0; round < 2; ++round) {
+        const int n_prev = n_free;
+        int k = 0;
+        n_free = 0;
+        while (k < n_prev) {
+            const int i = readlane_i(fr, k++);
+            if (++steps > guard)
+                return false;
+            const float r = L.c[i * kTile + lane] - v;
+            const TwoMin t = compact_two_min(r, live);
+            int j1 = t.j1;
+            int i0 = readlane_i(y, j1);
+            const float vj1 = readlane_f(v, j1);
+            const float lowered = vj1 - (t.u2 - t.u1);
+            const bool lowers = lowered < vj1;
+            if (lowers) {
+                if (lane == j1)
+                    v = lowered;
+            } else if (i0 >= 0) {
+                j1 = t.j2;
+                if (j1 < 0)
+                    return false;  // only reachable outside the wave path's range
+                i0 = readlane_i(y, j1);
+            }
+            if (lane == i)
+                x = j1;
+            if (lane == j1)
+                y = i;
+            if (i0 >= 0) {
+                if (lowers) {
+                    --k;
+                    if (lane == k)
+                        fr = i0;
+                } else {
+                    if (lane == n_free)
+                        fr = i0;
+                    ++n_free;
+                }
+            }
+        }
+    }
+
+    // ---- augmentation (:168-251) ----
+    int pred_col = 0;  // lane = column
+    for (int f = 0; f < n_free; ++f) {
+        const int start = readlane_i(fr, f);
+        PosState st;
+        st.col = lane;
+        st.d = live ? (L.c[start * kTile + lane] - v) : finf();
+        st.pr = start;
+        st.yc = y;
+        st.vc = v;
+        int low = 0, up = 0, n_ready = 0;
+        float level = 0.f;
+        int end = -1;
+        while (end < 0) {
+            if (low >= K)
+                return false;  // no unassigned column reachable: cannot happen
+            if (up == low) {
+                // gather the columns at the new minimum into [low, up): a
+                // smaller d restarts the group at low, an equal one joins it
+                // (:185-199); events in position order from a prefix minimum
+                n_ready = low;
+                const bool act = live && lane >= low;
+                const int dkey = act ? fkey(st.d) : kKeyNone;
+                const int before = wave_shift_up_key(wave_prefix_min_key(dkey));
+                const bool later = act && lane > low;
+                const uint64_t rec = ballot(later && dkey < before);
+                const uint64_t tie = ballot(later && dkey == before);
+                uint64_t ev = rec | tie;
+                up = low + 1;
+                while (ev) {
+                    const int kk = first_lane(ev);
+                    ev &= ev - 1;
+                    if ((rec >> kk) & 1ull) {
+                        swap_lanes(st, kk, low);
+                        up = low + 1;
+                    } else {
+                        if (kk != up)
+                            swap_lanes(st, kk, up);
+                        ++up;
+                    }
+                }
+                level = readlane_f(st.d, low);
+                // the first unassigned column of the group ends the path (:200-206)
+                const uint64_t open = ballot(live && lane >= low && lane < up && st.yc < 0);
+                if (open)
+                    end = readlane_i(st.col, first_lane(open));
+            }
+            if (end >= 0)
+                break;
+            // scan the row of the group's next column (:209-233)
+            const int q = low++;
+            const int jq = readlane_i(st.col, q);
+            const int iq = readlane_i(st.yc, q);
+            const float vq = readlane_f(st.vc, q);
+            const float h = L.c[iq * kTile + jq] - vq - level;
+            const bool act = live && lane >= up;
+            const float cp = act ? L.c[iq * kTile + st.col] : 0.f;
+            const float r = cp - st.vc - h;
+            const bool better = act && r < st.d;
+            const bool tie = better && r == level;
+            const uint64_t ret = ballot(tie && st.yc < 0);
+            if (ret) {
+                // the reference stops at the first such column in position
+                // order: columns before it are relaxed, it only gets its pred
+                const int kk = first_lane(ret);
+                if (better && lane < kk)
+                    st.d = r;
+                if (better && lane <= kk)
+                    st.pr = iq;
+                end = readlane_i(st.col, kk);
+                break;
+            }
+            if (better) {
+                st.d = r;
+                st.pr = iq;
+            }
+            uint64_t tm = ballot(tie);
+            while (tm) {
+                const int kk = first_lane(tm);
+                tm &= tm - 1;
+                if (kk != up)
+                    swap_lanes(st, kk, up);
+                ++up;
+            }
+        }
+        // duals of the columns finished before the last group (:236-239)
+        if (live && lane < n_ready)
+            st.vc = st.vc + st.d - level;
+        if (live) {
+            L.vbuf[st.col] = st.vc;
+            L.pbuf[st.col] = st.pr;
+        }
+        __syncthreads();
+        if (live) {
+            v = L.vbuf[lane];
+            pred_col = L.pbuf[lane];
+        }
+        __syncthreads();
+        // flip the assignment along the predecessors (:241-250)
+        int j = end, i;
+        int hops = 0;
+        do {
+            i = readlane_i(pred_col, j);
+            if (lane == j)
+                y = i;
+            const int prev = readlane_i(x, i);
+            if (lane == i)
+                x = j;
+            j = prev;
+            if (++hops > K)
+                return false;
+        } while (i != start);
+    }
+    x_out = x;
+    return true;
+}
+
+// Lane-serial transcription of jonker_compact_kernel<int32_t, float>
+// (jonker_compact_core.h:20-252) for inputs outside the wave path's range;
+// exact for any finite input.  Returns false when the guard trips.
+__device__ bool serial_solve_compact(uint32_t n, const float *c, SerialScratch &s) {
+    int32_t *x = s.x, *y = s.y, *fr = s.fr, *pred = s.pred, *cols = s.cols;
+    float *v = s.v, *d = s.d;
+    for (uint32_t i = 0; i < n; ++i)
+        fr[i] = 0;
+    for (int32_t j = (int32_t)n - 1; j >= 0; --j) {
+        float m = c[j];
+        int32_t im = 0;
+        for (uint32_t i = 1; i < n; ++i)
+            if (c[i * kTile + j] < m) {
+                m = c[i * kTile + j];
+                im = (int32_t)i;
+            }
+        v[j] = m;
+        if (++fr[im] == 1) {
+            x[im] = j;
+            y[j] = im;
+        } else {
+            y[j] = -1;
+        }
+    }
+    uint32_t n_free = 0;
+    for (uint32_t i = 0; i < n; ++i) {
+        const int32_t claims = fr[i];
+        if (claims == 0) {
+            fr[n_free++] = (int32_t)i;
+        } else if (claims == 1) {
+            const int32_t jx = x[i];
+            float m = kFltMax;
+            for (uint32_t j = 0; j < n; ++j)
+                if ((int32_t)j != jx && c[i * kTile + j] - v[j] < m)
+                    m = c[i * kTile + j] - v[j];
+            v[jx] = v[jx] - m;
+        }
+    }
+    const uint32_t guard = compact_arr_guard((int)n);
+    uint32_t steps = 0;
+    for (int round = 0; round < 2; ++round) {
+        const uint32_t n_prev = n_free;
+        uint32_t k = 0;
+        n_free = 0;
+        while (k < n_prev) {
+            const int32_t i = fr[k++];
+            if (++steps > guard)
+                return false;
+            const float *row = c + i * kTile;
+            float u1 = row[0] - v[0], u2 = kFltMax;
+            int32_t j1 = 0, j2 = -1;
+            for (uint32_t j = 1; j < n; ++j) {
+                const float h = row[j] - v[j];
+                if (!(h < u2))
+                    continue;
+                if (h >= u1) {
+                    u2 = h;
+                    j2 = (int32_t)j;
+                } else {
+                    u2 = u1;
+                    j2 = j1;
+                    u1 = h;
+                    j1 = (int32_t)j;
+                }
+            }
+            int32_t i0 = y[j1];
+            const float lowered = v[j1] - (u2 - u1);
+            const bool lowers = lowered < v[j1];
+            if (lowers) {
+                v[j1] = lowered;
+            } else if (i0 >= 0) {
+                if (j2 < 0)
+                    return false;  // the reference reads colsol[-1] here
+                j1 = j2;
+                i0 = y[j2];
+            }
+            x[i] = j1;
+            y[j1] = i;
+            if (i0 >= 0) {
+                if (lowers)
+                    fr[--k] = i0;
+                else
+                    fr[n_free++] = i0;
+            }
+        }
+    }
+    for (uint32_t f = 0; f < n_free; ++f) {
+        const int32_t start = fr[f];
+        for (uint32_t j = 0; j < n; ++j) {
+            d[j] = c[start * kTile + j] - v[j];
+            pred[j] = start;
+            cols[j] = (int32_t)j;
+        }
+        uint32_t low = 0, up = 0;
+        int32_t last = 0, end = -1;
+        float level = 0.f;
+        while (end < 0) {
+            if (low >= n)
+                return false;
+            if (up == low) {
+                last = (int32_t)low - 1;
+                level = d[cols[up++]];
+                for (uint32_t k = up; k < n; ++k) {
+                    const int32_t j = cols[k];
+                    const float h = d[j];
+                    if (h <= level) {
+                        if (h < level) {
+                            up = low;
+                            level = h;
+                        }
+                        cols[k] = cols[up];
+                        cols[up++] = j;
+                    }
+                }
+                for (uint32_t k = low; k < up; ++k)
+                    if (y[cols[k]] < 0) {
+                        end = cols[k];
+                        break;
+                    }
+            }
+            if (end >= 0)
+                break;
+            const int32_t jq = cols[low++];
+            const int32_t iq = y[jq];
+            const float *row = c + iq * kTile;
+            const float h = row[jq] - v[jq] - level;
+            for (uint32_t k = up; k < n; ++k) {
+                const int32_t j = cols[k];
+                const float r = row[j] - v[j] - h;
+                if (!(r < d[j]))
+                    continue;
+                pred[j] = iq;
+                if (r == level) {
+                    if (y[j] < 0) {
+                        end = j;
+                        break;
+                    }
+                    cols[k] = cols[up];
+                    cols[up++] = j;
+                }
+                d[j] = r;
+            }
+        }
+        for (int32_t k = 0; k <= last; ++k) {
+            const int32_t j = cols[k];
+            v[j] = v[j] + d[j] - level;
+        }
+        int32_t i;
+        uint32_t hops = 0;
+        do {
+            i = pred[end];
+            y[end] = i;
+            const int32_t j = end;
+            end = x[i];
+            x[i] = j;
+            if (++hops > n)
+                return false;
+        } while (i != start);
+    }
+    return true;
+}
+
+// One problem per 64-lane workgroup; COMPACT selects the solver of
+// assignment::jonker_compact_batch instead of jonker_dense_batch (same
+// statistics, sentinel, padding and output rules, ops.cpp:176-289).
+template <bool COMPACT>
 __global__ void __launch_bounds__(64)
 jv_solve_kernel(const float *__restrict__ costs, int64_t B, int N, int M,
                 const JvStats *__restrict__ partial, int n_partial,
@@ -960,7 +1400,21 @@ jv_solve_kernel(const float *__restrict__ costs, int64_t B, int N, int M,
     }
 
     int x = -1;
-    if (fast) {
+    if constexpr (COMPACT) {
+        if (fast) {
+            if (!wave_solve_compact(K, L, vmin, ymin, x)) {
+                if (lane == 0)
+                    atomicOr(&status[1], 1u);
+                x = -1;
+            }
+        } else {
+            if (lane == 0 && !serial_solve_compact((uint32_t)K, L.c, S))
+                atomicOr(&status[1], 1u);
+            __syncthreads();
+            if (lane < K)
+                x = S.x[lane];
+        }
+    } else if (fast) {
         // displacement chains need K >= 2 and no -0.0 (their second minimum is
         // read back from its key, which maps -0.0 to +0.0)
         const bool chain = K >= 2 && (flags & kJvFlagNegZero) == 0;
@@ -1021,13 +1475,45 @@ extern "C" int tm_jv_dense_batch_f32(const float *costs, int64_t B, int32_t N, i
         return kTmErrLaunch;
     if (K > kTile)
         return launch_jv_large(costs, B, N, M, partial, (int)blocks, out, d_status, stream);
-    hipLaunchKernelGGL(jv_solve_kernel, dim3((unsigned)B), dim3(64), 0, stream, costs, B, N, M,
-                       partial, (int)blocks, out, d_status);
+    hipLaunchKernelGGL(jv_solve_kernel<false>, dim3((unsigned)B), dim3(64), 0, stream, costs, B,
+                       N, M, partial, (int)blocks, out, d_status);
+    e = hipGetLastError();
+    return e == hipSuccess ? kTmOk : kTmErrLaunch;
+}
+
+extern "C" int tm_jv_compact_batch_f32(const float *costs, int64_t B, int32_t N, int32_t M,
+                                       int64_t *out, void *workspace, size_t workspace_bytes,
+                                       uint32_t *d_status, hipStream_t stream) {
+    if (B < 0 || N < 0 || M < 0)
+        return kTmErrInvalidArgument;
+    if (B == 0 || N == 0 || M == 0)
+        return kTmOk;  // caller fills -1
+    const int K = N > M ? N : M;
+    if (K > kTile)
+        return kTmErrUnsupportedShape;
+    if (workspace_bytes < tm_jv_workspace_bytes(B, N, M) || workspace == nullptr ||
+        d_status == nullptr)
+        return kTmErrWorkspace;
+    if (B > (int64_t)0x7fffffff)
+        return kTmErrUnsupportedShape;
+    const int64_t n = B * (int64_t)N * M;
+    int64_t blocks = (n / 4 + kStatsBlock - 1) / kStatsBlock;
+    blocks = blocks < 1 ? 1 : (blocks > kJvMaxStatBlocks ? kJvMaxStatBlocks : blocks);
+    JvStats *partial = static_cast<JvStats *>(workspace);
+    hipLaunchKernelGGL(jv_stats_kernel, dim3((unsigned)blocks), dim3(kStatsBlock), 0, stream,
+                       costs, n, partial, d_status);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess)
+        return kTmErrLaunch;
+    hipLaunchKernelGGL(jv_solve_kernel<true>, dim3((unsigned)B), dim3(64), 0, stream, costs, B,
+                       N, M, partial, (int)blocks, out, d_status);
     e = hipGetLastError();
     return e == hipSuccess ? kTmOk : kTmErrLaunch;
 }
 
 extern "C" int32_t tm_jv_max_k(void) { return jv_large_max_k(); }
+
+extern "C" int32_t tm_jv_compact_max_k(void) { return kTile; }
 
 extern "C" int tm_jv_check_status(const uint32_t *d_status, hipStream_t stream) {
     uint32_t words[2] = {0, 0};

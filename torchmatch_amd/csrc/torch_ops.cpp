@@ -64,10 +64,13 @@ void check_rc(int rc, const char *op_name) {
     }
 }
 
-// CUDA-key kernel of assignment::jonker_dense_batch.
-// Reference: assignment/cuda/dispatch.cu:137-177; results follow the CPU op
-// assignment/cpu/ops.cpp:176-289 (rectangular input accepted, like the CPU op).
-at::Tensor jonker_dense_batch_hip(const at::Tensor &costs) {
+using JvSolver = int (*)(const float *, int64_t, int32_t, int32_t, int64_t *, void *, size_t,
+                        uint32_t *, hipStream_t);
+
+// Shared body of the batched JV ops: checks, float32 view, workspace, one
+// solve launch, then the single status readback.
+at::Tensor jv_batch_hip(const at::Tensor &costs, JvSolver solver, int64_t max_k,
+                        const char *op_name) {
     TORCH_CHECK(costs.is_cuda(), "costs must be a CUDA tensor");
     TORCH_CHECK(costs.dim() == 3, "costs must be 3D (B, N, M), got ", costs.dim());
     TORCH_CHECK(costs.scalar_type() == at::kFloat || costs.scalar_type() == at::kDouble,
@@ -84,11 +87,11 @@ at::Tensor jonker_dense_batch_hip(const at::Tensor &costs) {
         return out;
     }
     const int64_t K = N > M ? N : M;
-    TORCH_CHECK(K <= tm_jv_max_k(), "jonker_dense_batch (gfx950) supports K = max(N, M) <= ",
-                tm_jv_max_k(), ", got K=", K);
+    TORCH_CHECK(K <= max_k, op_name, " (gfx950) supports K = max(N, M) <= ", max_k, ", got K=",
+                K);
 
     const hipStream_t stream = current_stream(costs);
-    check_not_capturing(stream, "jonker_dense_batch");
+    check_not_capturing(stream, op_name);
 
     // float64 input is solved in float32, as the reference device op does
     // (dispatch.cu:156).
@@ -96,23 +99,20 @@ at::Tensor jonker_dense_batch_hip(const at::Tensor &costs) {
     const size_t ws_bytes = tm_jv_workspace_bytes(B, (int32_t)N, (int32_t)M);
     auto ws = at::empty({(int64_t)ws_bytes}, costs.options().dtype(at::kByte));
     auto status = at::empty({2}, costs.options().dtype(at::kInt));
-    int rc = tm_jv_dense_batch_f32(cf.data_ptr<float>(), B, (int32_t)N, (int32_t)M,
-                                   out.data_ptr<int64_t>(), ws.data_ptr(), ws_bytes,
-                                   reinterpret_cast<uint32_t *>(status.data_ptr<int32_t>()),
-                                   stream);
-    check_rc(rc, "jonker_dense_batch");
+    int rc = solver(cf.data_ptr<float>(), B, (int32_t)N, (int32_t)M, out.data_ptr<int64_t>(),
+                    ws.data_ptr(), ws_bytes,
+                    reinterpret_cast<uint32_t *>(status.data_ptr<int32_t>()), stream);
+    check_rc(rc, op_name);
     rc = tm_jv_check_status(reinterpret_cast<const uint32_t *>(status.data_ptr<int32_t>()),
                             stream);
-    check_rc(rc, "jonker_dense_batch");
+    check_rc(rc, op_name);
     return out;
 }
 
-// CUDA-key kernel of assignment::jonker_dense_batch_unpacked: the solve above,
-// then the device unpack (tm_jv_unpack_i64) into the tuple the reference CPU op
-// returns (assignment/cpu/ops.cpp:291-417, registered at :504).
+// The device unpack (tm_jv_unpack_i64) of a packed (B, N) mapping into the
+// tuple the reference CPU ops return (assignment/cpu/ops.cpp:291-417).
 std::tuple<at::Tensor, at::Tensor, at::Tensor, at::Tensor>
-jonker_dense_batch_unpacked_hip(const at::Tensor &costs) {
-    const at::Tensor packed = jonker_dense_batch_hip(costs);
+unpack_hip(const at::Tensor &costs, const at::Tensor &packed, const char *op_name) {
     const c10::DeviceGuard guard(costs.device());
     const int64_t B = costs.size(0), N = costs.size(1), M = costs.size(2);
     const auto lopts = costs.options().dtype(at::kLong);
@@ -128,8 +128,37 @@ jonker_dense_batch_unpacked_hip(const at::Tensor &costs) {
                                     matches.data_ptr<int64_t>(), ur.data_ptr<int64_t>(),
                                     uc.data_ptr<int64_t>(), nm.data_ptr<int64_t>(),
                                     current_stream(costs));
-    check_rc(rc, "jonker_dense_batch_unpacked");
+    check_rc(rc, op_name);
     return {matches, ur, uc, nm};
+}
+
+// CUDA-key kernel of assignment::jonker_dense_batch.
+// Reference: assignment/cuda/dispatch.cu:137-177; results follow the CPU op
+// assignment/cpu/ops.cpp:176-289 (rectangular input accepted, like the CPU op).
+at::Tensor jonker_dense_batch_hip(const at::Tensor &costs) {
+    return jv_batch_hip(costs, &tm_jv_dense_batch_f32, tm_jv_max_k(), "jonker_dense_batch");
+}
+
+// CUDA-key kernel of assignment::jonker_dense_batch_unpacked (CPU op at
+// assignment/cpu/ops.cpp:436-440, registered at :504).
+std::tuple<at::Tensor, at::Tensor, at::Tensor, at::Tensor>
+jonker_dense_batch_unpacked_hip(const at::Tensor &costs) {
+    return unpack_hip(costs, jonker_dense_batch_hip(costs), "jonker_dense_batch_unpacked");
+}
+
+// CUDA-key kernel of assignment::jonker_compact_batch: the mapping of the CPU
+// op assignment/cpu/ops.cpp:431-433 (solve_batch around the compact solver of
+// jonker_compact_core.h), which has no device counterpart in the reference.
+at::Tensor jonker_compact_batch_hip(const at::Tensor &costs) {
+    return jv_batch_hip(costs, &tm_jv_compact_batch_f32, tm_jv_compact_max_k(),
+                        "jonker_compact_batch");
+}
+
+// CUDA-key kernel of assignment::jonker_compact_batch_unpacked (CPU op at
+// assignment/cpu/ops.cpp:441-445).
+std::tuple<at::Tensor, at::Tensor, at::Tensor, at::Tensor>
+jonker_compact_batch_unpacked_hip(const at::Tensor &costs) {
+    return unpack_hip(costs, jonker_compact_batch_hip(costs), "jonker_compact_batch_unpacked");
 }
 
 void check_keep(const at::Tensor &cost, const c10::optional<at::Tensor> &keep) {
@@ -224,6 +253,8 @@ sinkhorn_iterate_hip(const at::Tensor &cost, const c10::optional<at::Tensor> &ke
 TORCH_LIBRARY_IMPL(assignment, CUDA, m) {
     m.impl("jonker_dense_batch", &jonker_dense_batch_hip);
     m.impl("jonker_dense_batch_unpacked", &jonker_dense_batch_unpacked_hip);
+    m.impl("jonker_compact_batch", &jonker_compact_batch_hip);
+    m.impl("jonker_compact_batch_unpacked", &jonker_compact_batch_unpacked_hip);
 }
 
 TORCH_LIBRARY(torchmatch_amd, m) {
