@@ -15,8 +15,9 @@ reference's own JV solver (oracle/_ref, compiled from its source) or, where
 absent, the C restatement, on this host's cores, rank 0 only, on a bounded
 sample; Sinkhorn's CPU baseline is the op-for-op torch restatement.
 Extra legs (skipped by --no-extra): C3 = JV on (64, 512, 768) with 20% +inf
-(solves/s) and C5 = unbalanced Sinkhorn on (1, 16384, 16384) (iterations/s,
-HBM GB/s).  --copy-calibration runs only a 256 MiB device copy, the known
+(solves/s), C5 = unbalanced Sinkhorn on (1, 16384, 16384) (iterations/s,
+HBM GB/s) and jonker_compact_batch on the C2 input (solves/s, with the
+reference's compact solver as its CPU baseline).  --copy-calibration runs only a 256 MiB device copy, the known
 traffic that profiler byte counters are scaled against.
 """
 
@@ -221,6 +222,21 @@ def bench_jv_c3(device, reps: int = 3) -> dict:
             "solves_per_s": 64 / (ms * 1e-3), "ms_per_batch": ms}
 
 
+def bench_jv_compact(device, reps: int = 20) -> dict:
+    """jonker_compact_batch on the C2 input (1024, 64, 64), op time per batch."""
+    from torchmatch_amd import workloads
+
+    cost = workloads.jv_uniform(1024, 64, 64, seed=0).to(device)
+    op = torch.ops.assignment.jonker_compact_batch
+    for _ in range(3):
+        op(cost)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream(device)
+    ms = sorted(_events_time_ms(lambda: op(cost), 1, stream) for _ in range(reps))[reps // 2]
+    return {"config": {"workload": "jonker_compact_batch on C2", "B": 1024, "N": 64, "M": 64},
+            "solves_per_s": 1024 / (ms * 1e-3), "ms_per_batch": ms}
+
+
 def bench_unbalanced_c5(device, n_long: int = 100, n_short: int = 20) -> dict:
     """C5: unbalanced Sinkhorn on (1, 16384, 16384), reg 0.02, rho 1 (slope)."""
     from torchmatch_amd import workloads
@@ -255,16 +271,16 @@ def copy_calibration(device, mib: int = 256, reps: int = 5) -> dict:
     return {"copy_bytes_each_way": n * 4, "reps": reps}
 
 
-def cpu_baseline_jv(budget_s: float = 10.0) -> dict:
+def cpu_baseline_jv(budget_s: float = 10.0, compact: bool = False) -> dict:
     from oracle import jv
     from torchmatch_amd import workloads
 
     cost = workloads.jv_uniform(1024, 64, 64, seed=0).numpy()
     threads = jv.default_threads()
     if jv.ref_available():
-        fn, kind = jv.ref_jv_dense_batch, "reference"
+        fn, kind = (jv.ref_jv_compact_batch if compact else jv.ref_jv_dense_batch), "reference"
     else:
-        fn, kind = jv.jv_dense_batch, "port"
+        fn, kind = (jv.jv_compact_batch if compact else jv.jv_dense_batch), "port"
     fn(cost, threads)  # warm-up
     times = []
     t_end = time.perf_counter() + budget_s
@@ -361,8 +377,12 @@ def main() -> int:
                          for k, v in bench_jv_c3(device).items()}
         line["unbalanced_c5"] = {k: (round(v, 4) if isinstance(v, float) else v)
                                  for k, v in bench_unbalanced_c5(device).items()}
+        line["jv_compact_c2"] = {k: (round(v, 4) if isinstance(v, float) else v)
+                                 for k, v in bench_jv_compact(device).items()}
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline_jv()
+        if not args.no_extra:
+            line["jv_compact_c2"]["cpu_baseline"] = cpu_baseline_jv(5.0, compact=True)
         if not args.no_sinkhorn:
             line["sinkhorn"]["cpu_baseline"] = cpu_baseline_sinkhorn()
     print(json.dumps(line), flush=True)

@@ -8,8 +8,9 @@ batches there (assignment/_solve.py:75-76).  Checked against the committed
 golden fixtures (the "compact" mappings, written from the reference's own
 compiled header) and against the pinned C oracle (jvoc_square) on seeded
 inputs: uniform, integer-tied, +inf-masked, gated-sparse, rectangular both
-ways, K = 1..max, negative and huge magnitudes (the lane-serial path), -0.0,
-all-+inf problems, plus the NaN / -inf contract and the unpacked tuple.
+ways, K = 1..64 and large K up to 1024 (the second kernel), negative and
+huge magnitudes (the lane-serial paths), -0.0, all-+inf problems, plus the
+NaN / -inf contract and the unpacked tuple.
 """
 
 from __future__ import annotations
@@ -95,6 +96,25 @@ def test_random_batches_match_oracle(kind, device):
     for b, n, m in shapes:
         c = _random_batch(rng, kind, b, n, m)
         print(f"compact {kind} {(b, n, m)}", flush=True)
+        want = jv.jv_compact_batch(c)
+        got = run_op(c, device)
+        mism = np.argwhere((got != want).any(axis=1)).ravel()
+        assert mism.size == 0, f"{kind} {(b, n, m)}: {mism.size} problems differ"
+
+
+@pytest.mark.parametrize("kind", ["uniform", "tied", "masked", "tied_masked", "negative", "huge"])
+def test_large_k_match_oracle(kind, device):
+    """64 < K <= 1024: the large-K compact kernel (and its lane-serial path for
+    huge magnitudes)."""
+    if _max_k() <= 64:
+        pytest.skip("no large-K compact kernel in this build")
+    rng = np.random.default_rng(zlib.crc32(b"compact-large-" + kind.encode()))
+    shapes = [(16, 65, 65), (8, 100, 130), (8, 130, 100), (6, 300, 300), (3, 700, 768)]
+    if kind != "huge":
+        shapes.append((2, 1024, 1000))
+    for b, n, m in shapes:
+        c = _random_batch(rng, kind, b, n, m)
+        print(f"compact large {kind} {(b, n, m)}", flush=True)
         want = jv.jv_compact_batch(c)
         got = run_op(c, device)
         mism = np.argwhere((got != want).any(axis=1)).ravel()

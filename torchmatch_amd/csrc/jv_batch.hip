@@ -1,8 +1,9 @@
 // jv_batch.hip -- batched Jonker-Volgenant (float32) for gfx950.
 //
 // Reproduces the int64 row->col mapping of torchmatch's CPU
-// `assignment::jonker_dense_batch` bit for bit, and, for K <= 64, that of
-// `assignment::jonker_compact_batch` (section 3 below):
+// `assignment::jonker_dense_batch` bit for bit, and that of
+// `assignment::jonker_compact_batch` (section 3 below; K > 64 runs in
+// jv_compact_large.hip):
 //   sentinel + padding      sources/torchmatch/assignment/cpu/ops.cpp:67-93,176-289
 //   solver                  sources/torchmatch/assignment/cpu/jonker_dense_flat.h:27-274
 //   compact solver          sources/torchmatch/assignment/cpu/jonker_compact_core.h:20-252
@@ -38,6 +39,7 @@
 
 #include "jv_batch.h"
 #include "jv_common.h"
+#include "jv_compact.h"
 #include "wave.h"
 
 namespace tmamd {
@@ -885,26 +887,10 @@ __device__ __forceinline__ bool wave_solve(const int K, WaveLds &L, float v,
 // 3. compact variant (assignment::jonker_compact_batch), K <= 64
 // ---------------------------------------------------------------------------
 // jonker_compact_core.h:51-252 solves the same padded square problem as the
-// dense solver but with its own tie and ordering rules, so its mappings
-// differ on ties.  The code below follows it step by step:
-//   * column reduction from the last column, minima seeded by row 0 (on the
-//     wave path every cost is below LARGE, so the dense path's minima and
-//     claims are the same and are shared);
-//   * reduction transfer with FLT_MAX as the starting minimum;
-//   * augmenting row reduction without an iteration cap (a generous guard
-//     reports a runaway instead of spinning), the second minimum seeded by
-//     FLT_MAX, the displaced owner pushed back at the read position (lowered
-//     dual) or appended to the next round;
-//   * augmentation: the FIRST unassigned column of a new minimum group ends
-//     the path, and the finished columns' duals become (v + d) - min.
-
-constexpr float kFltMax = 3.402823466e38f;  // numeric_limits<float>::max()
-
-// Iteration guard of the compact augmenting row reduction (which has no cap
-// in the reference): far above what any input reaches in practice.
-__device__ __forceinline__ uint32_t compact_arr_guard(int K) {
-    return 64u * (uint32_t)K * (uint32_t)K + 4096u;
-}
+// dense solver with its own tie and ordering rules (listed in jv_compact.h),
+// so its mappings differ on ties.  On the wave path every cost is below
+// LARGE, so the dense path's column minima and claims are the same and the
+// column reduction is shared; the rest follows the compact rules.
 
 // find_umins_regular (jonker_compact_core.h:20-43) on the wave: j1 is the
 // first index of the smallest reduced cost, j2 the next column in (value,
@@ -1089,6 +1075,8 @@ __device__ __forceinline__ bool wave_solve_compact(const int K, WaveLds &L, floa
             const int q = low++;
             const int jq = readlane_i(st.col, q);
             const int iq = readlane_i(st.yc, q);
+            if (iq < 0)
+                return false;  // group columns are assigned: cannot happen
             const float vq = readlane_f(st.vc, q);
             const float h = L.c[iq * kTile + jq] - vq - level;
             const bool act = live && lane >= up;
@@ -1150,168 +1138,6 @@ __device__ __forceinline__ bool wave_solve_compact(const int K, WaveLds &L, floa
         } while (i != start);
     }
     x_out = x;
-    return true;
-}
-
-// Lane-serial transcription of jonker_compact_kernel<int32_t, float>
-// (jonker_compact_core.h:20-252) for inputs outside the wave path's range;
-// exact for any finite input.  Returns false when the guard trips.
-__device__ bool serial_solve_compact(uint32_t n, const float *c, SerialScratch &s) {
-    int32_t *x = s.x, *y = s.y, *fr = s.fr, *pred = s.pred, *cols = s.cols;
-    float *v = s.v, *d = s.d;
-    for (uint32_t i = 0; i < n; ++i)
-        fr[i] = 0;
-    for (int32_t j = (int32_t)n - 1; j >= 0; --j) {
-        float m = c[j];
-        int32_t im = 0;
-        for (uint32_t i = 1; i < n; ++i)
-            if (c[i * kTile + j] < m) {
-                m = c[i * kTile + j];
-                im = (int32_t)i;
-            }
-        v[j] = m;
-        if (++fr[im] == 1) {
-            x[im] = j;
-            y[j] = im;
-        } else {
-            y[j] = -1;
-        }
-    }
-    uint32_t n_free = 0;
-    for (uint32_t i = 0; i < n; ++i) {
-        const int32_t claims = fr[i];
-        if (claims == 0) {
-            fr[n_free++] = (int32_t)i;
-        } else if (claims == 1) {
-            const int32_t jx = x[i];
-            float m = kFltMax;
-            for (uint32_t j = 0; j < n; ++j)
-                if ((int32_t)j != jx && c[i * kTile + j] - v[j] < m)
-                    m = c[i * kTile + j] - v[j];
-            v[jx] = v[jx] - m;
-        }
-    }
-    const uint32_t guard = compact_arr_guard((int)n);
-    uint32_t steps = 0;
-    for (int round = 0; round < 2; ++round) {
-        const uint32_t n_prev = n_free;
-        uint32_t k = 0;
-        n_free = 0;
-        while (k < n_prev) {
-            const int32_t i = fr[k++];
-            if (++steps > guard)
-                return false;
-            const float *row = c + i * kTile;
-            float u1 = row[0] - v[0], u2 = kFltMax;
-            int32_t j1 = 0, j2 = -1;
-            for (uint32_t j = 1; j < n; ++j) {
-                const float h = row[j] - v[j];
-                if (!(h < u2))
-                    continue;
-                if (h >= u1) {
-                    u2 = h;
-                    j2 = (int32_t)j;
-                } else {
-                    u2 = u1;
-                    j2 = j1;
-                    u1 = h;
-                    j1 = (int32_t)j;
-                }
-            }
-            int32_t i0 = y[j1];
-            const float lowered = v[j1] - (u2 - u1);
-            const bool lowers = lowered < v[j1];
-            if (lowers) {
-                v[j1] = lowered;
-            } else if (i0 >= 0) {
-                if (j2 < 0)
-                    return false;  // the reference reads colsol[-1] here
-                j1 = j2;
-                i0 = y[j2];
-            }
-            x[i] = j1;
-            y[j1] = i;
-            if (i0 >= 0) {
-                if (lowers)
-                    fr[--k] = i0;
-                else
-                    fr[n_free++] = i0;
-            }
-        }
-    }
-    for (uint32_t f = 0; f < n_free; ++f) {
-        const int32_t start = fr[f];
-        for (uint32_t j = 0; j < n; ++j) {
-            d[j] = c[start * kTile + j] - v[j];
-            pred[j] = start;
-            cols[j] = (int32_t)j;
-        }
-        uint32_t low = 0, up = 0;
-        int32_t last = 0, end = -1;
-        float level = 0.f;
-        while (end < 0) {
-            if (low >= n)
-                return false;
-            if (up == low) {
-                last = (int32_t)low - 1;
-                level = d[cols[up++]];
-                for (uint32_t k = up; k < n; ++k) {
-                    const int32_t j = cols[k];
-                    const float h = d[j];
-                    if (h <= level) {
-                        if (h < level) {
-                            up = low;
-                            level = h;
-                        }
-                        cols[k] = cols[up];
-                        cols[up++] = j;
-                    }
-                }
-                for (uint32_t k = low; k < up; ++k)
-                    if (y[cols[k]] < 0) {
-                        end = cols[k];
-                        break;
-                    }
-            }
-            if (end >= 0)
-                break;
-            const int32_t jq = cols[low++];
-            const int32_t iq = y[jq];
-            const float *row = c + iq * kTile;
-            const float h = row[jq] - v[jq] - level;
-            for (uint32_t k = up; k < n; ++k) {
-                const int32_t j = cols[k];
-                const float r = row[j] - v[j] - h;
-                if (!(r < d[j]))
-                    continue;
-                pred[j] = iq;
-                if (r == level) {
-                    if (y[j] < 0) {
-                        end = j;
-                        break;
-                    }
-                    cols[k] = cols[up];
-                    cols[up++] = j;
-                }
-                d[j] = r;
-            }
-        }
-        for (int32_t k = 0; k <= last; ++k) {
-            const int32_t j = cols[k];
-            v[j] = v[j] + d[j] - level;
-        }
-        int32_t i;
-        uint32_t hops = 0;
-        do {
-            i = pred[end];
-            y[end] = i;
-            const int32_t j = end;
-            end = x[i];
-            x[i] = j;
-            if (++hops > n)
-                return false;
-        } while (i != start);
-    }
     return true;
 }
 
@@ -1408,7 +1234,10 @@ jv_solve_kernel(const float *__restrict__ costs, int64_t B, int N, int M,
                 x = -1;
             }
         } else {
-            if (lane == 0 && !serial_solve_compact((uint32_t)K, L.c, S))
+            const float *tile = L.c;
+            auto cost = [tile](int i, int j) { return tile[i * kTile + j]; };
+            if (lane == 0 && !compact_serial((uint32_t)K, cost, S.x, S.y, S.fr, S.pred, S.cols,
+                                             S.v, S.d))
                 atomicOr(&status[1], 1u);
             __syncthreads();
             if (lane < K)
@@ -1489,7 +1318,7 @@ extern "C" int tm_jv_compact_batch_f32(const float *costs, int64_t B, int32_t N,
     if (B == 0 || N == 0 || M == 0)
         return kTmOk;  // caller fills -1
     const int K = N > M ? N : M;
-    if (K > kTile)
+    if (K > jv_compact_max_k())
         return kTmErrUnsupportedShape;
     if (workspace_bytes < tm_jv_workspace_bytes(B, N, M) || workspace == nullptr ||
         d_status == nullptr)
@@ -1505,6 +1334,9 @@ extern "C" int tm_jv_compact_batch_f32(const float *costs, int64_t B, int32_t N,
     hipError_t e = hipGetLastError();
     if (e != hipSuccess)
         return kTmErrLaunch;
+    if (K > kTile)
+        return launch_jv_compact_large(costs, B, N, M, partial, (int)blocks, out, d_status,
+                                       stream);
     hipLaunchKernelGGL(jv_solve_kernel<true>, dim3((unsigned)B), dim3(64), 0, stream, costs, B,
                        N, M, partial, (int)blocks, out, d_status);
     e = hipGetLastError();
@@ -1513,7 +1345,7 @@ extern "C" int tm_jv_compact_batch_f32(const float *costs, int64_t B, int32_t N,
 
 extern "C" int32_t tm_jv_max_k(void) { return jv_large_max_k(); }
 
-extern "C" int32_t tm_jv_compact_max_k(void) { return kTile; }
+extern "C" int32_t tm_jv_compact_max_k(void) { return jv_compact_max_k(); }
 
 extern "C" int tm_jv_check_status(const uint32_t *d_status, hipStream_t stream) {
     uint32_t words[2] = {0, 0};
