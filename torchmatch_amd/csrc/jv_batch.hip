@@ -74,8 +74,18 @@ jv_stats_kernel(const float *__restrict__ costs, int64_t n, JvStats *__restrict_
             mn = fminf(mn, x);
         }
     };
-    for (int64_t k = (int64_t)blockIdx.x * kStatsBlock + threadIdx.x; k < n4; k += stride) {
-        const float4 q = c4[k];
+    int64_t k0 = (int64_t)blockIdx.x * kStatsBlock + threadIdx.x;
+    // four loads in flight per lane before any is folded
+    for (; k0 + 3 * stride < n4; k0 += 4 * stride) {
+        const float4 q0 = c4[k0], q1 = c4[k0 + stride], q2 = c4[k0 + 2 * stride],
+                     q3 = c4[k0 + 3 * stride];
+        visit(q0.x); visit(q0.y); visit(q0.z); visit(q0.w);
+        visit(q1.x); visit(q1.y); visit(q1.z); visit(q1.w);
+        visit(q2.x); visit(q2.y); visit(q2.z); visit(q2.w);
+        visit(q3.x); visit(q3.y); visit(q3.z); visit(q3.w);
+    }
+    for (; k0 < n4; k0 += stride) {
+        const float4 q = c4[k0];
         visit(q.x);
         visit(q.y);
         visit(q.z);
