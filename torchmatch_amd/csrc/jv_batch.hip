@@ -486,6 +486,15 @@ __device__ __forceinline__ CacheFill cache_fill(float crow, float v, int y, bool
     return f;
 }
 
+// COMPACT = false: jonker_dense_flat.h:124-274 (jonker_dense_batch);
+// COMPACT = true: jonker_compact_core.h:51-252 (jonker_compact_batch).  On the
+// wave path's value range (every cost far below LARGE and FLT_MAX) the two
+// solvers differ only in (a) the cap of the augmenting row reduction (none in
+// the compact one), (b) which unassigned column of a minimum group ends a path
+// (last / first), (c) the dual update's operand order, and (d) the starting
+// minimum of the reduction transfer (LARGE / FLT_MAX, which only matters for
+// K = 1); everything else is shared.
+template <bool COMPACT>
 __device__ __forceinline__ bool wave_solve(const int K, WaveLds &L, float v,
                                            int y, bool chain, int &x_out) {
     const int lane = lane_id();
@@ -527,7 +536,8 @@ __device__ __forceinline__ bool wave_solve(const int K, WaveLds &L, float v,
         // reduction transfer, unique rows in increasing order: each one sees
         // the v lowered by the rows before it; mn starts at LARGE and keeps
         // the first (lowest column) minimum, as the sequential scan does
-        const int large_key = fkey(kLarge);
+        const float start_min = COMPACT ? kFltMax : kLarge;
+        const int large_key = fkey(start_min);
         uint64_t t = ballot(live && x >= 0 && unique_row);
         while (t) {
             const int i = first_lane(t);
@@ -536,7 +546,7 @@ __device__ __forceinline__ bool wave_solve(const int K, WaveLds &L, float v,
             const float r = L.c[i * kTile + lane] - v;
             const int key = (live && lane != own) ? fkey(r) : kKeyNone;
             const int kmin = uniform_i(wave_min_key(key));
-            float mn = kLarge;
+            float mn = start_min;
             if (kmin < large_key)
                 mn = readlane_f(r, first_lane(ballot(key == kmin)));
             if (lane == own)
@@ -547,7 +557,10 @@ __device__ __forceinline__ bool wave_solve(const int K, WaveLds &L, float v,
     // ---- augmenting row reduction (carr_dense, jonker_dense_flat.h:178-235) ----
     // iteration guard: the reference's loop ends long before this; tripping it
     // means a bug here, reported through the status word instead of spinning
-    const uint32_t rr_limit = 4u * (uint32_t)K * (uint32_t)K * (uint32_t)K + 64u;
+    // (the compact reduction has no cap: its guard is a step budget, which
+    // also stands in for the cap of the chains below)
+    const uint32_t rr_limit =
+        COMPACT ? compact_arr_guard(K) : 4u * (uint32_t)K * (uint32_t)K * (uint32_t)K + 64u;
     // A general step follows the reference's branches with scalar selects.
     // When it displaces the previous owner of its column with a lowered dual
     // (the reference's `free_rows[--current] = i0`, almost every step on
@@ -587,7 +600,7 @@ __device__ __forceinline__ bool wave_solve(const int K, WaveLds &L, float v,
                 // position cur.  A row without a usable cache is rescanned
                 // first.  The first step that is not such a step goes to the
                 // general step below.
-                const uint32_t rr_cap = (cur + 1) * (uint32_t)K;
+                const uint32_t rr_cap = COMPACT ? rr_limit : (cur + 1) * (uint32_t)K;
                 while (true) {
                     while (((rc.stepm >> fi) & 1ull) && rr + 1 < rr_cap) {
                         const int c1 = readlane_i(rc.t1q, fi);
@@ -670,7 +683,7 @@ __device__ __forceinline__ bool wave_solve(const int K, WaveLds &L, float v,
             const float vj1 = readlane_f(v, j1);
             const float lowered = vj1 - (u2 - u1);
             const bool lowers = lowered < vj1;
-            const bool cap = rr < cur * (uint32_t)K;
+            const bool cap = COMPACT || rr < cur * (uint32_t)K;
             const bool vupd = cap && lowers;
             const bool swap2 = cap && !lowers && i0 >= 0 && j2 >= 0;
             const int jsel = swap2 ? j2 : j1;
@@ -712,7 +725,7 @@ __device__ __forceinline__ bool wave_solve(const int K, WaveLds &L, float v,
             // branch: cap (rr_cnt < current * n, current counted after the
             // read), dual lowered, column owned.  Anything else ends the chain
             // and the general step above redoes that step exactly.
-            const uint32_t rr_cap = (cur + 1) * (uint32_t)K;
+            const uint32_t rr_cap = COMPACT ? rr_limit : (cur + 1) * (uint32_t)K;
             uint64_t okm;
             int inext;
             float cnext;  // row of the displaced owner, loaded ahead
@@ -781,6 +794,7 @@ __device__ __forceinline__ bool wave_solve(const int K, WaveLds &L, float v,
         st.vc = v;
         int lo = 0, hi = 0, n_ready = 0;
         int final_j = -1;
+        float group_level = 0.f;
         while (final_j < 0) {
             if (lo >= K)
                 return false;  // no unassigned column reachable: cannot happen
@@ -808,10 +822,14 @@ __device__ __forceinline__ bool wave_solve(const int K, WaveLds &L, float v,
                         ++hi;
                     }
                 }
+                group_level = readlane_f(st.d, lo);
                 const uint64_t open =
                     ballot(live && lane >= lo && lane < hi && st.yc < 0);
+                // dense: the last unassigned column of the group ends the
+                // path (jonker_dense_flat.h:96-103); compact: the first
+                // (jonker_compact_core.h:200-206)
                 if (open)
-                    final_j = readlane_i(st.col, last_lane(open));
+                    final_j = readlane_i(st.col, COMPACT ? first_lane(open) : last_lane(open));
             }
             if (final_j >= 0)
                 break;
@@ -822,7 +840,9 @@ __device__ __forceinline__ bool wave_solve(const int K, WaveLds &L, float v,
                 const int q = slo++;
                 const int jq = readlane_i(st.col, q);
                 const int iq = readlane_i(st.yc, q);
-                const float level = readlane_f(st.d, q);
+                // the group's common d: compact uses the level of its
+                // gathering, dense the scanned column's own d (equal values)
+                const float level = COMPACT ? group_level : readlane_f(st.d, q);
                 const float vq = readlane_f(st.vc, q);
                 const float cq = L.c[iq * kTile + jq];
                 const float h = cq - vq - level;
@@ -834,10 +854,12 @@ __device__ __forceinline__ bool wave_solve(const int K, WaveLds &L, float v,
                 const uint64_t ret = ballot(tie && st.yc < 0);
                 if (ret) {
                     const int kk = first_lane(ret);
-                    if (better && lane <= kk) {
+                    // compact stops before relaxing column kk itself (only its
+                    // pred is set); that d is never read again either way
+                    if (better && (COMPACT ? lane < kk : lane <= kk))
                         st.d = r;
+                    if (better && lane <= kk)
                         st.pr = iq;
-                    }
                     final_j = readlane_i(st.col, kk);
                     early = true;
                     break;
@@ -863,7 +885,7 @@ __device__ __forceinline__ bool wave_solve(const int K, WaveLds &L, float v,
         // dual update of the columns made ready before the last level
         const float level = readlane_f(st.d, lo);
         if (live && lane < n_ready)
-            st.vc += st.d - level;
+            st.vc = COMPACT ? (st.vc + st.d) - level : st.vc + (st.d - level);
         if (live) {
             L.vbuf[st.col] = st.vc;
             L.pbuf[st.col] = st.pr;
@@ -894,262 +916,12 @@ __device__ __forceinline__ bool wave_solve(const int K, WaveLds &L, float v,
 }
 
 // ---------------------------------------------------------------------------
-// 3. compact variant (assignment::jonker_compact_batch), K <= 64
+// 3. the solve kernel (dense and compact), K <= 64
 // ---------------------------------------------------------------------------
 // jonker_compact_core.h:51-252 solves the same padded square problem as the
 // dense solver with its own tie and ordering rules (listed in jv_compact.h),
-// so its mappings differ on ties.  On the wave path every cost is below
-// LARGE, so the dense path's column minima and claims are the same and the
-// column reduction is shared; the rest follows the compact rules.
-
-// find_umins_regular (jonker_compact_core.h:20-43) on the wave: j1 is the
-// first index of the smallest reduced cost, j2 the next column in (value,
-// index) order, u1 / u2 their values.  Valid when every reduced cost is below
-// FLT_MAX (the wave path's range guarantees it).
-__device__ __forceinline__ TwoMin compact_two_min(float r, bool live) {
-    const int key = live ? fkey(r) : kKeyNone;
-    int k1, k2;
-    wave_min2_key(key, k1, k2);
-    k1 = uniform_i(k1);
-    k2 = uniform_i(k2);
-    const uint64_t at1 = ballot(key == k1);
-    TwoMin t;
-    t.j1 = first_lane(at1);
-    t.u1 = readlane_f(r, t.j1);
-    t.j2 = -1;
-    t.u2 = kFltMax;
-    if (k2 == k1)
-        t.j2 = first_lane(at1 & (at1 - 1));
-    else if (k2 != kKeyNone)
-        t.j2 = first_lane(ballot(key == k2));
-    if (t.j2 >= 0)
-        t.u2 = readlane_f(r, t.j2);
-    return t;
-}
-
-// Wave-parallel jonker_compact_kernel<int32_t, float> on the LDS tile.  Lane j
-// holds column j (v, y), lane i row i (x) and the free list (lane k =
-// free_rows[k]); augmentation keeps the column at position p of the search
-// order in lane p (PosState), as the dense path does.  Returns false when the
-// iteration guard trips.
-__device__ __forceinline__ bool wave_solve_compact(const int K, WaveLds &L, float v, int y,
-                                                   int &x_out) {
-    const int lane = lane_id();
-    const bool live = lane < K;
-
-    // ---- column reduction (:77-96): (v, y) = this column's minimum and first
-    // arg-min row; the largest column claiming a row keeps it
-    if (live) {
-        L.xmax[lane] = -1;
-        L.claims[lane] = 0;
-    }
-    __syncthreads();
-    if (live) {
-        atomicMax(&L.xmax[y], lane);
-        atomicAdd(&L.claims[y], 1);
-    }
-    __syncthreads();
-    int x = live ? L.xmax[lane] : -1;               // lane = row
-    const bool once = live && L.claims[lane] == 1;  // claimed exactly once
-    if (live && L.xmax[y] != lane)
-        y = -1;                                     // lane = column
-    if (!live) {
-        v = finf();
-        y = -1;
-    }
-
-    // ---- reduction transfer (:98-117), rows in increasing order ----
-    int fr = 0;  // lane k holds free_rows[k]
-    int n_free = 0;
-    {
-        uint64_t m = ballot(live && x < 0);
-        while (m) {
-            const int row = first_lane(m);
-            m &= m - 1;
-            if (lane == n_free)
-                fr = row;
-            ++n_free;
-        }
-        const int max_key = fkey(kFltMax);
-        uint64_t t = ballot(once);
-        while (t) {
-            const int i = first_lane(t);
-            t &= t - 1;
-            const int own = readlane_i(x, i);
-            const float r = L.c[i * kTile + lane] - v;
-            const int key = (live && lane != own) ? fkey(r) : kKeyNone;
-            const int kmin = uniform_i(wave_min_key(key));
-            float mn = kFltMax;
-            if (kmin < max_key)
-                mn = readlane_f(r, first_lane(ballot(key == kmin)));
-            if (lane == own)
-                v = v - mn;
-        }
-    }
-
-    // ---- augmenting row reduction (:119-166) ----
-    const uint32_t guard = compact_arr_guard(K);
-    uint32_t steps = 0;
-    for (int round = 0; round < 2; ++round) {
-        const int n_prev = n_free;
-        int k = 0;
-        n_free = 0;
-        while (k < n_prev) {
-            const int i = readlane_i(fr, k++);
-            if (++steps > guard)
-                return false;
-            const float r = L.c[i * kTile + lane] - v;
-            const TwoMin t = compact_two_min(r, live);
-            int j1 = t.j1;
-            int i0 = readlane_i(y, j1);
-            const float vj1 = readlane_f(v, j1);
-            const float lowered = vj1 - (t.u2 - t.u1);
-            const bool lowers = lowered < vj1;
-            if (lowers) {
-                if (lane == j1)
-                    v = lowered;
-            } else if (i0 >= 0) {
-                j1 = t.j2;
-                if (j1 < 0)
-                    return false;  // only reachable outside the wave path's range
-                i0 = readlane_i(y, j1);
-            }
-            if (lane == i)
-                x = j1;
-            if (lane == j1)
-                y = i;
-            if (i0 >= 0) {
-                if (lowers) {
-                    --k;
-                    if (lane == k)
-                        fr = i0;
-                } else {
-                    if (lane == n_free)
-                        fr = i0;
-                    ++n_free;
-                }
-            }
-        }
-    }
-
-    // ---- augmentation (:168-251) ----
-    int pred_col = 0;  // lane = column
-    for (int f = 0; f < n_free; ++f) {
-        const int start = readlane_i(fr, f);
-        PosState st;
-        st.col = lane;
-        st.d = live ? (L.c[start * kTile + lane] - v) : finf();
-        st.pr = start;
-        st.yc = y;
-        st.vc = v;
-        int low = 0, up = 0, n_ready = 0;
-        float level = 0.f;
-        int end = -1;
-        while (end < 0) {
-            if (low >= K)
-                return false;  // no unassigned column reachable: cannot happen
-            if (up == low) {
-                // gather the columns at the new minimum into [low, up): a
-                // smaller d restarts the group at low, an equal one joins it
-                // (:185-199); events in position order from a prefix minimum
-                n_ready = low;
-                const bool act = live && lane >= low;
-                const int dkey = act ? fkey(st.d) : kKeyNone;
-                const int before = wave_shift_up_key(wave_prefix_min_key(dkey));
-                const bool later = act && lane > low;
-                const uint64_t rec = ballot(later && dkey < before);
-                const uint64_t tie = ballot(later && dkey == before);
-                uint64_t ev = rec | tie;
-                up = low + 1;
-                while (ev) {
-                    const int kk = first_lane(ev);
-                    ev &= ev - 1;
-                    if ((rec >> kk) & 1ull) {
-                        swap_lanes(st, kk, low);
-                        up = low + 1;
-                    } else {
-                        if (kk != up)
-                            swap_lanes(st, kk, up);
-                        ++up;
-                    }
-                }
-                level = readlane_f(st.d, low);
-                // the first unassigned column of the group ends the path (:200-206)
-                const uint64_t open = ballot(live && lane >= low && lane < up && st.yc < 0);
-                if (open)
-                    end = readlane_i(st.col, first_lane(open));
-            }
-            if (end >= 0)
-                break;
-            // scan the row of the group's next column (:209-233)
-            const int q = low++;
-            const int jq = readlane_i(st.col, q);
-            const int iq = readlane_i(st.yc, q);
-            if (iq < 0)
-                return false;  // group columns are assigned: cannot happen
-            const float vq = readlane_f(st.vc, q);
-            const float h = L.c[iq * kTile + jq] - vq - level;
-            const bool act = live && lane >= up;
-            const float cp = act ? L.c[iq * kTile + st.col] : 0.f;
-            const float r = cp - st.vc - h;
-            const bool better = act && r < st.d;
-            const bool tie = better && r == level;
-            const uint64_t ret = ballot(tie && st.yc < 0);
-            if (ret) {
-                // the reference stops at the first such column in position
-                // order: columns before it are relaxed, it only gets its pred
-                const int kk = first_lane(ret);
-                if (better && lane < kk)
-                    st.d = r;
-                if (better && lane <= kk)
-                    st.pr = iq;
-                end = readlane_i(st.col, kk);
-                break;
-            }
-            if (better) {
-                st.d = r;
-                st.pr = iq;
-            }
-            uint64_t tm = ballot(tie);
-            while (tm) {
-                const int kk = first_lane(tm);
-                tm &= tm - 1;
-                if (kk != up)
-                    swap_lanes(st, kk, up);
-                ++up;
-            }
-        }
-        // duals of the columns finished before the last group (:236-239)
-        if (live && lane < n_ready)
-            st.vc = st.vc + st.d - level;
-        if (live) {
-            L.vbuf[st.col] = st.vc;
-            L.pbuf[st.col] = st.pr;
-        }
-        __syncthreads();
-        if (live) {
-            v = L.vbuf[lane];
-            pred_col = L.pbuf[lane];
-        }
-        __syncthreads();
-        // flip the assignment along the predecessors (:241-250)
-        int j = end, i;
-        int hops = 0;
-        do {
-            i = readlane_i(pred_col, j);
-            if (lane == j)
-                y = i;
-            const int prev = readlane_i(x, i);
-            if (lane == i)
-                x = j;
-            j = prev;
-            if (++hops > K)
-                return false;
-        } while (i != start);
-    }
-    x_out = x;
-    return true;
-}
+// so its mappings differ on ties.  wave_solve<true> above follows them on the
+// wave path; inputs outside its range take compact_serial (jv_compact.h).
 
 // One problem per 64-lane workgroup; COMPACT selects the solver of
 // assignment::jonker_compact_batch instead of jonker_dense_batch (same
@@ -1238,7 +1010,8 @@ jv_solve_kernel(const float *__restrict__ costs, int64_t B, int N, int M,
     int x = -1;
     if constexpr (COMPACT) {
         if (fast) {
-            if (!wave_solve_compact(K, L, vmin, ymin, x)) {
+            const bool chain = K >= 2 && (flags & kJvFlagNegZero) == 0;
+            if (!wave_solve<true>(K, L, vmin, ymin, chain, x)) {
                 if (lane == 0)
                     atomicOr(&status[1], 1u);
                 x = -1;
@@ -1257,7 +1030,7 @@ jv_solve_kernel(const float *__restrict__ costs, int64_t B, int N, int M,
         // displacement chains need K >= 2 and no -0.0 (their second minimum is
         // read back from its key, which maps -0.0 to +0.0)
         const bool chain = K >= 2 && (flags & kJvFlagNegZero) == 0;
-        if (!wave_solve(K, L, vmin, ymin, chain, x)) {
+        if (!wave_solve<false>(K, L, vmin, ymin, chain, x)) {
             if (lane == 0)
                 atomicOr(&status[1], 1u);
             x = -1;
