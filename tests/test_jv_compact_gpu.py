@@ -76,6 +76,9 @@ def _random_batch(rng, kind: str, b: int, n: int, m: int) -> np.ndarray:
         c = (rng.random((b, n, m), dtype=np.float32) - 0.7) * 100.0
     elif kind == "huge":  # beyond 1e15: lane-serial path
         c = rng.random((b, n, m), dtype=np.float32) * np.float32(3e16)
+    elif kind == "big":  # 1e12 .. 1e15: serial for compact, wave path for dense
+        c = rng.random((b, n, m), dtype=np.float32) * np.float32(5e13)
+        c[rng.random((b, n, m)) < 0.1] = np.inf
     elif kind == "signed_zero":
         c = rng.integers(-1, 2, (b, n, m)).astype(np.float32) * np.float32(0.0)
         c[rng.random((b, n, m)) < 0.5] = np.float32(1.0)
@@ -84,7 +87,7 @@ def _random_batch(rng, kind: str, b: int, n: int, m: int) -> np.ndarray:
     return c
 
 
-KINDS = ["uniform", "tied", "masked", "tied_masked", "negative", "huge", "signed_zero"]
+KINDS = ["uniform", "tied", "masked", "tied_masked", "negative", "huge", "big", "signed_zero"]
 
 
 @pytest.mark.parametrize("kind", KINDS)
@@ -102,7 +105,8 @@ def test_random_batches_match_oracle(kind, device):
         assert mism.size == 0, f"{kind} {(b, n, m)}: {mism.size} problems differ"
 
 
-@pytest.mark.parametrize("kind", ["uniform", "tied", "masked", "tied_masked", "negative", "huge"])
+@pytest.mark.parametrize("kind", ["uniform", "tied", "masked", "tied_masked", "negative", "huge",
+                                  "big"])
 def test_large_k_match_oracle(kind, device):
     """64 < K <= 1024: the large-K compact kernel (and its lane-serial path for
     huge magnitudes)."""
@@ -110,7 +114,7 @@ def test_large_k_match_oracle(kind, device):
         pytest.skip("no large-K compact kernel in this build")
     rng = np.random.default_rng(zlib.crc32(b"compact-large-" + kind.encode()))
     shapes = [(16, 65, 65), (8, 100, 130), (8, 130, 100), (6, 300, 300), (3, 700, 768)]
-    if kind != "huge":
+    if kind not in ("huge", "big"):
         shapes.append((2, 1024, 1000))
     for b, n, m in shapes:
         c = _random_batch(rng, kind, b, n, m)

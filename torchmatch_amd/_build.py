@@ -31,8 +31,7 @@ CABI_SO = LIB_DIR / "libtorchmatch_amd.so"
 OPS_SO = PKG / "_C.so"
 PROBE_SO = LIB_DIR / "libtm_lds_probe.so"
 
-HIP_SOURCES = ["jv_batch.hip", "jv_large.hip", "jv_compact_large.hip", "jv_unpack.hip",
-               "sinkhorn.hip"]
+HIP_SOURCES = ["jv_batch.hip", "jv_large.hip", "jv_unpack.hip", "sinkhorn.hip"]
 ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
 ARCH = "gfx950"
 

@@ -38,7 +38,7 @@ int launch_jv_large(const float *costs, int64_t B, int N, int M, const JvStats *
 int jv_large_max_k();
 
 // Compact solver (assignment::jonker_compact_batch) for K in (64,
-// jv_compact_max_k()] (jv_compact_large.hip).
+// jv_compact_max_k()] (jv_large.hip).
 int launch_jv_compact_large(const float *costs, int64_t B, int N, int M,
                             const JvStats *partial, int n_partial, int64_t *out,
                             uint32_t *status, hipStream_t stream);

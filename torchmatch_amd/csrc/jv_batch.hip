@@ -1009,7 +1009,7 @@ jv_solve_kernel(const float *__restrict__ costs, int64_t B, int N, int M,
 
     int x = -1;
     if constexpr (COMPACT) {
-        if (fast) {
+        if (fast && compact_wave_range(any_finite, mx, mn, has_inf, sentinel)) {
             const bool chain = K >= 2 && (flags & kJvFlagNegZero) == 0;
             if (!wave_solve<true>(K, L, vmin, ymin, chain, x)) {
                 if (lane == 0)

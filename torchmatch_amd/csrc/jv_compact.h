@@ -1,5 +1,5 @@
 // jv_compact.h -- pieces of the compact JV solver shared by the K <= 64
-// (jv_batch.hip) and 64 < K <= 1024 (jv_compact_large.hip) kernels.
+// (jv_batch.hip) and 64 < K <= 1024 (jv_large.hip) kernels.
 //
 // jonker_compact_core.h:20-252 (torchmatch's square JV behind the CPU op
 // assignment::jonker_compact_batch) has its own tie and ordering rules:
@@ -14,6 +14,7 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+#include <math.h>
 #include <stdint.h>
 
 namespace tmamd {
@@ -26,6 +27,20 @@ constexpr float kFltMax = 3.402823466e38f;  // numeric_limits<float>::max()
 // is reported instead of spinning.
 __device__ __forceinline__ uint32_t compact_arr_guard(int K) {
     return 8u * (uint32_t)K * (uint32_t)K + 65536u;
+}
+
+// The compact solver runs on the dense wave solvers (with its switches) when
+// every cost of the padded tile, the +inf sentinel included, lies within
+// +-1e12: the duals then stay far below LARGE (1e18), where the dense code's
+// LARGE-specific branches would part from the compact rules (FLT_MAX seeds).
+// Other inputs take compact_serial below.
+constexpr float kCompactWaveRange = 1e12f;
+
+__device__ __forceinline__ bool compact_wave_range(bool any_finite, float mx, float mn,
+                                                   bool has_inf, float sentinel) {
+    if (any_finite && (mx > kCompactWaveRange || mn < -kCompactWaveRange))
+        return false;
+    return !has_inf || fabsf(sentinel) <= kCompactWaveRange;
 }
 
 // Lane-serial transcription of jonker_compact_kernel<int32_t, float>

@@ -3,7 +3,9 @@
 // Same contract as the K <= 64 kernel in jv_batch.hip: the int64 row->col
 // mapping of torchmatch's CPU `jonker_dense_batch` bit for bit
 // (sources/torchmatch/assignment/cpu/ops.cpp:176-289,
-//  sources/torchmatch/assignment/cpu/jonker_dense_flat.h:27-274).
+//  sources/torchmatch/assignment/cpu/jonker_dense_flat.h:27-274), and with
+// COMPACT that of `jonker_compact_batch` (ops.cpp:431-433 around
+// jonker_compact_core.h:20-252; its rules are listed in jv_compact.h).
 //
 // One 64-lane workgroup per problem.  A K x K tile no longer fits in LDS, so
 // the cost is read from global memory (L2 / Infinity Cache) through a view
@@ -22,6 +24,7 @@
 
 #include "jv_batch.h"
 #include "jv_common.h"
+#include "jv_compact.h"
 #include "wave.h"
 
 namespace tmamd {
@@ -354,6 +357,13 @@ __device__ void scan_row(LargeLds &L, const CostView &C, int fi, int E, int K,
     }
 }
 
+// COMPACT = false: jonker_dense_flat.h:124-274; COMPACT = true:
+// jonker_compact_core.h:51-252 (only called on its value range, where every
+// reduced cost stays far below LARGE): the same steps with no cap on the
+// augmenting row reduction, the first unassigned column of a minimum group
+// ending a path, the dual update (v + d) - min and FLT_MAX as the transfer's
+// starting minimum.
+template <bool COMPACT>
 __device__ bool large_solve(const int K, const int E, LargeLds &L, const CostView &C) {
     const int lane = lane_id();
 
@@ -453,8 +463,9 @@ __device__ bool large_solve(const int K, const int E, LargeLds &L, const CostVie
             }
             best = uniform_i(wave_min_key(best));
             lds_sync();
-            float mn = kLarge;
-            if (best < fkey(kLarge)) {
+            const float start_min = COMPACT ? kFltMax : kLarge;
+            float mn = start_min;
+            if (best < fkey(start_min)) {
                 for (int e2 = 0; e2 < E; ++e2) {
                     const int j = e2 * 64 + lane;
                     const uint64_t hit = ballot(j < K && j != own && fkey(L.rbuf[j]) == best);
@@ -471,7 +482,8 @@ __device__ bool large_solve(const int K, const int E, LargeLds &L, const CostVie
     }
 
     // ---- augmenting row reduction (carr_dense, jonker_dense_flat.h:178-235) ----
-    const uint32_t rr_limit = 4u * (uint32_t)K * (uint32_t)K + 64u;
+    const uint32_t rr_limit =
+        COMPACT ? compact_arr_guard(K) : 4u * (uint32_t)K * (uint32_t)K + 64u;
     for (int i = lane; i < K; i += 64)
         L.ctau[i] = -finf();
     float *cbuf = reinterpret_cast<float *>(L.ev);  // row costs of the last scan
@@ -539,7 +551,7 @@ __device__ bool large_solve(const int K, const int E, LargeLds &L, const CostVie
             const float vj1 = L.v[j1];
             const float lowered = vj1 - (u2 - u1);
             const bool lowers = lowered < vj1;
-            const bool cap = rr < cur * (uint32_t)K;
+            const bool cap = COMPACT || rr < cur * (uint32_t)K;
             if (cap && !lowers && i0 >= 0 && j2 >= 0) {
                 jsel = j2;
                 i0 = L.y[j2];
@@ -611,6 +623,7 @@ __device__ bool large_solve(const int K, const int E, LargeLds &L, const CostVie
         }
         lds_sync();
         int lo = 0, hi = 0, n_ready = 0, final_j = -1;
+        float group_level = 0.f;  // d of the current minimum group
         while (final_j < 0) {
             if (lo >= K)
                 return false;
@@ -657,31 +670,50 @@ __device__ bool large_solve(const int K, const int E, LargeLds &L, const CostVie
                     // never read again (the next path resets it).
                     const int c_lo = last_rec >= 0 ? (L.ev[last_rec] & 0x7fffffff) : 0;
                     int found = -1;
-                    for (int top = n_ev; top > last_rec + 1 && found < 0; top -= 64) {
-                        const int k = top - 64 + lane;
-                        const bool ok = k > last_rec && k < top && L.y[L.ev[max(k, 0)]] < 0;
-                        const uint64_t open = ballot(ok);
-                        if (open)
-                            found = L.ev[top - 64 + last_lane(open)];
+                    if (COMPACT) {
+                        // the first unassigned column of the block ends the path
+                        if (L.y[c_lo] < 0)
+                            found = c_lo;
+                        for (int k0 = last_rec + 1; k0 < n_ev && found < 0; k0 += 64) {
+                            const int k = k0 + lane;
+                            const bool ok = k < n_ev && L.y[L.ev[min(k, n_ev - 1)]] < 0;
+                            const uint64_t open = ballot(ok);
+                            if (open)
+                                found = L.ev[k0 + first_lane(open)];
+                        }
+                    } else {
+                        for (int top = n_ev; top > last_rec + 1 && found < 0; top -= 64) {
+                            const int k = top - 64 + lane;
+                            const bool ok = k > last_rec && k < top && L.y[L.ev[max(k, 0)]] < 0;
+                            const uint64_t open = ballot(ok);
+                            if (open)
+                                found = L.ev[top - 64 + last_lane(open)];
+                        }
+                        if (found < 0 && L.y[c_lo] < 0)
+                            found = c_lo;
                     }
-                    if (found < 0 && L.y[c_lo] < 0)
-                        found = c_lo;
                     if (found >= 0) {
                         final_j = found;
                         break;
                     }
                 }
                 hi = replay_find_events(L, n_ev, lo);
-                // the LAST unassigned column of the tied block wins
-                int last = -1;
+                group_level = L.d[L.cols[lo]];
+                // dense: the LAST unassigned column of the tied block wins
+                // (jonker_dense_flat.h:96-103); compact: the first
+                // (jonker_compact_core.h:200-206)
+                int pick = -1;
                 for (int base = lo; base < hi; base += 64) {
                     const int p = base + lane;
                     const uint64_t open = ballot(p < hi && L.y[L.cols[p]] < 0);
-                    if (open)
-                        last = base + last_lane(open);
+                    if (open) {
+                        pick = base + (COMPACT ? first_lane(open) : last_lane(open));
+                        if (COMPACT)
+                            break;
+                    }
                 }
-                if (last >= 0)
-                    final_j = L.cols[last];
+                if (pick >= 0)
+                    final_j = L.cols[pick];
             }
             if (final_j >= 0)
                 break;
@@ -692,7 +724,9 @@ __device__ bool large_solve(const int K, const int E, LargeLds &L, const CostVie
                 const int q = slo++;
                 const int jq = L.cols[q];
                 const int iq = L.y[jq];
-                const float level = L.d[jq];
+                // the group's common d: compact uses the level of its
+                // gathering, dense the scanned column's own d (equal values)
+                const float level = COMPACT ? group_level : L.d[jq];
                 int n_ev = 0;
                 const int base0 = shi;
                 // gather row iq at column jq and at the columns of positions
@@ -740,10 +774,11 @@ __device__ bool large_solve(const int K, const int E, LargeLds &L, const CostVie
                     const uint64_t ret = ballot(tie && L.y[jp] < 0);
                     if (ret) {
                         const int kk = first_lane(ret);
-                        if (better && lane <= kk) {
+                        // compact stops before relaxing column kk itself
+                        if (better && (COMPACT ? lane < kk : lane <= kk))
                             L.d[jp] = r;
+                        if (better && lane <= kk)
                             L.pred[jp] = iq;
-                        }
                         final_j = readlane_i(jp, kk);
                         early = true;
                         break;
@@ -771,7 +806,7 @@ __device__ bool large_solve(const int K, const int E, LargeLds &L, const CostVie
             const int p = base + lane;
             if (p < n_ready) {
                 const int j = L.cols[p];
-                L.v[j] += L.d[j] - level;
+                L.v[j] = COMPACT ? (L.v[j] + L.d[j]) - level : L.v[j] + (L.d[j] - level);
             }
         }
         lds_sync();
@@ -793,6 +828,7 @@ __device__ bool large_solve(const int K, const int E, LargeLds &L, const CostVie
     return true;
 }
 
+template <bool COMPACT>
 __global__ void __launch_bounds__(64)
 jv_solve_large_kernel(const float *__restrict__ costs, int64_t B, int N, int M,
                       const JvStats *__restrict__ partial, int n_partial,
@@ -819,7 +855,23 @@ jv_solve_large_kernel(const float *__restrict__ costs, int64_t B, int N, int M,
     C.N = N;
     C.M = M;
     C.sentinel = any_finite ? (mx + 1.0f) * (float)(K + 1) : 1.0f;
-    if (!large_solve(K, E, L, C)) {
+    bool ok;
+    if (!COMPACT || compact_wave_range(any_finite, mx, mn, (flags & kJvFlagPosInf) != 0,
+                                       C.sentinel)) {
+        ok = large_solve<COMPACT>(K, E, L, C);
+    } else {
+        // compact outside the wave path's range: the lane-serial transcription
+        if (lane == 0) {
+            auto cost = [C](int i, int j) {
+                return (i >= C.N || j >= C.M) ? 0.f : fix_cost(C, C.src[(int64_t)i * C.M + j], j);
+            };
+            L.ev[0] = compact_serial((uint32_t)K, cost, L.x, L.y, L.fr, L.pred, L.cols, L.v,
+                                     L.d) ? 1 : 0;
+        }
+        lds_sync();
+        ok = L.ev[0] != 0;
+    }
+    if (!ok) {
         if (lane == 0)
             atomicOr(&status[1], 1u);
         for (int i = lane; i < N; i += 64)
@@ -836,11 +888,21 @@ jv_solve_large_kernel(const float *__restrict__ costs, int64_t B, int N, int M,
 
 int launch_jv_large(const float *costs, int64_t B, int N, int M, const JvStats *partial,
                     int n_partial, int64_t *out, uint32_t *status, hipStream_t stream) {
-    hipLaunchKernelGGL(jv_solve_large_kernel, dim3((unsigned)B), dim3(64), 0, stream, costs, B,
-                       N, M, partial, n_partial, out, status);
+    hipLaunchKernelGGL(jv_solve_large_kernel<false>, dim3((unsigned)B), dim3(64), 0, stream,
+                       costs, B, N, M, partial, n_partial, out, status);
+    return hipGetLastError() == hipSuccess ? kTmOk : kTmErrLaunch;
+}
+
+int launch_jv_compact_large(const float *costs, int64_t B, int N, int M,
+                            const JvStats *partial, int n_partial, int64_t *out,
+                            uint32_t *status, hipStream_t stream) {
+    hipLaunchKernelGGL(jv_solve_large_kernel<true>, dim3((unsigned)B), dim3(64), 0, stream,
+                       costs, B, N, M, partial, n_partial, out, status);
     return hipGetLastError() == hipSuccess ? kTmOk : kTmErrLaunch;
 }
 
 int jv_large_max_k() { return kMaxLargeK; }
+
+int jv_compact_max_k() { return kMaxLargeK; }
 
 } // namespace tmamd
