@@ -3,7 +3,7 @@
 // Reproduces the int64 row->col mapping of torchmatch's CPU
 // `assignment::jonker_dense_batch` bit for bit, and that of
 // `assignment::jonker_compact_batch` (section 3 below; K > 64 runs in
-// jv_compact_large.hip):
+// jv_large.hip):
 //   sentinel + padding      sources/torchmatch/assignment/cpu/ops.cpp:67-93,176-289
 //   solver                  sources/torchmatch/assignment/cpu/jonker_dense_flat.h:27-274
 //   compact solver          sources/torchmatch/assignment/cpu/jonker_compact_core.h:20-252
