@@ -60,6 +60,12 @@ def test_schemas_match_reference():
         "assignment::jonker_dense_batch_unpacked(Tensor costs) -> "
         "(Tensor, Tensor, Tensor, Tensor)"
     )
+    assert str(torch.ops.assignment.jonker_compact_batch.default._schema) == \
+        "assignment::jonker_compact_batch(Tensor costs) -> Tensor"
+    assert str(torch.ops.assignment.jonker_compact_batch_unpacked.default._schema) == (
+        "assignment::jonker_compact_batch_unpacked(Tensor costs) -> "
+        "(Tensor, Tensor, Tensor, Tensor)"
+    )
     assert str(torch.ops.transport.log_sinkhorn.default._schema) == (
         "transport::log_sinkhorn(Tensor cost, float eps, SymInt n_iter, Tensor a, Tensor b, "
         "Tensor? mask=None, float? scaling=None) -> Tensor"
@@ -79,6 +85,8 @@ def test_no_host_fallback():
     """CPU tensors are refused loudly: the package has no host path."""
     with pytest.raises(NotImplementedError):
         torch.ops.assignment.jonker_dense_batch(torch.rand(2, 3, 3))
+    with pytest.raises(NotImplementedError):
+        torch.ops.assignment.jonker_compact_batch(torch.rand(2, 3, 3))
     with pytest.raises(ValueError, match="ROCm"):
         torchmatch_amd.assignment.solve(torch.rand(2, 3, 3))
     with pytest.raises(NotImplementedError):
@@ -95,6 +103,10 @@ def test_fake_kernels():
         out = torch.ops.assignment.jonker_dense_batch(c)
         assert out.shape == (5, 7) and out.dtype == torch.long
         shapes = [t.shape for t in torch.ops.assignment.jonker_dense_batch_unpacked(c)]
+        assert shapes == [(5, 7, 2), (5, 7), (5, 9), (5,)]
+        out = torch.ops.assignment.jonker_compact_batch(c)
+        assert out.shape == (5, 7) and out.dtype == torch.long
+        shapes = [t.shape for t in torch.ops.assignment.jonker_compact_batch_unpacked(c)]
         assert shapes == [(5, 7, 2), (5, 7), (5, 9), (5,)]
         plan = torch.ops.transport.log_sinkhorn(c, 0.1, 3, torch.empty(5, 7), torch.empty(5, 9))
         assert plan.shape == (5, 7, 9)

@@ -1,7 +1,8 @@
-"""Direct access to the ``torch.ops.assignment.*`` op this package provides.
+"""Direct access to the ``torch.ops.assignment.*`` ops this package provides.
 
-Mirrors ``assignment/ops.py:17-28`` of the reference for the one op on the
-gfx950 path; the reference's other CPU / CUDA solvers are not part of it.
+Mirrors ``assignment/ops.py:17-28`` of the reference for the batched JV ops
+on the gfx950 path (device kernels of the same op names); the reference's
+single-problem and other CPU / CUDA solvers are not part of it.
 """
 
 from __future__ import annotations
@@ -12,6 +13,16 @@ from torchmatch_amd._loader import load as _load
 
 _load()
 
-jonker_dense_batch = torch.ops.assignment.jonker_dense_batch
+_OPS = torch.ops.assignment
 
-__all__ = ["jonker_dense_batch"]
+jonker_dense_batch = _OPS.jonker_dense_batch
+jonker_compact_batch = _OPS.jonker_compact_batch
+jonker_dense_batch_unpacked = _OPS.jonker_dense_batch_unpacked
+jonker_compact_batch_unpacked = _OPS.jonker_compact_batch_unpacked
+
+__all__ = [
+    "jonker_compact_batch",
+    "jonker_compact_batch_unpacked",
+    "jonker_dense_batch",
+    "jonker_dense_batch_unpacked",
+]
