@@ -49,9 +49,9 @@ JV_BYTES_PER_RELAXATION = 12
 # runs and commands are recorded in profiles/kernels_bench_default.md.
 MEASURED_TRAFFIC = {
     # jv_stats_kernel + jv_solve_kernel on C2
-    "jv_c2": int(((8213.5 + 8316.5) * 2 + 8.0 + 512.0) * 1024),
+    "jv_c2": int(((8229.5 + 8314.0) * 2 + 8.0 + 512.0) * 1024),
     # sk_row_sweep + sk_col_sweep + sk_col_merge per C4 iteration
-    "sinkhorn_c4": int(((132774.4 + 131633.1 + 419.5) * 2 + 256.1 + 512.0 + 128.0) * 1024),
+    "sinkhorn_c4": int(((132776.2 + 131627.1 + 415.5) * 2 + 256.1 + 512.0 + 128.0) * 1024),
 }
 
 
