@@ -168,3 +168,40 @@ def test_differs_from_dense_on_ties(device):
     np.testing.assert_array_equal(compact, jv.jv_compact_batch(c.numpy()))
     np.testing.assert_array_equal(dense, jv.jv_dense_batch(c.numpy()))
     assert (compact != dense).any(axis=1).sum() > 32
+
+
+def test_edge_contracts(device):
+    """Empty shapes, float64 (solved in float32, as the device JV op does),
+    non-contiguous input and the K limit, as for the dense op."""
+    for shape in [(0, 4, 4), (3, 0, 4), (3, 4, 0)]:
+        out = torch.ops.assignment.jonker_compact_batch(torch.empty(shape, device=device))
+        assert out.shape == shape[:2] and (out == -1).all()
+    c64 = torch.rand(32, 20, 20, dtype=torch.float64)
+    want = jv.jv_compact_batch(c64.to(torch.float32).numpy())
+    np.testing.assert_array_equal(run_op(c64, device), want)
+    with pytest.raises(RuntimeError, match="contiguous"):
+        torch.ops.assignment.jonker_compact_batch(
+            torch.rand(4, 8, 8, device=device).transpose(1, 2))
+    k = _max_k() + 1
+    with pytest.raises(RuntimeError, match="K"):
+        torch.ops.assignment.jonker_compact_batch(torch.rand(1, k, k, device=device))
+
+
+def test_c_abi_direct(device):
+    """The compact entry through the C ABI with raw device pointers."""
+    lib = _native.lib()
+    cost = workloads.integer_tied(128, 48, 64, seed=12, hi=3)
+    dc = cost.to(device)
+    out = torch.empty(128, 48, dtype=torch.int64, device=device)
+    ws_bytes = lib.tm_jv_workspace_bytes(128, 48, 64)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=device)
+    status = torch.zeros(2, dtype=torch.int32, device=device)
+    stream = torch.cuda.current_stream(device).cuda_stream
+    rc = lib.tm_jv_compact_batch_f32(dc.data_ptr(), 128, 48, 64, out.data_ptr(), ws.data_ptr(),
+                                     ws_bytes, status.data_ptr(), stream)
+    assert rc == _native.TM_OK
+    assert lib.tm_jv_check_status(status.data_ptr(), stream) == _native.TM_OK
+    np.testing.assert_array_equal(out.cpu().numpy(), jv.jv_compact_batch(cost.numpy()))
+    rc = lib.tm_jv_compact_batch_f32(dc.data_ptr(), 128, 48, 64, out.data_ptr(),
+                                     ws.data_ptr(), 8, status.data_ptr(), stream)
+    assert rc == _native.TM_ERR_WORKSPACE

@@ -211,3 +211,37 @@ def test_zero_size_potentials(device):
                                    return_potentials=True)
     assert plan.shape == (2, 0, 5) and f.shape == (2, 0)
     assert torch.equal(g, torch.zeros(2, 5, device=device))
+
+
+_GUARD_SCRIPT = """
+import sys
+sys.path.insert(0, {root!r})
+import torch
+import torchmatch_amd  # noqa: F401
+cost = torch.rand(2, 16, 16, device="cuda")
+a = torch.full((2, 16), 1 / 16, device="cuda")
+graph = torch.cuda.CUDAGraph()
+try:
+    with torch.cuda.graph(graph):
+        torch.ops.transport.log_sinkhorn(cost, 0.1, 5, a, a)
+except RuntimeError as exc:
+    message = str(exc)
+    print("GUARD_RAISED_OK" if "CUDA graph capture" in message else "WRONG: " + message)
+    sys.exit(0)
+print("GUARD_DID_NOT_RAISE")
+sys.exit(1)
+"""
+
+
+def test_graph_capture_guard(device):
+    """The validation readback cannot run under stream capture: the op says
+    so (as the JV op does, assignment/cuda/dispatch.cu:97-106) instead of
+    failing inside the capture."""
+    import subprocess
+    import sys
+    from pathlib import Path
+
+    root = str(Path(__file__).resolve().parents[1])
+    res = subprocess.run([sys.executable, "-c", _GUARD_SCRIPT.format(root=root)],
+                         capture_output=True, text=True, timeout=120)
+    assert "GUARD_RAISED_OK" in res.stdout, f"{res.stdout!r} {res.stderr[-2000:]!r}"
