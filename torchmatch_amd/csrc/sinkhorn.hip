@@ -28,10 +28,10 @@
 // is an exact two-pass LSE over registers (max, then sum of exp); longer rows
 // are split over the waves of a block, one 256*NV-column chunk per wave, whose
 // (max, sum) pairs merge in LDS.  Column sweep: a block owns a column strip over a
-// chunk of rows; 16 threads span the 64-column strip with float4 loads, 16
-// row groups fold rows online (one rescale per group of U rows), and an LDS
-// merge of the row groups yields the column LSE (or a partial when rows are
-// chunked).
+// chunk of rows; 16 threads span a 64-column strip (8 a 32-column one) with
+// float4 loads, 16 (32) row groups fold rows online (one rescale per group of
+// U rows), and an LDS merge of the row groups yields the column LSE (or a
+// partial when rows are chunked).
 // exp / log run on the native v_exp_f32 / v_log_f32 (base 2).
 #include <hip/hip_runtime.h>
 #include <math.h>
@@ -50,6 +50,8 @@ constexpr int kRowsPerWave = 1;       // rows per wave (occupancy beats log_v re
 constexpr int kRowNV = 8;             // float4 per lane per row chunk (2048 cols)
 constexpr int kColThreads = 256;      // column-sweep block: strip threads x row groups
 constexpr int kColStrip = 64;         // strip width (columns): 16 threads x 16 row groups
+constexpr int kColStripNarrow = 32;   // narrow strip: 8 threads x 32 row groups
+constexpr int64_t kColNarrowBlocks = 4 * 256;  // narrow strips when they fill this many
 constexpr int64_t kColBlocksTarget = 5 * 256;  // column-sweep blocks to aim for
 constexpr int kColU = 8;              // rows per group fold
 constexpr float kLog2e = 1.4426950408889634f;
@@ -112,7 +114,7 @@ __device__ __forceinline__ float update_potential(float lse, float log_marg, flo
 
 struct SinkhornLayout {
     int64_t B, N, M;
-    int n_chunk, rows_per_chunk, n_strip;
+    int n_chunk, rows_per_chunk, n_strip, strip;
     size_t off_k, off_logmu, off_lognu, off_infrow, off_infcol, off_colpart, off_stats, total;
 };
 
@@ -123,10 +125,15 @@ SinkhornLayout make_layout(int64_t B, int64_t N, int64_t M) {
     L.B = B;
     L.N = N;
     L.M = M;
-    L.n_strip = (int)((M + kColStrip - 1) / kColStrip);
-    // split rows into chunks until the column sweep has about five blocks per
-    // CU (its 68 VGPRs allow seven; five measured best), keeping >= 256 rows
-    // per chunk
+    // 32-column strips when they alone give the column sweep about four
+    // blocks per CU (no row chunks, so no merge pass: C4 runs 81 us per
+    // iteration instead of 83), else 64-column strips split into row chunks
+    // until there are about five blocks per CU (68 VGPRs allow seven; five
+    // measured best), keeping >= 256 rows per chunk
+    L.strip = B * ((M + kColStripNarrow - 1) / kColStripNarrow) >= kColNarrowBlocks
+                  ? kColStripNarrow
+                  : kColStrip;
+    L.n_strip = (int)((M + L.strip - 1) / L.strip);
     const int64_t blocks = B * L.n_strip;
     int64_t chunks = kColBlocksTarget / blocks;
     if (chunks < 1)
@@ -550,10 +557,11 @@ sk_row_sweep_scalar(const float *__restrict__ K, const float *__restrict__ log_v
 
 // ---- column sweep: log_v ----------------------------------------------------------
 
-// grid (n_strip, n_chunk, B).  Thread tc = tid % 16 owns columns
-// strip*64 + 4*tc .. +3, row group tg = tid / 16 folds rows chunk_start + tg,
-// + 16, ... .  With one chunk the block finishes the LSE and updates log_v;
-// otherwise it writes (max, sum) partials for sk_col_merge.
+// grid (n_strip, n_chunk, B), SW-column strips.  Thread tc = tid % (SW/4)
+// owns columns strip*SW + 4*tc .. +3, row group tg = tid / (SW/4) folds rows
+// chunk_start + tg, + G, ... (G = 256 / (SW/4) groups).  With one chunk the
+// block finishes the LSE and updates log_v; otherwise it writes (max, sum)
+// partials for sk_col_merge.
 template <bool VEC, int SW>
 __global__ void __launch_bounds__(kColThreads)
 sk_col_sweep(const float *__restrict__ K, const float *__restrict__ log_u,
@@ -921,16 +929,26 @@ extern "C" int tm_sinkhorn_iterate_f32(const float *cost, const uint8_t *keep, i
             else
                 TM_LAUNCH(sk_row_sweep_split<16>, split_grid, dim3(16 * 64), 0, stream, K, log_v,
                           log_mu, inf_row, log_u, N, M, damp, ub);
-            TM_LAUNCH((sk_col_sweep<true, kColStrip>), col_grid, dim3(kColThreads), 0, stream, K,
-                      log_u, log_nu, inf_col, log_v, colpart, N, M, L.rows_per_chunk, L.n_chunk,
-                      damp, unbalanced ? 1 : 0);
+            if (L.strip == kColStripNarrow)
+                TM_LAUNCH((sk_col_sweep<true, kColStripNarrow>), col_grid, dim3(kColThreads), 0,
+                          stream, K, log_u, log_nu, inf_col, log_v, colpart, N, M,
+                          L.rows_per_chunk, L.n_chunk, damp, unbalanced ? 1 : 0);
+            else
+                TM_LAUNCH((sk_col_sweep<true, kColStrip>), col_grid, dim3(kColThreads), 0,
+                          stream, K, log_u, log_nu, inf_col, log_v, colpart, N, M,
+                          L.rows_per_chunk, L.n_chunk, damp, unbalanced ? 1 : 0);
         } else {
             TM_LAUNCH(sk_row_sweep_scalar, dim3(grid_for(B * N, 4, 1 << 30)), dim3(256), 0,
                       stream, K, log_v, log_mu, inf_row, log_u, B, N, M, damp,
                       unbalanced ? 1 : 0);
-            TM_LAUNCH((sk_col_sweep<false, kColStrip>), col_grid, dim3(kColThreads), 0, stream, K,
-                      log_u, log_nu, inf_col, log_v, colpart, N, M, L.rows_per_chunk, L.n_chunk,
-                      damp, unbalanced ? 1 : 0);
+            if (L.strip == kColStripNarrow)
+                TM_LAUNCH((sk_col_sweep<false, kColStripNarrow>), col_grid, dim3(kColThreads), 0,
+                          stream, K, log_u, log_nu, inf_col, log_v, colpart, N, M,
+                          L.rows_per_chunk, L.n_chunk, damp, unbalanced ? 1 : 0);
+            else
+                TM_LAUNCH((sk_col_sweep<false, kColStrip>), col_grid, dim3(kColThreads), 0,
+                          stream, K, log_u, log_nu, inf_col, log_v, colpart, N, M,
+                          L.rows_per_chunk, L.n_chunk, damp, unbalanced ? 1 : 0);
         }
         if (L.n_chunk > 1)
             TM_LAUNCH(sk_col_merge, dim3(grid_for(B * M, kMapBlock, 1 << 30)), dim3(kMapBlock),
