@@ -84,8 +84,11 @@ size_t tm_jv_workspace_bytes(int64_t B, int32_t N, int32_t M);
  *   out        device, (B, N) int64: row -> column, -1 for rows matched into
  *              padding columns (N > M); identical to the reference CPU op
  *   workspace  device, >= tm_jv_workspace_bytes(B, N, M), any contents
- *   d_status   device, two uint32: [0] receives TM_JV_FLAG_* for the whole
- *              batch, [1] is non-zero if a solve hit its iteration guard
+ *   d_status   two uint32 the kernels write with plain stores: device
+ *              memory, or the device address of host-mapped pinned memory
+ *              (hipHostGetDevicePointer), which saves the copy-back; [0]
+ *              receives TM_JV_FLAG_* for the whole batch, [1] is non-zero if
+ *              a solve hit its iteration guard
  * The +inf sentinel (max finite + 1) * (K + 1) is computed on the device over
  * the whole batch, as the reference does; no host round trip happens inside.
  * If the batch holds NaN or -inf, `out` is filled with -1 and the flag is set:
@@ -111,6 +114,10 @@ int tm_jv_compact_batch_f32(const float *costs, int64_t B, int32_t N, int32_t M,
  * cuda_common.cuh:241-249).  Returns TM_OK, TM_ERR_NAN, TM_ERR_NEG_INF,
  * TM_ERR_INTERNAL or TM_ERR_HIP. */
 int tm_jv_check_status(const uint32_t *d_status, hipStream_t stream);
+
+/* The same verdict from status words already on the host (host-mapped
+ * d_status after the caller synchronised the stream).  No HIP call. */
+int tm_jv_status_code(const uint32_t *h_status);
 
 /* Unpack B packed mappings (the `out` of tm_jv_dense_batch_f32: row -> column
  * in [0, M) or -1) into the tuple of assignment::jonker_dense_batch_unpacked:

@@ -1013,7 +1013,7 @@ jv_solve_kernel(const float *__restrict__ costs, int64_t B, int N, int M,
             const bool chain = K >= 2 && (flags & kJvFlagNegZero) == 0;
             if (!wave_solve<true>(K, L, vmin, ymin, chain, x)) {
                 if (lane == 0)
-                    atomicOr(&status[1], 1u);
+                    raise_guard(status);
                 x = -1;
             }
         } else {
@@ -1021,7 +1021,7 @@ jv_solve_kernel(const float *__restrict__ costs, int64_t B, int N, int M,
             auto cost = [tile](int i, int j) { return tile[i * kTile + j]; };
             if (lane == 0 && !compact_serial((uint32_t)K, cost, S.x, S.y, S.fr, S.pred, S.cols,
                                              S.v, S.d))
-                atomicOr(&status[1], 1u);
+                raise_guard(status);
             __syncthreads();
             if (lane < K)
                 x = S.x[lane];
@@ -1032,7 +1032,7 @@ jv_solve_kernel(const float *__restrict__ costs, int64_t B, int N, int M,
         const bool chain = K >= 2 && (flags & kJvFlagNegZero) == 0;
         if (!wave_solve<false>(K, L, vmin, ymin, chain, x)) {
             if (lane == 0)
-                atomicOr(&status[1], 1u);
+                raise_guard(status);
             x = -1;
         }
     } else {
@@ -1130,6 +1130,18 @@ extern "C" int32_t tm_jv_max_k(void) { return jv_large_max_k(); }
 
 extern "C" int32_t tm_jv_compact_max_k(void) { return jv_compact_max_k(); }
 
+extern "C" int tm_jv_status_code(const uint32_t *h_status) {
+    if (h_status == nullptr)
+        return TM_ERR_INVALID_ARGUMENT;
+    if (h_status[1] != 0)
+        return TM_ERR_INTERNAL;
+    if (h_status[0] & kJvFlagNan)
+        return TM_ERR_NAN;
+    if (h_status[0] & kJvFlagNegInf)
+        return TM_ERR_NEG_INF;
+    return TM_OK;
+}
+
 extern "C" int tm_jv_check_status(const uint32_t *d_status, hipStream_t stream) {
     uint32_t words[2] = {0, 0};
     if (hipMemcpyAsync(words, d_status, sizeof(words), hipMemcpyDeviceToHost, stream) !=
@@ -1137,12 +1149,5 @@ extern "C" int tm_jv_check_status(const uint32_t *d_status, hipStream_t stream) 
         return TM_ERR_HIP;
     if (hipStreamSynchronize(stream) != hipSuccess)
         return TM_ERR_HIP;
-    const uint32_t flags = words[0];
-    if (words[1] != 0)
-        return TM_ERR_INTERNAL;
-    if (flags & kJvFlagNan)
-        return TM_ERR_NAN;
-    if (flags & kJvFlagNegInf)
-        return TM_ERR_NEG_INF;
-    return TM_OK;
+    return tm_jv_status_code(words);
 }

@@ -16,6 +16,13 @@ constexpr float kFastRange = 1e15f;  // wave paths valid for |cost| <= this
 
 __device__ __forceinline__ float finf() { return __int_as_float(0x7f800000); }
 
+// Raise the internal-error word of the status pair.  Every writer stores the
+// same value, so a plain store suffices; it also works when the status words
+// live in host-mapped pinned memory, where device atomics are not assumed.
+__device__ __forceinline__ void raise_guard(uint32_t *status) {
+    __hip_atomic_store(&status[1], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
 // Fold the per-block partials (uniform result in every lane of the wave).
 __device__ __forceinline__ void fold_stats(const JvStats *__restrict__ partial, int n_partial,
                                            float &mx, float &mn, uint32_t &flags) {

@@ -873,7 +873,7 @@ jv_solve_large_kernel(const float *__restrict__ costs, int64_t B, int N, int M,
     }
     if (!ok) {
         if (lane == 0)
-            atomicOr(&status[1], 1u);
+            raise_guard(status);
         for (int i = lane; i < N; i += 64)
             ob[i] = -1;
         return;

@@ -98,6 +98,29 @@ at::Tensor jv_batch_hip(const at::Tensor &costs, JvSolver solver, int64_t max_k,
     const at::Tensor cf = costs.scalar_type() == at::kFloat ? costs : costs.to(at::kFloat);
     const size_t ws_bytes = tm_jv_workspace_bytes(B, (int32_t)N, (int32_t)M);
     auto ws = at::empty({(int64_t)ws_bytes}, costs.options().dtype(at::kByte));
+    // The status words go to pinned host memory the kernels write directly,
+    // so the readback is the stream synchronisation alone (no copy command);
+    // device memory and a copy when the pinned block cannot be mapped.
+    auto hstatus = at::empty({2}, at::TensorOptions().dtype(at::kInt).pinned_memory(true));
+    void *mapped = nullptr;
+    if (hipHostGetDevicePointer(&mapped, hstatus.data_ptr(), 0) != hipSuccess) {
+        (void)hipGetLastError();
+        mapped = nullptr;
+    }
+    if (mapped != nullptr) {
+        int rc = solver(cf.data_ptr<float>(), B, (int32_t)N, (int32_t)M,
+                        out.data_ptr<int64_t>(), ws.data_ptr(), ws_bytes,
+                        static_cast<uint32_t *>(mapped), stream);
+        // synchronise before any error leaves: a launched kernel must not
+        // write the pinned words after they went back to the allocator
+        const hipError_t se = hipStreamSynchronize(stream);
+        check_rc(rc, op_name);
+        TORCH_CHECK(se == hipSuccess, op_name, ": stream synchronisation failed: ",
+                    hipGetErrorString(se));
+        rc = tm_jv_status_code(reinterpret_cast<const uint32_t *>(hstatus.data_ptr<int32_t>()));
+        check_rc(rc, op_name);
+        return out;
+    }
     auto status = at::empty({2}, costs.options().dtype(at::kInt));
     int rc = solver(cf.data_ptr<float>(), B, (int32_t)N, (int32_t)M, out.data_ptr<int64_t>(),
                     ws.data_ptr(), ws_bytes,
