@@ -50,8 +50,8 @@ JV_BYTES_PER_RELAXATION = 12
 MEASURED_TRAFFIC = {
     # jv_stats_kernel + jv_solve_kernel on C2
     "jv_c2": int(((8229.5 + 8314.0) * 2 + 8.0 + 512.0) * 1024),
-    # sk_row_sweep + sk_col_sweep + sk_col_merge per C4 iteration
-    "sinkhorn_c4": int(((132776.2 + 131627.1 + 415.5) * 2 + 256.1 + 512.0 + 128.0) * 1024),
+    # sk_row_sweep + sk_col_sweep (32-column strips, no merge) per C4 iteration
+    "sinkhorn_c4": int(((132773.2 + 131835.0) * 2 + 256.0 + 128.0) * 1024),
 }
 
 
