@@ -10,7 +10,7 @@ Produces, next to this file:
   (``csrc/lds_probe.hip``) that ``bench.py`` prices the JV kernels against;
   measurement support, not part of the C ABI.
 
-``python -m torchmatch_amd._build`` runs it; ``__graft_entry__.build()`` calls
+``python torchmatch_amd/_build.py`` runs it; ``__graft_entry__.build()`` calls
 :func:`build` too.  hipcc cross-compiles, so no GPU is needed.
 """
 

@@ -38,7 +38,7 @@ _state: dict[str, object] = {"loaded": False, "libs": []}
 
 
 class ExtensionMissingError(RuntimeError):
-    """The gfx950 extension was not built (run ``python -m torchmatch_amd._build``)."""
+    """The gfx950 extension was not built (run ``python torchmatch_amd/_build.py``)."""
 
 
 def _has_op(namespace: str, name: str) -> bool:
@@ -84,7 +84,7 @@ def load() -> None:
     if not OPS_SO.exists() or not CABI_SO.exists():
         msg = (
             f"torchmatch_amd native extension not found ({OPS_SO}, {CABI_SO}); "
-            "build it with `python -m torchmatch_amd._build` -- there is no "
+            "build it with `python torchmatch_amd/_build.py` -- there is no "
             "non-native fallback"
         )
         raise ExtensionMissingError(msg)

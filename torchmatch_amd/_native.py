@@ -87,7 +87,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
 @lru_cache(maxsize=1)
 def lib() -> ctypes.CDLL:
     if not CABI_SO.exists():
-        msg = f"{CABI_SO} is not built; run `python -m torchmatch_amd._build`"
+        msg = f"{CABI_SO} is not built; run `python torchmatch_amd/_build.py`"
         raise ExtensionMissingError(msg)
     handle = ctypes.CDLL(str(CABI_SO))
     for name, (restype, argtypes) in SIGNATURES.items():
