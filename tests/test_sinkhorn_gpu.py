@@ -54,7 +54,10 @@ CASES = [
     (3, 300, 200, 0.1, 100),
     (1, 130, 517, 0.05, 80),
     (2, 1024, 1024, 0.05, 60),
+    (3, 77, 1028, 0.05, 60),
+    (2, 200, 2048, 0.05, 60),
     # rows longer than one 2048-column chunk: several waves per row
+    (1, 100, 3000, 0.05, 40),
     (1, 48, 4100, 0.05, 40),
     (1, 32, 16384, 0.05, 30),
     (1, 16, 40000, 0.1, 20),
@@ -93,6 +96,48 @@ def test_unbalanced_matches_oracle(B, N, M, eps, n_iter, rho, device):
     pr = _plan_rel(plan, ref_plan)
     print(f"unbalanced {(B, N, M, eps, n_iter, rho)} plan rel {pr:.3e}", flush=True)
     assert pr <= REL_TOL
+
+
+# The step's two kernel shapes: one pass over K per step (row LSE, then the
+# same rows folded into per-column partials) and the two-sweep step ("0"); the
+# long-row pass in its 8-wave shape too.  Each is held to the oracle.
+STEP_SHAPES = [
+    # env value, (B, N, M); each case also holds all-+inf rows and columns
+    (None, (2, 150, 1500)),
+    ("0", (2, 150, 1500)),
+    (None, (1, 40, 12000)),
+    ("16x1x4", (1, 40, 12000)),
+    ("0", (1, 40, 12000)),
+]
+
+
+@pytest.mark.parametrize(("env", "shape"), STEP_SHAPES)
+def test_step_shapes_match_oracle(env, shape, device, monkeypatch):
+    if env is None:
+        monkeypatch.delenv("TORCHMATCH_AMD_SINKHORN_FUSED", raising=False)
+    else:
+        monkeypatch.setenv("TORCHMATCH_AMD_SINKHORN_FUSED", env)
+    B, N, M = shape
+    cost = workloads.sinkhorn_points(B, N, M, 8, seed=N + 7)
+    cost[0, 3, :] = float("inf")           # all-+inf row
+    cost[B - 1, :, 5] = float("inf")       # all-+inf column
+    cost[0, 9, M // 3: M // 2] = float("inf")
+    a = workloads.dirichlet(B, N, 1.0, seed=21)
+    b = workloads.dirichlet(B, M, 1.0, seed=22)
+    print(f"step shape env={env} {shape}", flush=True)
+    ref_plan, ref_f, ref_g, _, _ = sk.log_sinkhorn_plan(cost, eps=0.05, n_iter=40, a=a, b=b)
+    plan, f, g = solve(cost.to(device), reg=0.05, n_iter=40, a=a.to(device), b=b.to(device),
+                       unpack=True)
+    torch.cuda.synchronize()
+    pr, fr, gr = _plan_rel(plan, ref_plan), _rel(f, ref_f), _rel(g, ref_g)
+    print(f"  plan rel {pr:.3e}  f rel {fr:.3e}  g rel {gr:.3e}", flush=True)
+    assert pr <= REL_TOL and fr <= REL_TOL and gr <= REL_TOL
+    ref_u = sk.unbalanced_sinkhorn_plan(cost, eps=0.05, n_iter=40, rho=0.7, a=a, b=b * 1.3)[0]
+    plan_u = torch.ops.transport.unbalanced_sinkhorn(cost.to(device), 0.05, 40, 0.7,
+                                                     a.to(device), (b * 1.3).to(device))
+    pu = _plan_rel(plan_u, ref_u)
+    print(f"  unbalanced plan rel {pu:.3e}", flush=True)
+    assert pu <= REL_TOL
 
 
 def test_forbidden_cells_rows_and_columns(device):

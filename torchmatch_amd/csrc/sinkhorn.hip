@@ -36,6 +36,7 @@
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdint.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include "jv_batch.h"
@@ -115,10 +116,56 @@ __device__ __forceinline__ float update_potential(float lse, float log_marg, flo
 struct SinkhornLayout {
     int64_t B, N, M;
     int n_chunk, rows_per_chunk, n_strip, strip;
+    int fused;                   // FusedVariant of sk_fused_step, 0: two-sweep step
+    int fz_chunk, fz_rows;       // its row chunks per batch and rows per chunk
     size_t off_k, off_logmu, off_lognu, off_infrow, off_infcol, off_colpart, off_stats, total;
 };
 
 __host__ __device__ inline size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+
+// sk_fused_step instantiations: (W waves per row, RW row groups, NV float4
+// per lane), chosen by row length; resident blocks per CU from their VGPR use.
+enum FusedVariant { kFzNone = 0, kFz1x4x4, kFz1x4x8, kFz2x1x8, kFz4x1x8, kFz8x1x8, kFz16x1x4 };
+struct FusedShape {
+    int W, RW, NV, blocks_per_cu;
+};
+constexpr FusedShape kFusedShapes[] = {
+    {0, 0, 0, 0}, {1, 4, 4, 6}, {1, 4, 8, 3}, {2, 1, 8, 6}, {4, 1, 8, 3}, {8, 1, 8, 1},
+    {16, 1, 4, 1},
+};
+constexpr int kFusedMinRowsPerWave = 8;
+
+void choose_fused(SinkhornLayout &L) {
+    L.fused = kFzNone;
+    L.fz_chunk = L.fz_rows = 0;
+    const int64_t M = L.M;
+    if (M % 4 != 0 || M <= 512 || M > 16384)
+        return;
+    L.fused = M <= 1024 ? kFz1x4x4
+              : M <= 2048 ? kFz1x4x8
+              : M <= 4096 ? kFz2x1x8
+              : M <= 8192 ? kFz4x1x8
+                          : kFz8x1x8;
+    if (const char *env = getenv("TORCHMATCH_AMD_SINKHORN_FUSED")) {
+        // "0": the two-sweep step; "16x1x4": that long-row shape
+        if (strcmp(env, "0") == 0)
+            L.fused = kFzNone;
+        else if (strcmp(env, "16x1x4") == 0 && M > 8192)
+            L.fused = kFz16x1x4;
+        if (L.fused == kFzNone)
+            return;
+    }
+    const FusedShape &f = kFusedShapes[L.fused];
+    // one resident round of blocks over the 256 CUs, each wave >= 8 rows
+    int64_t chunks = (256 * (int64_t)f.blocks_per_cu) / L.B;
+    const int64_t max_chunks = L.N / ((int64_t)f.RW * kFusedMinRowsPerWave);
+    if (chunks > max_chunks)
+        chunks = max_chunks;
+    if (chunks < 1)
+        chunks = 1;
+    L.fz_rows = (int)((L.N + chunks - 1) / chunks);
+    L.fz_chunk = (int)((L.N + L.fz_rows - 1) / L.fz_rows);
+}
 
 SinkhornLayout make_layout(int64_t B, int64_t N, int64_t M) {
     SinkhornLayout L{};
@@ -142,6 +189,7 @@ SinkhornLayout make_layout(int64_t B, int64_t N, int64_t M) {
         --chunks;
     L.n_chunk = (int)chunks;
     L.rows_per_chunk = (int)((N + chunks - 1) / chunks);
+    choose_fused(L);
     size_t off = 0;
     L.off_k = off;
     off = align_up(off + sizeof(float) * (size_t)(B * N * M), 256);
@@ -154,8 +202,12 @@ SinkhornLayout make_layout(int64_t B, int64_t N, int64_t M) {
     L.off_infcol = off;
     off = align_up(off + (size_t)(B * M), 256);
     L.off_colpart = off;
-    if (L.n_chunk > 1)
-        off = align_up(off + sizeof(float2) * (size_t)B * L.n_chunk * (size_t)M, 256);
+    {
+        int64_t parts = L.n_chunk > 1 ? L.n_chunk : 0;
+        if (L.fused && L.fz_chunk > parts)
+            parts = L.fz_chunk;
+        off = align_up(off + sizeof(float2) * (size_t)B * (size_t)parts * (size_t)M, 256);
+    }
     L.off_stats = off;
     off += 256;
     L.total = off;
@@ -676,6 +728,322 @@ sk_col_merge(const float2 *__restrict__ colpart, const float *__restrict__ log_n
     log_v[t] = update_potential(lse, log_nu[t], log_v[t], damp, unbalanced != 0);
 }
 
+// ---- fused step: row sweep and column partials in one read of K ----------------------
+//
+// The column step of iteration s needs log_u of iteration s, which the row step
+// produces one row at a time; the row is still in registers when its new log_u
+// is known, so each row is folded into per-column (max, sum) accumulators right
+// there.  One step then reads K once (B*N*M*4 bytes) instead of twice.  The
+// column LSE of the step is the merge of the accumulators of every row chunk
+// (sk_col_merge_blk), launched after the pass; the next step's row sweep needs
+// that log_v, so the merge cannot move into the pass.
+//
+// Both LSEs work in base 2 on the native v_exp_f32: y = t*log2(e) comes from
+// one fma of K with the potential scaled once (log_v per column in LDS, log_u
+// per row), and
+//   row:    exact two-pass over the row in registers (max, then sum of 2^(y-max));
+//   column: one value at a time with one exp per value,
+//           d = y - m;  e = 2^(-|d|);  s = d > 0 ? s*e + 1 : s + e;  m = max(m, y),
+//           the exact running form of sum_k 2^(y_k - max); m starts at -FLT_MAX
+//           rather than -inf so that y - m is never (-inf) - (-inf).
+// Two exps per element at the transcendental unit's quarter rate make the pass
+// VALU-heavy, so the column fold avoids any rescaling pass.
+
+constexpr float kFltMaxNeg = -3.402823466e38f;
+
+// Clang vector (not HIP's float4 struct): arrays of it passed by reference to
+// the inlined helpers below stay in registers.
+typedef float vf4 __attribute__((ext_vector_type(4)));
+
+// base-2 log-sum-exp partial: m = max of y (may be +-inf), s = sum 2^(y - shift(m))
+__device__ __forceinline__ Lse lse2_merge(Lse p, Lse q) {
+    const float m = fmaxf(p.m, q.m);
+    const float sh = lse_shift(m);
+    const float a = (p.s == 0.f) ? 0.f : p.s * __builtin_amdgcn_exp2f(lse_shift(p.m) - sh);
+    const float c = (q.s == 0.f) ? 0.f : q.s * __builtin_amdgcn_exp2f(lse_shift(q.m) - sh);
+    return Lse{m, a + c};
+}
+
+// natural-log LSE of a base-2 partial
+__device__ __forceinline__ float lse2_value(Lse p) {
+    return (__builtin_amdgcn_logf(p.s) + lse_shift(p.m)) * kLn2;
+}
+
+// max without the NaN canonicalisation fmaxf costs on this target (two extra
+// v_max per call): v_maximum3_f32.  The values here are never NaN (the cost
+// is validated), and +-inf order as with fmaxf.
+__device__ __forceinline__ float fmax_nn(float a, float b) {
+    return __builtin_elementwise_maximum(a, b);
+}
+
+__device__ __forceinline__ void col_fold2(float &m, float &s, float y) {
+    const float d = y - m;
+    const float e = __builtin_amdgcn_exp2f(-fabsf(d));  // 0 for y = -inf
+    s = d > 0.f ? fmaf(s, e, 1.f) : s + e;
+    m = fmax_nn(m, y);
+}
+
+// All NV float4 of a row in flight at once: scalar row base + 32-bit lane
+// byte offsets (the saddr form of the load).  Lanes past the row end read its
+// last float4 again (offsets clamped); their log_v in LDS is -inf, which
+// keeps them out of the row LSE, and their column sums are never stored.
+template <int NV>
+__device__ __forceinline__ void fz_load(vf4 (&dst)[NV], const vf4 *__restrict__ row4,
+                                        const uint32_t (&qb)[NV]) {
+    const char *base = reinterpret_cast<const char *>(row4);
+#pragma unroll
+    for (int k = 0; k < NV; ++k)
+        dst[k] = *reinterpret_cast<const vf4 *>(base + qb[k]);
+}
+
+// One row (batch-flat index r) of the fused step: base-2 row LSE (the W waves
+// of a row merge their partials in LDS slot `par`), the log_u update, then the
+// column fold.  Returns the slot parity for the next row.
+template <int W, int NV>
+__device__ __forceinline__ int fz_row(const vf4 (&kk)[NV], const vf4 *lv_s,
+                                      float2 (*rowpart)[W], int par, int w, int lane,
+                                      int64_t r, const float *__restrict__ log_mu,
+                                      const uint8_t *__restrict__ inf_row,
+                                      float *__restrict__ log_u, float damp, int unbalanced,
+                                      float (&cm)[4 * NV], float (&cs)[4 * NV]) {
+    if (inf_row[r])
+        return par;  // lse = -inf: log_u keeps its value, and K is -inf on the row
+    // read before the row barrier: wave 0 rewrites log_u[r] after it
+    const float mu_r = log_mu[r], u_r = log_u[r];
+    float y[4 * NV];
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+        const vf4 lv = lv_s[(k * W + w) * 64 + lane];
+        y[4 * k + 0] = fmaf(kk[k].x, kLog2e, lv.x);
+        y[4 * k + 1] = fmaf(kk[k].y, kLog2e, lv.y);
+        y[4 * k + 2] = fmaf(kk[k].z, kLog2e, lv.z);
+        y[4 * k + 3] = fmaf(kk[k].w, kLog2e, lv.w);
+    }
+    float m = y[0];
+#pragma unroll
+    for (int k = 1; k < 4 * NV; ++k)
+        m = fmax_nn(m, y[k]);
+    m = wave_max_all(m);
+    const float sh = lse_shift(m);
+    float s = 0.f;
+#pragma unroll
+    for (int k = 0; k < 4 * NV; ++k)
+        s += __builtin_amdgcn_exp2f(y[k] - sh);
+    s = wave_sum_all(s);
+    Lse tot{m, s};
+    if constexpr (W > 1) {
+        if (lane == 0)
+            rowpart[par][w] = make_float2(m, s);
+        __syncthreads();
+        tot = Lse{rowpart[par][0].x, rowpart[par][0].y};
+#pragma unroll
+        for (int k = 1; k < W; ++k)
+            tot = lse2_merge(tot, Lse{rowpart[par][k].x, rowpart[par][k].y});
+        par ^= 1;
+    }
+    const float lu = update_potential(lse2_value(tot), mu_r, u_r, damp, unbalanced != 0);
+    if (w == 0 && lane == 0)
+        log_u[r] = lu;
+    const float lu2 = lu * kLog2e;
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+        col_fold2(cm[4 * k + 0], cs[4 * k + 0], fmaf(kk[k].x, kLog2e, lu2));
+        col_fold2(cm[4 * k + 1], cs[4 * k + 1], fmaf(kk[k].y, kLog2e, lu2));
+        col_fold2(cm[4 * k + 2], cs[4 * k + 2], fmaf(kk[k].z, kLog2e, lu2));
+        col_fold2(cm[4 * k + 3], cs[4 * k + 3], fmaf(kk[k].w, kLog2e, lu2));
+    }
+    return par;
+}
+
+// grid (n_chunk, B), block W*RW waves.  Rows of chunk c of batch b are
+// [c*rows_per_chunk, min(N, (c+1)*rows_per_chunk)).  A row spans W waves:
+// wave (g, w) of row group g owns float4 columns q = (k*W + w)*64 + lane,
+// k < NV, of rows i0 + g, i0 + g + RW, ...  With W > 1 the W (max, sum)
+// pairs of a row merge in LDS (one barrier per row, double-buffered slots;
+// RW = 1 then, so every wave of the block sees the same rows and the same
+// barriers).  With RW > 1 the row groups' column accumulators merge in LDS
+// after the last row.  DB: double-buffered rows.  colpart receives base-2
+// (max, sum) pairs.  Requires
+// M % 4 == 0, M <= 256*W*NV, 16-byte aligned K and log_v.
+template <int W, int RW, int NV, bool DB>
+__global__ void __launch_bounds__(W * RW * 64)
+sk_fused_step(const float *__restrict__ K, const float *__restrict__ log_v,
+              const float *__restrict__ log_mu, const uint8_t *__restrict__ inf_row,
+              float *__restrict__ log_u, float2 *__restrict__ colpart, int64_t N, int64_t M,
+              int rows_per_chunk, int n_chunk, float damp, int unbalanced) {
+    static_assert(W == 1 || RW == 1, "a row is split over waves only with one row group");
+    constexpr int MV = W * 64 * NV;  // float4 per row at most
+    __shared__ vf4 lv_s[MV];         // log_v * log2(e) of the batch, -inf past M
+    __shared__ float2 rowpart[2][W];
+    const int chunk = blockIdx.x;
+    const int64_t b = blockIdx.y;
+    // wave-uniform (readfirstlane): row addresses and loop bounds stay scalar
+    const int wid = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int w = wid % W, g = wid / W;
+    const int lane = lane_id();
+    const int64_t m4 = M / 4;
+    const int64_t i0 = (int64_t)chunk * rows_per_chunk;
+    const int64_t i1 = (i0 + rows_per_chunk < N) ? i0 + rows_per_chunk : N;
+
+    const float4 *lv4 = reinterpret_cast<const float4 *>(log_v + b * M);
+    for (int q = threadIdx.x; q < MV; q += W * RW * 64) {
+        const float4 v = q < m4 ? lv4[q] : make_float4(-f_inf(), -f_inf(), -f_inf(), -f_inf());
+        lv_s[q] = vf4{v.x * kLog2e, v.y * kLog2e, v.z * kLog2e, v.w * kLog2e};
+    }
+    __syncthreads();
+
+    uint32_t qb[NV];  // byte offset of the lane's float4 k in a row (clamped)
+    bool qok[NV];
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+        const int q = (k * W + w) * 64 + lane;
+        qok[k] = q < m4;
+        qb[k] = 16u * (uint32_t)(qok[k] ? q : (int)m4 - 1);
+    }
+    float cm[4 * NV], cs[4 * NV];
+#pragma unroll
+    for (int k = 0; k < 4 * NV; ++k) {
+        cm[k] = kFltMaxNeg;
+        cs[k] = 0.f;
+    }
+    const vf4 *Kb4 = reinterpret_cast<const vf4 *>(K + b * N * M);
+    const int64_t rb = b * N;
+    int par = 0;
+    int64_t i = i0 + g;
+    if constexpr (!DB) {
+        // one row buffer: the next row's loads are issued as soon as a row's
+        // values are folded, and the other waves of the SIMD (three fit)
+        // cover their latency; a second buffer would cost the third wave
+        vf4 ka[NV];
+        if (i < i1)
+            fz_load<NV>(ka, Kb4 + i * m4, qb);
+        for (; i < i1; i += RW) {
+            par = fz_row<W, NV>(ka, lv_s, rowpart, par, w, lane, rb + i, log_mu, inf_row,
+                                log_u, damp, unbalanced, cm, cs);
+            if (i + RW < i1)
+                fz_load<NV>(ka, Kb4 + (i + RW) * m4, qb);
+        }
+    } else {
+        // two row buffers: with one block per CU all waves meet at every row
+        // barrier, so no other wave covers a row's load; the next row's loads
+        // are in flight while a row is reduced
+        vf4 ka[NV], kb[NV];
+        if (i < i1)
+            fz_load<NV>(ka, Kb4 + i * m4, qb);
+        while (i < i1) {
+            if (i + RW < i1)
+                fz_load<NV>(kb, Kb4 + (i + RW) * m4, qb);
+            par = fz_row<W, NV>(ka, lv_s, rowpart, par, w, lane, rb + i, log_mu, inf_row,
+                                log_u, damp, unbalanced, cm, cs);
+            i += RW;
+            if (i >= i1)
+                break;
+            if (i + RW < i1)
+                fz_load<NV>(ka, Kb4 + (i + RW) * m4, qb);
+            par = fz_row<W, NV>(kb, lv_s, rowpart, par, w, lane, rb + i, log_mu, inf_row,
+                                log_u, damp, unbalanced, cm, cs);
+            i += RW;
+        }
+    }
+
+    // merge the row groups' accumulators (same columns) in LDS: g >= h/2
+    // hands over to g - h/2, halving until row group 0 holds the chunk's sum
+    if constexpr (RW > 1) {
+        __shared__ float4 xm[RW / 2][NV][64], xs[RW / 2][NV][64];
+        for (int h = RW; h > 1; h >>= 1) {
+            const int half = h >> 1;
+            if (g >= half && g < h) {
+#pragma unroll
+                for (int k = 0; k < NV; ++k) {
+                    xm[g - half][k][lane] =
+                        make_float4(cm[4 * k], cm[4 * k + 1], cm[4 * k + 2], cm[4 * k + 3]);
+                    xs[g - half][k][lane] =
+                        make_float4(cs[4 * k], cs[4 * k + 1], cs[4 * k + 2], cs[4 * k + 3]);
+                }
+            }
+            __syncthreads();
+            if (g < half) {
+#pragma unroll
+                for (int k = 0; k < NV; ++k) {
+                    const float4 om = xm[g][k][lane], os = xs[g][k][lane];
+                    const float pm[4] = {om.x, om.y, om.z, om.w};
+                    const float ps[4] = {os.x, os.y, os.z, os.w};
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) {
+                        const Lse mrg =
+                            lse2_merge(Lse{cm[4 * k + c], cs[4 * k + c]}, Lse{pm[c], ps[c]});
+                        cm[4 * k + c] = mrg.m;
+                        cs[4 * k + c] = mrg.s;
+                    }
+                }
+            }
+            __syncthreads();
+        }
+    }
+    if (g != 0)
+        return;
+    float2 *dst = colpart + (b * n_chunk + chunk) * M;
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+        if (qok[k]) {
+            float4 *d4 = reinterpret_cast<float4 *>(dst + qb[k] / 4);
+            float pm[4], ps[4];
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                // a column that saw no value above -inf reads (-inf, 0); one
+                // that saw +inf reads (+inf, +inf), whose LSE is +inf as with
+                // torch's shift rule
+                pm[c] = cs[4 * k + c] != 0.f ? cm[4 * k + c] : -f_inf();
+                ps[c] = cm[4 * k + c] == f_inf() ? f_inf() : cs[4 * k + c];
+            }
+            d4[0] = make_float4(pm[0], ps[0], pm[1], ps[1]);
+            d4[1] = make_float4(pm[2], ps[2], pm[3], ps[3]);
+        }
+    }
+}
+
+// grid (ceil(M/64), B), 4 waves: lanes are 64 consecutive columns (coalesced
+// 512-byte reads of one chunk), wave w merges the base-2 partials of chunks
+// w, w+4, ..., the four waves merge in LDS and wave 0 updates log_v.
+constexpr int kMergeWaves = 4;
+__global__ void __launch_bounds__(kMergeWaves * 64)
+sk_col_merge_blk(const float2 *__restrict__ colpart, const float *__restrict__ log_nu,
+                 const uint8_t *__restrict__ inf_col, float *__restrict__ log_v, int64_t M,
+                 int n_chunk, float damp, int unbalanced) {
+    const int64_t b = blockIdx.y;
+    const int w = (int)(threadIdx.x >> 6);
+    const int lane = lane_id();
+    const int64_t j = (int64_t)blockIdx.x * 64 + lane;
+    const int64_t jj = j < M ? j : M - 1;
+    Lse acc{-f_inf(), 0.f};
+    int c = w;
+    for (; c + 3 * kMergeWaves < n_chunk; c += 4 * kMergeWaves) {
+        float2 p[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+            p[u] = colpart[(b * n_chunk + c + u * kMergeWaves) * M + jj];
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+            acc = lse2_merge(acc, Lse{p[u].x, p[u].y});
+    }
+    for (; c < n_chunk; c += kMergeWaves) {
+        const float2 p = colpart[(b * n_chunk + c) * M + jj];
+        acc = lse2_merge(acc, Lse{p.x, p.y});
+    }
+    __shared__ float2 part[kMergeWaves][64];
+    part[w][lane] = make_float2(acc.m, acc.s);
+    __syncthreads();
+    if (w != 0 || j >= M)
+        return;
+#pragma unroll
+    for (int k = 1; k < kMergeWaves; ++k)
+        acc = lse2_merge(acc, Lse{part[k][lane].x, part[k][lane].y});
+    const int64_t t = b * M + j;
+    if (inf_col[t])
+        return;
+    log_v[t] = update_potential(lse2_value(acc), log_nu[t], log_v[t], damp, unbalanced != 0);
+}
+
 // ---- final plan -------------------------------------------------------------------
 
 // log_plan[b,i,j] = (log_u[b,i] + K[b,i,j]) + log_v[b,j], K holding -C'/e_final
@@ -764,6 +1132,32 @@ int launch_log_kernel(const float *cost, const uint8_t *keep, float *K, int64_t 
     else
         TM_LAUNCH(sk_log_kernel<false>, grid, dim3(kMapBlock), 0, stream, cost, keep, K, nK, e,
                   vec);
+    return TM_OK;
+}
+
+int launch_fused_step(const SinkhornLayout &L, const float *K, float *log_v,
+                      const float *log_mu, const uint8_t *inf_row, float *log_u,
+                      const float *log_nu, const uint8_t *inf_col, float2 *colpart, float damp,
+                      int ub, hipStream_t stream) {
+    const dim3 grid((unsigned)L.fz_chunk, (unsigned)L.B);
+    const FusedShape &f = kFusedShapes[L.fused];
+    const dim3 block(f.W * f.RW * 64);
+#define TM_FUSED(W_, RW_, NV_, DB_)                                                        \
+    TM_LAUNCH((sk_fused_step<W_, RW_, NV_, DB_>), grid, block, 0, stream, K, log_v, log_mu, \
+              inf_row, log_u, colpart, L.N, L.M, L.fz_rows, L.fz_chunk, damp, ub)
+    switch (L.fused) {
+    case kFz1x4x4: TM_FUSED(1, 4, 4, false); break;
+    case kFz1x4x8: TM_FUSED(1, 4, 8, false); break;
+    case kFz2x1x8: TM_FUSED(2, 1, 8, false); break;
+    case kFz4x1x8: TM_FUSED(4, 1, 8, false); break;
+    case kFz8x1x8: TM_FUSED(8, 1, 8, true); break;
+    case kFz16x1x4: TM_FUSED(16, 1, 4, true); break;
+    default: return TM_ERR_INTERNAL;
+    }
+#undef TM_FUSED
+    TM_LAUNCH(sk_col_merge_blk, dim3((unsigned)((L.M + 63) / 64), (unsigned)L.B),
+              dim3(kMergeWaves * 64), 0, stream, colpart, log_nu, inf_col, log_v, L.M,
+              L.fz_chunk, damp, ub);
     return TM_OK;
 }
 
@@ -893,6 +1287,8 @@ extern "C" int tm_sinkhorn_iterate_f32(const float *cost, const uint8_t *keep, i
     const bool unbalanced = rho > 0.0;
     const int64_t nK = B * N * M;
     const bool vec = (M % 4) == 0 && ((uintptr_t)log_v % 16) == 0;
+    const bool fused = L.fused != kFzNone && vec && ((uintptr_t)K % 16) == 0 &&
+                       L.fz_chunk <= 0x7fffffff;
 
     TM_LAUNCH(sk_fill, dim3(grid_for(B * N, kMapBlock, 1 << 30)), dim3(kMapBlock), 0, stream,
               log_u, B * N, 0.f);
@@ -913,6 +1309,14 @@ extern "C" int tm_sinkhorn_iterate_f32(const float *cost, const uint8_t *keep, i
             cur_eps = e;
         }
         const float damp = unbalanced ? (float)(1.0 / (1.0 + eps_sched[s] / rho)) : 1.f;
+        if (fused) {
+            const int rc = launch_fused_step(L, K, log_v, log_mu, inf_row, log_u, log_nu,
+                                             inf_col, colpart, damp, unbalanced ? 1 : 0,
+                                             stream);
+            if (rc != TM_OK)
+                return rc;
+            continue;
+        }
         if (vec) {
             const int64_t chunks = (M / 4 + 64 * kRowNV - 1) / (64 * kRowNV);
             const dim3 split_grid((unsigned)(B * N));
