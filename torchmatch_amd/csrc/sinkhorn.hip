@@ -118,19 +118,23 @@ struct SinkhornLayout {
     int n_chunk, rows_per_chunk, n_strip, strip;
     int fused;                   // FusedVariant of sk_fused_step, 0: two-sweep step
     int fz_chunk, fz_rows;       // its row chunks per batch and rows per chunk
-    size_t off_k, off_logmu, off_lognu, off_infrow, off_infcol, off_colpart, off_stats, total;
+    int fz_interleave;           // chunks take every n_chunk-th row (else a range)
+    size_t off_k, off_logmu, off_lognu, off_infrow, off_infcol, off_colpart, off_lse2col,
+        off_stats, total;
 };
 
 __host__ __device__ inline size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
 // sk_fused_step instantiations: (W waves per row, RW row groups, NV float4
-// per lane), chosen by row length; resident blocks per CU from their VGPR use.
+// per lane), chosen by row length; resident blocks per CU from their VGPR and
+// LDS use (65 / 120 / 146 / 146 / 184 / 94 VGPRs; 16 / 32 / 33 / 66 / 131 /
+// 131 KiB of LDS).
 enum FusedVariant { kFzNone = 0, kFz1x4x4, kFz1x4x8, kFz2x1x8, kFz4x1x8, kFz8x1x8, kFz16x1x4 };
 struct FusedShape {
     int W, RW, NV, blocks_per_cu;
 };
 constexpr FusedShape kFusedShapes[] = {
-    {0, 0, 0, 0}, {1, 4, 4, 6}, {1, 4, 8, 3}, {2, 1, 8, 6}, {4, 1, 8, 3}, {8, 1, 8, 1},
+    {0, 0, 0, 0}, {1, 4, 4, 7}, {1, 4, 8, 2}, {2, 1, 8, 4}, {4, 1, 8, 2}, {8, 1, 8, 1},
     {16, 1, 4, 1},
 };
 constexpr int kFusedMinRowsPerWave = 8;
@@ -165,6 +169,10 @@ void choose_fused(SinkhornLayout &L) {
         chunks = 1;
     L.fz_rows = (int)((L.N + chunks - 1) / chunks);
     L.fz_chunk = (int)((L.N + L.fz_rows - 1) / L.fz_rows);
+    // rows split over several waves (one block per CU): blocks march through
+    // the rows side by side (measured faster on C5); rows of one wave: each
+    // block streams its own range (faster on C4)
+    L.fz_interleave = f.W > 1;
 }
 
 SinkhornLayout make_layout(int64_t B, int64_t N, int64_t M) {
@@ -208,6 +216,9 @@ SinkhornLayout make_layout(int64_t B, int64_t N, int64_t M) {
             parts = L.fz_chunk;
         off = align_up(off + sizeof(float2) * (size_t)B * (size_t)parts * (size_t)M, 256);
     }
+    L.off_lse2col = off;
+    if (L.fused)
+        off = align_up(off + sizeof(float) * (size_t)(B * M), 256);
     L.off_stats = off;
     off += 256;
     L.total = off;
@@ -732,42 +743,35 @@ sk_col_merge(const float2 *__restrict__ colpart, const float *__restrict__ log_n
 //
 // The column step of iteration s needs log_u of iteration s, which the row step
 // produces one row at a time; the row is still in registers when its new log_u
-// is known, so each row is folded into per-column (max, sum) accumulators right
-// there.  One step then reads K once (B*N*M*4 bytes) instead of twice.  The
-// column LSE of the step is the merge of the accumulators of every row chunk
-// (sk_col_merge_blk), launched after the pass; the next step's row sweep needs
-// that log_v, so the merge cannot move into the pass.
+// is known, so each row is folded into per-column sums right there.  One step
+// then reads K once (B*N*M*4 bytes) instead of twice.  The column LSE of the
+// step is the merge of the sums of every row chunk (sk_col_merge_blk),
+// launched after the pass; the next step's row sweep needs that log_v, so the
+// merge cannot move into the pass.
 //
 // Both LSEs work in base 2 on the native v_exp_f32: y = t*log2(e) comes from
 // one fma of K with the potential scaled once (log_v per column in LDS, log_u
-// per row), and
-//   row:    exact two-pass over the row in registers (max, then sum of 2^(y-max));
-//   column: one value at a time with one exp per value,
-//           d = y - m;  e = 2^(-|d|);  s = d > 0 ? s*e + 1 : s + e;  m = max(m, y),
-//           the exact running form of sum_k 2^(y_k - max); m starts at -FLT_MAX
-//           rather than -inf so that y - m is never (-inf) - (-inf).
-// Two exps per element at the transcendental unit's quarter rate make the pass
-// VALU-heavy, so the column fold avoids any rescaling pass.
+// per row).
+//   row:    exact two-pass over the row in registers (max, then sum of
+//           2^(y - max)), as the reference's logsumexp;
+//   column: sum of 2^(y - c_j) with c_j the column's base-2 LSE of the previous
+//           step (lse2_col).  A shift is only a scale: the sum keeps its
+//           relative precision as long as it neither overflows nor underflows,
+//           and the merge accepts a column only when its total lies in
+//           [2^-16, 2^16] (so |LSE - c_j| <= 16 and log2 of the total adds at
+//           most 1e-6 of rounding); any other column, every column of the first
+//           step, is recomputed exactly from K by the merge.  This is three
+//           VALU ops and one exp per value instead of the eight of an exact
+//           running max; the pass is VALU-bound (two quarter-rate exps per
+//           element), so that is what sets its speed.
 
 constexpr float kFltMaxNeg = -3.402823466e38f;
+constexpr float kShiftLo = 1.52587890625e-05f;  // 2^-16
+constexpr float kShiftHi = 65536.f;             // 2^16
 
 // Clang vector (not HIP's float4 struct): arrays of it passed by reference to
 // the inlined helpers below stay in registers.
 typedef float vf4 __attribute__((ext_vector_type(4)));
-
-// base-2 log-sum-exp partial: m = max of y (may be +-inf), s = sum 2^(y - shift(m))
-__device__ __forceinline__ Lse lse2_merge(Lse p, Lse q) {
-    const float m = fmaxf(p.m, q.m);
-    const float sh = lse_shift(m);
-    const float a = (p.s == 0.f) ? 0.f : p.s * __builtin_amdgcn_exp2f(lse_shift(p.m) - sh);
-    const float c = (q.s == 0.f) ? 0.f : q.s * __builtin_amdgcn_exp2f(lse_shift(q.m) - sh);
-    return Lse{m, a + c};
-}
-
-// natural-log LSE of a base-2 partial
-__device__ __forceinline__ float lse2_value(Lse p) {
-    return (__builtin_amdgcn_logf(p.s) + lse_shift(p.m)) * kLn2;
-}
 
 // max without the NaN canonicalisation fmaxf costs on this target (two extra
 // v_max per call): v_maximum3_f32.  The values here are never NaN (the cost
@@ -776,6 +780,22 @@ __device__ __forceinline__ float fmax_nn(float a, float b) {
     return __builtin_elementwise_maximum(a, b);
 }
 
+// base-2 log-sum-exp partial: m = max or shift of y (may be +-inf),
+// s = sum 2^(y - shift(m))
+__device__ __forceinline__ Lse lse2_merge(Lse p, Lse q) {
+    const float m = fmaxf(p.m, q.m);
+    const float sh = lse_shift(m);
+    const float a = (p.s == 0.f) ? 0.f : p.s * __builtin_amdgcn_exp2f(lse_shift(p.m) - sh);
+    const float c = (q.s == 0.f) ? 0.f : q.s * __builtin_amdgcn_exp2f(lse_shift(q.m) - sh);
+    return Lse{m, a + c};
+}
+
+// base-2 LSE of a base-2 partial
+__device__ __forceinline__ float lse2_log2(Lse p) { return __builtin_amdgcn_logf(p.s) + lse_shift(p.m); }
+
+// exact running (max, sum) fold of one base-2 value: one exp per value,
+// d = y - m;  e = 2^(-|d|);  s = d > 0 ? s*e + 1 : s + e;  m = max(m, y);
+// m starts at -FLT_MAX rather than -inf so that y - m is never (-inf) - (-inf)
 __device__ __forceinline__ void col_fold2(float &m, float &s, float y) {
     const float d = y - m;
     const float e = __builtin_amdgcn_exp2f(-fabsf(d));  // 0 for y = -inf
@@ -783,52 +803,69 @@ __device__ __forceinline__ void col_fold2(float &m, float &s, float y) {
     m = fmax_nn(m, y);
 }
 
+// (max, sum) of col_fold2 as a partial: a column that saw no value above -inf
+// reads (-inf, 0), one that saw +inf reads (+inf, +inf), whose LSE is +inf as
+// with torch's shift rule
+__device__ __forceinline__ Lse fold_partial(float m, float s) {
+    return Lse{s != 0.f ? m : -f_inf(), m == f_inf() ? f_inf() : s};
+}
+
 // All NV float4 of a row in flight at once: scalar row base + 32-bit lane
 // byte offsets (the saddr form of the load).  Lanes past the row end read its
 // last float4 again (offsets clamped); their log_v in LDS is -inf, which
 // keeps them out of the row LSE, and their column sums are never stored.
+// The row's flag, log marginal and current log_u are loaded with it: a load
+// issued later would make the wait for it a wait for every row in flight.
 template <int NV>
-__device__ __forceinline__ void fz_load(vf4 (&dst)[NV], const vf4 *__restrict__ row4,
-                                        const uint32_t (&qb)[NV]) {
+__device__ __forceinline__ void fz_load(vf4 (&dst)[NV], float &mu, float &u, int &skip,
+                                        const vf4 *__restrict__ row4, const uint32_t (&qb)[NV],
+                                        int64_t r, const float *__restrict__ log_mu,
+                                        const float *__restrict__ log_u,
+                                        const uint8_t *__restrict__ inf_row) {
     const char *base = reinterpret_cast<const char *>(row4);
 #pragma unroll
     for (int k = 0; k < NV; ++k)
         dst[k] = *reinterpret_cast<const vf4 *>(base + qb[k]);
+    skip = inf_row[r];
+    mu = log_mu[r];
+    u = log_u[r];
 }
 
 // One row (batch-flat index r) of the fused step: base-2 row LSE (the W waves
 // of a row merge their partials in LDS slot `par`), the log_u update, then the
-// column fold.  Returns the slot parity for the next row.
-template <int W, int NV>
-__device__ __forceinline__ int fz_row(const vf4 (&kk)[NV], const vf4 *lv_s,
-                                      float2 (*rowpart)[W], int par, int w, int lane,
-                                      int64_t r, const float *__restrict__ log_mu,
-                                      const uint8_t *__restrict__ inf_row,
+// column sums against the shifts in LDS.  Returns the slot parity for the next
+// row.
+template <int W, int NV, bool EXACT>
+__device__ __forceinline__ int fz_row(const vf4 (&kk)[NV], float mu_r, float u_r, int skip,
+                                      const vf4 *lv_s, const vf4 *cs_s, float2 (*rowpart)[W],
+                                      int par, int w, int lane, int64_t r,
                                       float *__restrict__ log_u, float damp, int unbalanced,
-                                      float (&cm)[4 * NV], float (&cs)[4 * NV]) {
-    if (inf_row[r])
+                                      float (&cm)[EXACT ? 4 * NV : 1], float (&cs)[4 * NV]) {
+    // u_r was read with the row, before the row barrier after which wave 0
+    // rewrites log_u[r]
+    if (skip)
         return par;  // lse = -inf: log_u keeps its value, and K is -inf on the row
-    // read before the row barrier: wave 0 rewrites log_u[r] after it
-    const float mu_r = log_mu[r], u_r = log_u[r];
-    float y[4 * NV];
+    float m = -f_inf();
 #pragma unroll
     for (int k = 0; k < NV; ++k) {
         const vf4 lv = lv_s[(k * W + w) * 64 + lane];
-        y[4 * k + 0] = fmaf(kk[k].x, kLog2e, lv.x);
-        y[4 * k + 1] = fmaf(kk[k].y, kLog2e, lv.y);
-        y[4 * k + 2] = fmaf(kk[k].z, kLog2e, lv.z);
-        y[4 * k + 3] = fmaf(kk[k].w, kLog2e, lv.w);
+        m = fmax_nn(fmax_nn(m, fmaf(kk[k].x, kLog2e, lv.x)), fmaf(kk[k].y, kLog2e, lv.y));
+        m = fmax_nn(fmax_nn(m, fmaf(kk[k].z, kLog2e, lv.z)), fmaf(kk[k].w, kLog2e, lv.w));
     }
-    float m = y[0];
-#pragma unroll
-    for (int k = 1; k < 4 * NV; ++k)
-        m = fmax_nn(m, y[k]);
     m = wave_max_all(m);
     const float sh = lse_shift(m);
+    // y is formed again from log_v in LDS rather than kept in 32 VGPRs: the
+    // pass is bound by the rows in flight per SIMD, and VGPRs buy rows
+    asm volatile("" ::: "memory");
     float s = 0.f;
 #pragma unroll
-    for (int k = 0; k < 4 * NV; ++k)
-        s += __builtin_amdgcn_exp2f(y[k] - sh);
+    for (int k = 0; k < NV; ++k) {
+        const vf4 lv = lv_s[(k * W + w) * 64 + lane];
+        s += __builtin_amdgcn_exp2f(fmaf(kk[k].x, kLog2e, lv.x) - sh);
+        s += __builtin_amdgcn_exp2f(fmaf(kk[k].y, kLog2e, lv.y) - sh);
+        s += __builtin_amdgcn_exp2f(fmaf(kk[k].z, kLog2e, lv.z) - sh);
+        s += __builtin_amdgcn_exp2f(fmaf(kk[k].w, kLog2e, lv.w) - sh);
+    }
     s = wave_sum_all(s);
     Lse tot{m, s};
     if constexpr (W > 1) {
@@ -841,39 +878,55 @@ __device__ __forceinline__ int fz_row(const vf4 (&kk)[NV], const vf4 *lv_s,
             tot = lse2_merge(tot, Lse{rowpart[par][k].x, rowpart[par][k].y});
         par ^= 1;
     }
-    const float lu = update_potential(lse2_value(tot), mu_r, u_r, damp, unbalanced != 0);
+    const float lu = update_potential(lse2_log2(tot) * kLn2, mu_r, u_r, damp, unbalanced != 0);
     if (w == 0 && lane == 0)
         log_u[r] = lu;
     const float lu2 = lu * kLog2e;
+    if constexpr (EXACT) {
 #pragma unroll
-    for (int k = 0; k < NV; ++k) {
-        col_fold2(cm[4 * k + 0], cs[4 * k + 0], fmaf(kk[k].x, kLog2e, lu2));
-        col_fold2(cm[4 * k + 1], cs[4 * k + 1], fmaf(kk[k].y, kLog2e, lu2));
-        col_fold2(cm[4 * k + 2], cs[4 * k + 2], fmaf(kk[k].z, kLog2e, lu2));
-        col_fold2(cm[4 * k + 3], cs[4 * k + 3], fmaf(kk[k].w, kLog2e, lu2));
+        for (int k = 0; k < NV; ++k) {
+            col_fold2(cm[4 * k + 0], cs[4 * k + 0], fmaf(kk[k].x, kLog2e, lu2));
+            col_fold2(cm[4 * k + 1], cs[4 * k + 1], fmaf(kk[k].y, kLog2e, lu2));
+            col_fold2(cm[4 * k + 2], cs[4 * k + 2], fmaf(kk[k].z, kLog2e, lu2));
+            col_fold2(cm[4 * k + 3], cs[4 * k + 3], fmaf(kk[k].w, kLog2e, lu2));
+        }
+    } else {
+#pragma unroll
+        for (int k = 0; k < NV; ++k) {
+            const vf4 c = cs_s[(k * W + w) * 64 + lane];
+            cs[4 * k + 0] += __builtin_amdgcn_exp2f(fmaf(kk[k].x, kLog2e, lu2) - c.x);
+            cs[4 * k + 1] += __builtin_amdgcn_exp2f(fmaf(kk[k].y, kLog2e, lu2) - c.y);
+            cs[4 * k + 2] += __builtin_amdgcn_exp2f(fmaf(kk[k].z, kLog2e, lu2) - c.z);
+            cs[4 * k + 3] += __builtin_amdgcn_exp2f(fmaf(kk[k].w, kLog2e, lu2) - c.w);
+        }
     }
     return par;
 }
 
-// grid (n_chunk, B), block W*RW waves.  Rows of chunk c of batch b are
-// [c*rows_per_chunk, min(N, (c+1)*rows_per_chunk)).  A row spans W waves:
-// wave (g, w) of row group g owns float4 columns q = (k*W + w)*64 + lane,
-// k < NV, of rows i0 + g, i0 + g + RW, ...  With W > 1 the W (max, sum)
+// grid (n_chunk, B), block W*RW waves.  Chunk c of batch b holds the rows
+// [c*rows_per_chunk, (c+1)*rows_per_chunk) or, interleaved, the rows c,
+// c + n_chunk, c + 2*n_chunk, ... (the blocks of a batch then march through
+// its rows side by side).  A row spans W waves: wave (g, w) of row group g
+// owns float4 columns q = (k*W + w)*64 + lane, k < NV, of the chunk's rows
+// number g, g + RW, ...  The first rows' loads go out before the block fills
+// LDS, so they overlap that prologue.  With W > 1 the W (max, sum)
 // pairs of a row merge in LDS (one barrier per row, double-buffered slots;
 // RW = 1 then, so every wave of the block sees the same rows and the same
-// barriers).  With RW > 1 the row groups' column accumulators merge in LDS
-// after the last row.  DB: double-buffered rows.  colpart receives base-2
-// (max, sum) pairs.  Requires
-// M % 4 == 0, M <= 256*W*NV, 16-byte aligned K and log_v.
-template <int W, int RW, int NV, bool DB>
+// barriers).  With RW > 1 the row groups' column sums add up in LDS after the
+// last row.  NB: row buffers per wave.  colpart receives (c_j, sum) base-2
+// partials, or with EXACT the exact running (max, sum) of col_fold2 (the
+// first step, and the first after an epsilon change, have no usable shift).  Requires M % 4 == 0, M <= 256*W*NV, 16-byte aligned K and log_v.
+template <int W, int RW, int NV, int NB, bool EXACT>
 __global__ void __launch_bounds__(W * RW * 64)
 sk_fused_step(const float *__restrict__ K, const float *__restrict__ log_v,
-              const float *__restrict__ log_mu, const uint8_t *__restrict__ inf_row,
-              float *__restrict__ log_u, float2 *__restrict__ colpart, int64_t N, int64_t M,
-              int rows_per_chunk, int n_chunk, float damp, int unbalanced) {
+              const float *__restrict__ lse2_col, const float *__restrict__ log_mu,
+              const uint8_t *__restrict__ inf_row, float *__restrict__ log_u,
+              float2 *__restrict__ colpart, int64_t N, int64_t M, int n_chunk,
+              int rows_per_chunk, int interleave, float damp, int unbalanced) {
     static_assert(W == 1 || RW == 1, "a row is split over waves only with one row group");
     constexpr int MV = W * 64 * NV;  // float4 per row at most
     __shared__ vf4 lv_s[MV];         // log_v * log2(e) of the batch, -inf past M
+    __shared__ vf4 cs_s[MV];         // column shifts c_j (base 2)
     __shared__ float2 rowpart[2][W];
     const int chunk = blockIdx.x;
     const int64_t b = blockIdx.y;
@@ -882,15 +935,14 @@ sk_fused_step(const float *__restrict__ K, const float *__restrict__ log_v,
     const int w = wid % W, g = wid / W;
     const int lane = lane_id();
     const int64_t m4 = M / 4;
-    const int64_t i0 = (int64_t)chunk * rows_per_chunk;
-    const int64_t i1 = (i0 + rows_per_chunk < N) ? i0 + rows_per_chunk : N;
-
-    const float4 *lv4 = reinterpret_cast<const float4 *>(log_v + b * M);
-    for (int q = threadIdx.x; q < MV; q += W * RW * 64) {
-        const float4 v = q < m4 ? lv4[q] : make_float4(-f_inf(), -f_inf(), -f_inf(), -f_inf());
-        lv_s[q] = vf4{v.x * kLog2e, v.y * kLog2e, v.z * kLog2e, v.w * kLog2e};
-    }
-    __syncthreads();
+    // this wave's rows: i = first, first + step, ... < end
+    const int64_t first = interleave ? chunk + (int64_t)n_chunk * g
+                                     : (int64_t)chunk * rows_per_chunk + g;
+    const int64_t step = interleave ? (int64_t)n_chunk * RW : RW;
+    const int64_t end = interleave ? N
+                        : ((int64_t)(chunk + 1) * rows_per_chunk < N
+                               ? (int64_t)(chunk + 1) * rows_per_chunk
+                               : N);
 
     uint32_t qb[NV];  // byte offset of the lane's float4 k in a row (clamped)
     bool qok[NV];
@@ -900,80 +952,107 @@ sk_fused_step(const float *__restrict__ K, const float *__restrict__ log_v,
         qok[k] = q < m4;
         qb[k] = 16u * (uint32_t)(qok[k] ? q : (int)m4 - 1);
     }
-    float cm[4 * NV], cs[4 * NV];
+    float cs[4 * NV], cm[EXACT ? 4 * NV : 1];
 #pragma unroll
-    for (int k = 0; k < 4 * NV; ++k) {
-        cm[k] = kFltMaxNeg;
+    for (int k = 0; k < 4 * NV; ++k)
         cs[k] = 0.f;
-    }
+#pragma unroll
+    for (int k = 0; k < (EXACT ? 4 * NV : 1); ++k)
+        cm[k] = kFltMaxNeg;
     const vf4 *Kb4 = reinterpret_cast<const vf4 *>(K + b * N * M);
     const int64_t rb = b * N;
     int par = 0;
-    int64_t i = i0 + g;
-    if constexpr (!DB) {
-        // one row buffer: the next row's loads are issued as soon as a row's
-        // values are folded, and the other waves of the SIMD (three fit)
-        // cover their latency; a second buffer would cost the third wave
-        vf4 ka[NV];
-        if (i < i1)
-            fz_load<NV>(ka, Kb4 + i * m4, qb);
-        for (; i < i1; i += RW) {
-            par = fz_row<W, NV>(ka, lv_s, rowpart, par, w, lane, rb + i, log_mu, inf_row,
-                                log_u, damp, unbalanced, cm, cs);
-            if (i + RW < i1)
-                fz_load<NV>(ka, Kb4 + (i + RW) * m4, qb);
+    int64_t i = first;
+    // NB row buffers: a wave keeps NB - 1 rows' loads in flight while it
+    // reduces one (NB = 1: the next row's loads go out once a row is folded)
+    vf4 kr[NB][NV];
+    float rmu[NB], ru[NB];
+    int rskip[NB];
+#define TM_FZ_LOAD(P_, I_)                                                                   \
+    fz_load<NV>(kr[P_], rmu[P_], ru[P_], rskip[P_], Kb4 + (I_) * m4, qb, rb + (I_), log_mu, \
+                log_u, inf_row)
+    if constexpr (NB == 1) {
+        if (i < end)
+            TM_FZ_LOAD(0, i);
+    } else {
+#pragma unroll
+        for (int p = 0; p < NB - 1; ++p)
+            if (i + p * step < end)
+                TM_FZ_LOAD(p, i + p * step);
+    }
+    const float4 *lv4 = reinterpret_cast<const float4 *>(log_v + b * M);
+    const float4 *cs4 = reinterpret_cast<const float4 *>(lse2_col + b * M);
+    for (int q = threadIdx.x; q < MV; q += W * RW * 64) {
+        const float4 v = q < m4 ? lv4[q] : make_float4(-f_inf(), -f_inf(), -f_inf(), -f_inf());
+        lv_s[q] = vf4{v.x * kLog2e, v.y * kLog2e, v.z * kLog2e, v.w * kLog2e};
+        const float4 c = q < m4 ? cs4[q] : make_float4(0.f, 0.f, 0.f, 0.f);
+        cs_s[q] = vf4{c.x, c.y, c.z, c.w};
+    }
+    __syncthreads();
+
+    if constexpr (NB == 1) {
+        for (; i < end; i += step) {
+            par = fz_row<W, NV, EXACT>(kr[0], rmu[0], ru[0], rskip[0], lv_s, cs_s, rowpart,
+                                       par, w, lane, rb + i, log_u, damp, unbalanced, cm, cs);
+            if (i + step < end)
+                TM_FZ_LOAD(0, i + step);
         }
     } else {
-        // two row buffers: with one block per CU all waves meet at every row
-        // barrier, so no other wave covers a row's load; the next row's loads
-        // are in flight while a row is reduced
-        vf4 ka[NV], kb[NV];
-        if (i < i1)
-            fz_load<NV>(ka, Kb4 + i * m4, qb);
-        while (i < i1) {
-            if (i + RW < i1)
-                fz_load<NV>(kb, Kb4 + (i + RW) * m4, qb);
-            par = fz_row<W, NV>(ka, lv_s, rowpart, par, w, lane, rb + i, log_mu, inf_row,
-                                log_u, damp, unbalanced, cm, cs);
-            i += RW;
-            if (i >= i1)
-                break;
-            if (i + RW < i1)
-                fz_load<NV>(ka, Kb4 + (i + RW) * m4, qb);
-            par = fz_row<W, NV>(kb, lv_s, rowpart, par, w, lane, rb + i, log_mu, inf_row,
-                                log_u, damp, unbalanced, cm, cs);
-            i += RW;
+        while (i < end) {
+#pragma unroll
+            for (int p = 0; p < NB; ++p) {
+                if (i < end) {
+                    const int64_t ia = i + (int64_t)(NB - 1) * step;
+                    if (ia < end)
+                        TM_FZ_LOAD((p + NB - 1) % NB, ia);
+                    par = fz_row<W, NV, EXACT>(kr[p], rmu[p], ru[p], rskip[p], lv_s, cs_s,
+                                               rowpart, par, w, lane, rb + i, log_u, damp,
+                                               unbalanced, cm, cs);
+                    i += step;
+                }
+            }
         }
     }
+#undef TM_FZ_LOAD
 
-    // merge the row groups' accumulators (same columns) in LDS: g >= h/2
+    // add the row groups' sums (same columns, same shifts) in LDS: g >= h/2
     // hands over to g - h/2, halving until row group 0 holds the chunk's sum
     if constexpr (RW > 1) {
-        __shared__ float4 xm[RW / 2][NV][64], xs[RW / 2][NV][64];
+        __shared__ vf4 xs[RW / 2][NV][64];
+        __shared__ vf4 xm[EXACT ? RW / 2 : 1][NV][64];
         for (int h = RW; h > 1; h >>= 1) {
             const int half = h >> 1;
             if (g >= half && g < h) {
 #pragma unroll
                 for (int k = 0; k < NV; ++k) {
-                    xm[g - half][k][lane] =
-                        make_float4(cm[4 * k], cm[4 * k + 1], cm[4 * k + 2], cm[4 * k + 3]);
-                    xs[g - half][k][lane] =
-                        make_float4(cs[4 * k], cs[4 * k + 1], cs[4 * k + 2], cs[4 * k + 3]);
+                    xs[g - half][k][lane] = vf4{cs[4 * k], cs[4 * k + 1], cs[4 * k + 2],
+                                                cs[4 * k + 3]};
+                    if constexpr (EXACT)
+                        xm[g - half][k][lane] = vf4{cm[4 * k], cm[4 * k + 1], cm[4 * k + 2],
+                                                    cm[4 * k + 3]};
                 }
             }
             __syncthreads();
             if (g < half) {
 #pragma unroll
                 for (int k = 0; k < NV; ++k) {
-                    const float4 om = xm[g][k][lane], os = xs[g][k][lane];
-                    const float pm[4] = {om.x, om.y, om.z, om.w};
-                    const float ps[4] = {os.x, os.y, os.z, os.w};
+                    const vf4 o = xs[g][k][lane];
+                    if constexpr (EXACT) {
+                        const vf4 om = xm[g][k][lane];
+                        const float pm[4] = {om.x, om.y, om.z, om.w};
+                        const float ps[4] = {o.x, o.y, o.z, o.w};
 #pragma unroll
-                    for (int c = 0; c < 4; ++c) {
-                        const Lse mrg =
-                            lse2_merge(Lse{cm[4 * k + c], cs[4 * k + c]}, Lse{pm[c], ps[c]});
-                        cm[4 * k + c] = mrg.m;
-                        cs[4 * k + c] = mrg.s;
+                        for (int c = 0; c < 4; ++c) {
+                            const Lse mrg = lse2_merge(fold_partial(cm[4 * k + c], cs[4 * k + c]),
+                                                       fold_partial(pm[c], ps[c]));
+                            cm[4 * k + c] = mrg.s != 0.f ? mrg.m : kFltMaxNeg;
+                            cs[4 * k + c] = mrg.s;
+                        }
+                    } else {
+                        cs[4 * k + 0] += o.x;
+                        cs[4 * k + 1] += o.y;
+                        cs[4 * k + 2] += o.z;
+                        cs[4 * k + 3] += o.w;
                     }
                 }
             }
@@ -987,29 +1066,36 @@ sk_fused_step(const float *__restrict__ K, const float *__restrict__ log_v,
     for (int k = 0; k < NV; ++k) {
         if (qok[k]) {
             float4 *d4 = reinterpret_cast<float4 *>(dst + qb[k] / 4);
-            float pm[4], ps[4];
+            if constexpr (EXACT) {
+                Lse p[4];
 #pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                // a column that saw no value above -inf reads (-inf, 0); one
-                // that saw +inf reads (+inf, +inf), whose LSE is +inf as with
-                // torch's shift rule
-                pm[c] = cs[4 * k + c] != 0.f ? cm[4 * k + c] : -f_inf();
-                ps[c] = cm[4 * k + c] == f_inf() ? f_inf() : cs[4 * k + c];
+                for (int c = 0; c < 4; ++c)
+                    p[c] = fold_partial(cm[4 * k + c], cs[4 * k + c]);
+                d4[0] = make_float4(p[0].m, p[0].s, p[1].m, p[1].s);
+                d4[1] = make_float4(p[2].m, p[2].s, p[3].m, p[3].s);
+            } else {
+                const vf4 c = cs_s[(k * W + w) * 64 + lane];
+                d4[0] = make_float4(c.x, cs[4 * k + 0], c.y, cs[4 * k + 1]);
+                d4[1] = make_float4(c.z, cs[4 * k + 2], c.w, cs[4 * k + 3]);
             }
-            d4[0] = make_float4(pm[0], ps[0], pm[1], ps[1]);
-            d4[1] = make_float4(pm[2], ps[2], pm[3], ps[3]);
         }
     }
 }
 
-// grid (ceil(M/64), B), 4 waves: lanes are 64 consecutive columns (coalesced
-// 512-byte reads of one chunk), wave w merges the base-2 partials of chunks
-// w, w+4, ..., the four waves merge in LDS and wave 0 updates log_v.
-constexpr int kMergeWaves = 4;
+// grid (ceil(M/64), B), MW waves (16 for many chunks, else 4): lanes are 64
+// consecutive columns (coalesced 512-byte reads of one chunk), wave w merges
+// the partials of chunks w, w+MW, ..., and the waves merge in LDS.  With shifted partials (exact = 0) a column
+// whose total lies outside [2^-16, 2^16] (its shift was stale) is recomputed
+// exactly: the block then folds its 64 columns of every row of K with the
+// step's final log_u (wave w takes rows w, w+MW, ...).  Wave 0 updates log_v
+// and stores each column's base-2 LSE as the next step's shift.
+template <int kMergeWaves>
 __global__ void __launch_bounds__(kMergeWaves * 64)
-sk_col_merge_blk(const float2 *__restrict__ colpart, const float *__restrict__ log_nu,
-                 const uint8_t *__restrict__ inf_col, float *__restrict__ log_v, int64_t M,
-                 int n_chunk, float damp, int unbalanced) {
+sk_col_merge_blk(const float2 *__restrict__ colpart, const float *__restrict__ K,
+                 const float *__restrict__ log_u, const float *__restrict__ log_nu,
+                 const uint8_t *__restrict__ inf_col, float *__restrict__ log_v,
+                 float *__restrict__ lse2_col, int64_t N, int64_t M, int n_chunk, int exact,
+                 float damp, int unbalanced) {
     const int64_t b = blockIdx.y;
     const int w = (int)(threadIdx.x >> 6);
     const int lane = lane_id();
@@ -1033,15 +1119,34 @@ sk_col_merge_blk(const float2 *__restrict__ colpart, const float *__restrict__ l
     __shared__ float2 part[kMergeWaves][64];
     part[w][lane] = make_float2(acc.m, acc.s);
     __syncthreads();
-    if (w != 0 || j >= M)
-        return;
 #pragma unroll
-    for (int k = 1; k < kMergeWaves; ++k)
-        acc = lse2_merge(acc, Lse{part[k][lane].x, part[k][lane].y});
-    const int64_t t = b * M + j;
-    if (inf_col[t])
+    for (int k = 0; k < kMergeWaves; ++k)
+        if (k != w)
+            acc = lse2_merge(acc, Lse{part[k][lane].x, part[k][lane].y});
+    const int64_t t = b * M + jj;
+    const bool live = j < M && !inf_col[t];
+    // exact partials are (max, sum) pairs, whose merge needs no check
+    const bool ok = exact || (acc.s >= kShiftLo && acc.s <= kShiftHi);  // false for NaN
+    float lse2 = lse2_log2(acc);
+    if (__syncthreads_or(live && !ok)) {
+        float m = kFltMaxNeg, s = 0.f;
+        const float *col = K + b * N * M + jj;
+        for (int64_t i = w; i < N; i += kMergeWaves)
+            col_fold2(m, s, fmaf(col[i * M], kLog2e, log_u[b * N + i] * kLog2e));
+        __syncthreads();  // part[] is read above by every wave
+        part[w][lane] = make_float2(m, s);
+        __syncthreads();
+        Lse ex = fold_partial(part[0][lane].x, part[0][lane].y);
+#pragma unroll
+        for (int k = 1; k < kMergeWaves; ++k)
+            ex = lse2_merge(ex, fold_partial(part[k][lane].x, part[k][lane].y));
+        if (!ok)
+            lse2 = lse2_log2(ex);
+    }
+    if (w != 0 || !live)
         return;
-    log_v[t] = update_potential(lse2_value(acc), log_nu[t], log_v[t], damp, unbalanced != 0);
+    lse2_col[t] = lse2;
+    log_v[t] = update_potential(lse2 * kLn2, log_nu[t], log_v[t], damp, unbalanced != 0);
 }
 
 // ---- final plan -------------------------------------------------------------------
@@ -1135,29 +1240,44 @@ int launch_log_kernel(const float *cost, const uint8_t *keep, float *K, int64_t 
     return TM_OK;
 }
 
-int launch_fused_step(const SinkhornLayout &L, const float *K, float *log_v,
-                      const float *log_mu, const uint8_t *inf_row, float *log_u,
-                      const float *log_nu, const uint8_t *inf_col, float2 *colpart, float damp,
-                      int ub, hipStream_t stream) {
+int launch_fused_step(const SinkhornLayout &L, bool exact, const float *K, float *log_v,
+                      float *lse2_col, const float *log_mu, const uint8_t *inf_row,
+                      float *log_u, const float *log_nu, const uint8_t *inf_col,
+                      float2 *colpart, float damp, int ub, hipStream_t stream) {
     const dim3 grid((unsigned)L.fz_chunk, (unsigned)L.B);
     const FusedShape &f = kFusedShapes[L.fused];
     const dim3 block(f.W * f.RW * 64);
-#define TM_FUSED(W_, RW_, NV_, DB_)                                                        \
-    TM_LAUNCH((sk_fused_step<W_, RW_, NV_, DB_>), grid, block, 0, stream, K, log_v, log_mu, \
-              inf_row, log_u, colpart, L.N, L.M, L.fz_rows, L.fz_chunk, damp, ub)
+#define TM_FUSED1(W_, RW_, NV_, NB_, EX_)                                                  \
+    TM_LAUNCH((sk_fused_step<W_, RW_, NV_, NB_, EX_>), grid, block, 0, stream, K, log_v,     \
+              lse2_col, log_mu, inf_row, log_u, colpart, L.N, L.M, L.fz_chunk, L.fz_rows,    \
+              L.fz_interleave, damp, ub)
+#define TM_FUSED(W_, RW_, NV_, NB_)                                                         \
+    do {                                                                                    \
+        if (exact)                                                                          \
+            TM_FUSED1(W_, RW_, NV_, NB_, true);                                             \
+        else                                                                                \
+            TM_FUSED1(W_, RW_, NV_, NB_, false);                                            \
+    } while (0)
     switch (L.fused) {
-    case kFz1x4x4: TM_FUSED(1, 4, 4, false); break;
-    case kFz1x4x8: TM_FUSED(1, 4, 8, false); break;
-    case kFz2x1x8: TM_FUSED(2, 1, 8, false); break;
-    case kFz4x1x8: TM_FUSED(4, 1, 8, false); break;
-    case kFz8x1x8: TM_FUSED(8, 1, 8, true); break;
-    case kFz16x1x4: TM_FUSED(16, 1, 4, true); break;
+    case kFz1x4x4: TM_FUSED(1, 4, 4, 1); break;
+    case kFz1x4x8: TM_FUSED(1, 4, 8, 3); break;
+    case kFz2x1x8: TM_FUSED(2, 1, 8, 1); break;
+    case kFz4x1x8: TM_FUSED(4, 1, 8, 1); break;
+    case kFz8x1x8: TM_FUSED(8, 1, 8, 2); break;
+    case kFz16x1x4: TM_FUSED(16, 1, 4, 2); break;
     default: return TM_ERR_INTERNAL;
     }
 #undef TM_FUSED
-    TM_LAUNCH(sk_col_merge_blk, dim3((unsigned)((L.M + 63) / 64), (unsigned)L.B),
-              dim3(kMergeWaves * 64), 0, stream, colpart, log_nu, inf_col, log_v, L.M,
-              L.fz_chunk, damp, ub);
+#undef TM_FUSED1
+    const dim3 mgrid((unsigned)((L.M + 63) / 64), (unsigned)L.B);
+    if (L.fz_chunk > 64)  // C5: 256 chunks, 10.2 us with 16 waves against 11.3 with 4
+        TM_LAUNCH(sk_col_merge_blk<16>, mgrid, dim3(16 * 64), 0, stream, colpart, K, log_u,
+                  log_nu, inf_col, log_v, lse2_col, L.N, L.M, L.fz_chunk, exact ? 1 : 0, damp,
+                  ub);
+    else  // C4: 32 chunks, 5.0 us with 4 waves against 8.5 with 16
+        TM_LAUNCH(sk_col_merge_blk<4>, mgrid, dim3(4 * 64), 0, stream, colpart, K, log_u,
+                  log_nu, inf_col, log_v, lse2_col, L.N, L.M, L.fz_chunk, exact ? 1 : 0, damp,
+                  ub);
     return TM_OK;
 }
 
@@ -1294,6 +1414,10 @@ extern "C" int tm_sinkhorn_iterate_f32(const float *cost, const uint8_t *keep, i
               log_u, B * N, 0.f);
     TM_LAUNCH(sk_fill, dim3(grid_for(B * M, kMapBlock, 1 << 30)), dim3(kMapBlock), 0, stream,
               log_v, B * M, 0.f);
+    float *lse2_col = reinterpret_cast<float *>(ws + L.off_lse2col);
+    if (fused)  // no column shift yet (the first step folds exactly)
+        TM_LAUNCH(sk_fill, dim3(grid_for(B * M, kMapBlock, 1 << 30)), dim3(kMapBlock), 0,
+                  stream, lse2_col, B * M, __builtin_nanf(""));
 
     const int64_t waves_per_batch = (N + kRowsPerWave - 1) / kRowsPerWave;
     const int64_t row_waves = B * waves_per_batch;
@@ -1302,17 +1426,22 @@ extern "C" int tm_sinkhorn_iterate_f32(const float *cost, const uint8_t *keep, i
     float cur_eps = k_eps > 0.f ? k_eps : -1.f;  // the epsilon K currently holds
     for (int32_t s = 0; s < n_iter; ++s) {
         const float e = (float)eps_sched[s];
+        // the fused step's column shifts come from the previous step with the
+        // same kernel K: the first step, and the first after K changes, fold
+        // exactly instead
+        bool exact = s == 0;
         if (e != cur_eps) {
             const int rc = launch_log_kernel(cost, keep, K, nK, e, stream);
             if (rc != TM_OK)
                 return rc;
             cur_eps = e;
+            exact = true;
         }
         const float damp = unbalanced ? (float)(1.0 / (1.0 + eps_sched[s] / rho)) : 1.f;
         if (fused) {
-            const int rc = launch_fused_step(L, K, log_v, log_mu, inf_row, log_u, log_nu,
-                                             inf_col, colpart, damp, unbalanced ? 1 : 0,
-                                             stream);
+            const int rc = launch_fused_step(L, exact, K, log_v, lse2_col, log_mu, inf_row,
+                                             log_u, log_nu, inf_col, colpart, damp,
+                                             unbalanced ? 1 : 0, stream);
             if (rc != TM_OK)
                 return rc;
             continue;
