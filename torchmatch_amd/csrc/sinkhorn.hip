@@ -766,8 +766,7 @@ sk_col_merge(const float2 *__restrict__ colpart, const float *__restrict__ log_n
 //           element), so that is what sets its speed.
 
 constexpr float kFltMaxNeg = -3.402823466e38f;
-constexpr float kShiftLo = 1.52587890625e-05f;  // 2^-16
-constexpr float kShiftHi = 65536.f;             // 2^16
+constexpr float kShiftWindow = 16.f;  // accepted |LSE - shift|, base 2
 
 // Clang vector (not HIP's float4 struct): arrays of it passed by reference to
 // the inlined helpers below stay in registers.
@@ -1084,8 +1083,9 @@ sk_fused_step(const float *__restrict__ K, const float *__restrict__ log_v,
 
 // grid (ceil(M/64), B), MW waves (16 for many chunks, else 4): lanes are 64
 // consecutive columns (coalesced 512-byte reads of one chunk), wave w merges
-// the partials of chunks w, w+MW, ..., and the waves merge in LDS.  With shifted partials (exact = 0) a column
-// whose total lies outside [2^-16, 2^16] (its shift was stale) is recomputed
+// the partials of chunks w, w+MW, ..., and the waves merge in LDS.  With
+// shifted partials (exact = 0) a column whose total lies outside
+// [sum_lo, sum_hi] = [2^-16, 2^16] (its shift was stale) is recomputed
 // exactly: the block then folds its 64 columns of every row of K with the
 // step's final log_u (wave w takes rows w, w+MW, ...).  Wave 0 updates log_v
 // and stores each column's base-2 LSE as the next step's shift.
@@ -1095,7 +1095,7 @@ sk_col_merge_blk(const float2 *__restrict__ colpart, const float *__restrict__ K
                  const float *__restrict__ log_u, const float *__restrict__ log_nu,
                  const uint8_t *__restrict__ inf_col, float *__restrict__ log_v,
                  float *__restrict__ lse2_col, int64_t N, int64_t M, int n_chunk, int exact,
-                 float damp, int unbalanced) {
+                 float sum_lo, float sum_hi, float damp, int unbalanced) {
     const int64_t b = blockIdx.y;
     const int w = (int)(threadIdx.x >> 6);
     const int lane = lane_id();
@@ -1126,7 +1126,7 @@ sk_col_merge_blk(const float2 *__restrict__ colpart, const float *__restrict__ K
     const int64_t t = b * M + jj;
     const bool live = j < M && !inf_col[t];
     // exact partials are (max, sum) pairs, whose merge needs no check
-    const bool ok = exact || (acc.s >= kShiftLo && acc.s <= kShiftHi);  // false for NaN
+    const bool ok = exact || (acc.s >= sum_lo && acc.s <= sum_hi);  // false for NaN
     float lse2 = lse2_log2(acc);
     if (__syncthreads_or(live && !ok)) {
         float m = kFltMaxNeg, s = 0.f;
@@ -1270,14 +1270,21 @@ int launch_fused_step(const SinkhornLayout &L, bool exact, const float *K, float
 #undef TM_FUSED
 #undef TM_FUSED1
     const dim3 mgrid((unsigned)((L.M + 63) / 64), (unsigned)L.B);
+    // TORCHMATCH_AMD_SINKHORN_SHIFT_WINDOW narrows the accepted |LSE - shift|
+    // (base 2; default 16): "0" sends every column through the exact
+    // recompute, which is how the tests reach that path
+    float win = kShiftWindow;
+    if (const char *env = getenv("TORCHMATCH_AMD_SINKHORN_SHIFT_WINDOW"))
+        win = fminf(kShiftWindow, fmaxf(0.f, (float)atof(env)));
+    const float sum_lo = exp2f(-win), sum_hi = win > 0.f ? exp2f(win) : 0.f;
     if (L.fz_chunk > 64)  // C5: 256 chunks, 10.2 us with 16 waves against 11.3 with 4
         TM_LAUNCH(sk_col_merge_blk<16>, mgrid, dim3(16 * 64), 0, stream, colpart, K, log_u,
-                  log_nu, inf_col, log_v, lse2_col, L.N, L.M, L.fz_chunk, exact ? 1 : 0, damp,
-                  ub);
+                  log_nu, inf_col, log_v, lse2_col, L.N, L.M, L.fz_chunk, exact ? 1 : 0, sum_lo,
+                  sum_hi, damp, ub);
     else  // C4: 32 chunks, 5.0 us with 4 waves against 8.5 with 16
         TM_LAUNCH(sk_col_merge_blk<4>, mgrid, dim3(4 * 64), 0, stream, colpart, K, log_u,
-                  log_nu, inf_col, log_v, lse2_col, L.N, L.M, L.fz_chunk, exact ? 1 : 0, damp,
-                  ub);
+                  log_nu, inf_col, log_v, lse2_col, L.N, L.M, L.fz_chunk, exact ? 1 : 0, sum_lo,
+                  sum_hi, damp, ub);
     return TM_OK;
 }
 
