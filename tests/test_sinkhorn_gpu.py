@@ -216,6 +216,30 @@ def test_eps_scaling_schedule(device):
     assert _plan_rel(plan.unsqueeze(0), ref_plan) <= REL_TOL
 
 
+@pytest.mark.parametrize(("N", "M"), [(200, 1500), (40, 9000)])
+def test_eps_scaling_and_mask_on_fused_step(N, M, device):
+    """epsilon scaling on shapes that take the one-read step: K is rebuilt
+    while epsilon decays (each such step folds exactly), then the shifted
+    column sums resume once epsilon settles at reg; and a keep mask."""
+    cost = workloads.sinkhorn_points(1, N, M, 8, seed=M)
+    a = workloads.dirichlet(1, N, 1.0, seed=7)
+    b = workloads.dirichlet(1, M, 1.0, seed=8)
+    ref_plan = sk.log_sinkhorn_plan(cost, eps=0.05, n_iter=30, a=a, b=b, scaling=0.5)[0]
+    plan = solve(cost.to(device), reg=0.05, n_iter=30, a=a.to(device), b=b.to(device),
+                 scaling=0.5)
+    pr = _plan_rel(plan, ref_plan)
+    print(f"scaling {(N, M)} plan rel {pr:.3e}", flush=True)
+    assert pr <= REL_TOL
+    mask = torch.rand(1, N, M, generator=torch.Generator().manual_seed(1)) > 0.3
+    ref_plan = sk.log_sinkhorn_plan(cost.masked_fill(~mask, float("inf")), eps=0.05,
+                                    n_iter=30, a=a, b=b)[0]
+    plan = torch.ops.transport.log_sinkhorn(cost.to(device), 0.05, 30, a.to(device),
+                                            b.to(device), mask.to(device))
+    pr = _plan_rel(plan, ref_plan)
+    print(f"mask {(N, M)} plan rel {pr:.3e}", flush=True)
+    assert pr <= REL_TOL
+
+
 def test_uniform_cost_gives_uniform_plan(device):
     """test_transport_log_sinkhorn.py:12-21 (closed form)."""
     cost = torch.ones(4, 4, device=device)
