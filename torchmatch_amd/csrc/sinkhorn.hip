@@ -16,13 +16,23 @@
 // the reference then overwrites with -inf, so those sweeps are skipped here.
 //
 // HBM layout (row-major float32, resident for the whole call):
-//   K       (B, N, M)  log kernel, rewritten only when the schedule's epsilon
-//                      changes (once for a constant schedule)
-//   log_u/v (B, N) / (B, M) the caller's outputs, updated in place every step
-//   colpart (B, n_chunk, M) float2 (max, sum) partials, only when the column
-//                      sweep splits rows into several chunks (large B*M small)
-// One step = row sweep (reads K once) + column sweep (reads K once): the
-// algorithmic minimum of 2 * B*N*M*4 bytes.
+//   K        (B, N, M)  log kernel, rewritten only when the schedule's epsilon
+//                       changes (once for a constant schedule)
+//   log_u/v  (B, N) / (B, M) the caller's outputs, updated in place every step
+//   colpart  (B, n_chunk, M) column partials of row chunks: float sums (fused
+//                       step) or float2 (max, sum) pairs (exact fused step,
+//                       two-sweep column sweep with chunked rows)
+//   lse2_col (B, M)     each column's base-2 LSE of the previous fused step
+//
+// One step, in one of two forms:
+//   fused (sk_fused_step + sk_col_merge_blk; 512 < M <= 16384, M % 4 == 0):
+//     K is read once.  Each row's LSE is reduced from registers, its log_u
+//     updated, and the same registers add the row into per-column sums
+//     against the previous step's column LSE; the merge adds the chunks'
+//     sums and recomputes exactly any column whose sum left the accepted
+//     window.  B*N*M*4 algorithmic bytes.
+//   two-sweep (sk_row_sweep* + sk_col_sweep [+ sk_col_merge]): a row sweep
+//     and a column sweep each read K, 2 * B*N*M*4 bytes.
 //
 // Row sweep: rows of up to 2048 columns belong to one wave each, and each
 // is an exact two-pass LSE over registers (max, then sum of exp); longer rows
@@ -912,9 +922,11 @@ __device__ __forceinline__ int fz_row(const vf4 (&kk)[NV], float mu_r, float u_r
 // pairs of a row merge in LDS (one barrier per row, double-buffered slots;
 // RW = 1 then, so every wave of the block sees the same rows and the same
 // barriers).  With RW > 1 the row groups' column sums add up in LDS after the
-// last row.  NB: row buffers per wave.  colpart receives (c_j, sum) base-2
-// partials, or with EXACT the exact running (max, sum) of col_fold2 (the
-// first step, and the first after an epsilon change, have no usable shift).  Requires M % 4 == 0, M <= 256*W*NV, 16-byte aligned K and log_v.
+// last row.  NB: row buffers per wave.  colpart receives one float per column
+// (the sum against the shift c_j, which every chunk shares), or with EXACT the
+// exact running (max, sum) pair of col_fold2 (the first step, and the first
+// after an epsilon change, have no usable shift).  Requires M % 4 == 0,
+// M <= 256*W*NV, 16-byte aligned K and log_v.
 template <int W, int RW, int NV, int NB, bool EXACT>
 __global__ void __launch_bounds__(W * RW * 64)
 sk_fused_step(const float *__restrict__ K, const float *__restrict__ log_v,
@@ -1064,8 +1076,8 @@ sk_fused_step(const float *__restrict__ K, const float *__restrict__ log_v,
 #pragma unroll
     for (int k = 0; k < NV; ++k) {
         if (qok[k]) {
-            float4 *d4 = reinterpret_cast<float4 *>(dst + qb[k] / 4);
             if constexpr (EXACT) {
+                float4 *d4 = reinterpret_cast<float4 *>(dst + qb[k] / 4);
                 Lse p[4];
 #pragma unroll
                 for (int c = 0; c < 4; ++c)
@@ -1073,9 +1085,11 @@ sk_fused_step(const float *__restrict__ K, const float *__restrict__ log_v,
                 d4[0] = make_float4(p[0].m, p[0].s, p[1].m, p[1].s);
                 d4[1] = make_float4(p[2].m, p[2].s, p[3].m, p[3].s);
             } else {
-                const vf4 c = cs_s[(k * W + w) * 64 + lane];
-                d4[0] = make_float4(c.x, cs[4 * k + 0], c.y, cs[4 * k + 1]);
-                d4[1] = make_float4(c.z, cs[4 * k + 2], c.w, cs[4 * k + 3]);
+                // every chunk shares the column's shift: the sum alone (the
+                // float view of the same buffer, chunk-major)
+                float *sum = reinterpret_cast<float *>(colpart) + (b * n_chunk + chunk) * M;
+                *reinterpret_cast<float4 *>(sum + qb[k] / 4) =
+                    make_float4(cs[4 * k + 0], cs[4 * k + 1], cs[4 * k + 2], cs[4 * k + 3]);
             }
         }
     }
@@ -1103,18 +1117,33 @@ sk_col_merge_blk(const float2 *__restrict__ colpart, const float *__restrict__ K
     const int64_t jj = j < M ? j : M - 1;
     Lse acc{-f_inf(), 0.f};
     int c = w;
-    for (; c + 3 * kMergeWaves < n_chunk; c += 4 * kMergeWaves) {
-        float2 p[4];
+    if (exact) {  // (max, sum) pairs
+        for (; c + 3 * kMergeWaves < n_chunk; c += 4 * kMergeWaves) {
+            float2 p[4];
 #pragma unroll
-        for (int u = 0; u < 4; ++u)
-            p[u] = colpart[(b * n_chunk + c + u * kMergeWaves) * M + jj];
+            for (int u = 0; u < 4; ++u)
+                p[u] = colpart[(b * n_chunk + c + u * kMergeWaves) * M + jj];
 #pragma unroll
-        for (int u = 0; u < 4; ++u)
-            acc = lse2_merge(acc, Lse{p[u].x, p[u].y});
-    }
-    for (; c < n_chunk; c += kMergeWaves) {
-        const float2 p = colpart[(b * n_chunk + c) * M + jj];
-        acc = lse2_merge(acc, Lse{p.x, p.y});
+            for (int u = 0; u < 4; ++u)
+                acc = lse2_merge(acc, Lse{p[u].x, p[u].y});
+        }
+        for (; c < n_chunk; c += kMergeWaves) {
+            const float2 p = colpart[(b * n_chunk + c) * M + jj];
+            acc = lse2_merge(acc, Lse{p.x, p.y});
+        }
+    } else {  // sums against the column's shift: plain adds
+        const float *sum = reinterpret_cast<const float *>(colpart);
+        float t = 0.f;
+        for (; c + 3 * kMergeWaves < n_chunk; c += 4 * kMergeWaves) {
+            float p[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+                p[u] = sum[(b * n_chunk + c + u * kMergeWaves) * M + jj];
+            t += (p[0] + p[1]) + (p[2] + p[3]);
+        }
+        for (; c < n_chunk; c += kMergeWaves)
+            t += sum[(b * n_chunk + c) * M + jj];
+        acc = Lse{lse2_col[b * M + jj], t};
     }
     __shared__ float2 part[kMergeWaves][64];
     part[w][lane] = make_float2(acc.m, acc.s);
