@@ -25,7 +25,7 @@
 //   lse2_col (B, M)     each column's base-2 LSE of the previous fused step
 //
 // One step, in one of two forms:
-//   fused (sk_fused_step + sk_col_merge_blk; 512 < M <= 16384, M % 4 == 0):
+//   fused (sk_fused_step + sk_col_merge_blk; 128 <= M <= 16384, M % 4 == 0):
 //     K is read once.  Each row's LSE is reduced from registers, its log_u
 //     updated, and the same registers add the row into per-column sums
 //     against the previous step's column LSE; the merge adds the chunks'
@@ -138,14 +138,16 @@ __host__ __device__ inline size_t align_up(size_t x, size_t a) { return (x + a -
 // sk_fused_step instantiations: (W waves per row, RW row groups, NV float4
 // per lane), chosen by row length; resident blocks per CU from their VGPR and
 // LDS use (65 / 120 / 146 / 146 / 184 / 94 VGPRs; 16 / 32 / 33 / 66 / 131 /
-// 131 KiB of LDS).
-enum FusedVariant { kFzNone = 0, kFz1x4x4, kFz1x4x8, kFz2x1x8, kFz4x1x8, kFz8x1x8, kFz16x1x4 };
+// 131 KiB of LDS; the short-row shapes are far below both limits).
+enum FusedVariant {
+    kFzNone = 0, kFz1x4x4, kFz1x4x8, kFz2x1x8, kFz4x1x8, kFz8x1x8, kFz16x1x4, kFz1x4x1, kFz1x4x2
+};
 struct FusedShape {
     int W, RW, NV, blocks_per_cu;
 };
 constexpr FusedShape kFusedShapes[] = {
     {0, 0, 0, 0}, {1, 4, 4, 7}, {1, 4, 8, 2}, {2, 1, 8, 4}, {4, 1, 8, 2}, {8, 1, 8, 1},
-    {16, 1, 4, 1},
+    {16, 1, 4, 1}, {1, 4, 1, 8}, {1, 4, 2, 8},
 };
 constexpr int kFusedMinRowsPerWave = 8;
 
@@ -153,9 +155,11 @@ void choose_fused(SinkhornLayout &L) {
     L.fused = kFzNone;
     L.fz_chunk = L.fz_rows = 0;
     const int64_t M = L.M;
-    if (M % 4 != 0 || M <= 512 || M > 16384)
+    if (M % 4 != 0 || M < 128 || M > 16384)
         return;
-    L.fused = M <= 1024 ? kFz1x4x4
+    L.fused = M <= 256    ? kFz1x4x1
+              : M <= 512  ? kFz1x4x2
+              : M <= 1024 ? kFz1x4x4
               : M <= 2048 ? kFz1x4x8
               : M <= 4096 ? kFz2x1x8
               : M <= 8192 ? kFz4x1x8
@@ -1294,6 +1298,8 @@ int launch_fused_step(const SinkhornLayout &L, bool exact, const float *K, float
     case kFz4x1x8: TM_FUSED(4, 1, 8, 1); break;
     case kFz8x1x8: TM_FUSED(8, 1, 8, 2); break;
     case kFz16x1x4: TM_FUSED(16, 1, 4, 2); break;
+    case kFz1x4x1: TM_FUSED(1, 4, 1, 2); break;
+    case kFz1x4x2: TM_FUSED(1, 4, 2, 2); break;
     default: return TM_ERR_INTERNAL;
     }
 #undef TM_FUSED
