@@ -75,14 +75,21 @@ jv_stats_kernel(const float *__restrict__ costs, int64_t n, JvStats *__restrict_
         }
     };
     int64_t k0 = (int64_t)blockIdx.x * kStatsBlock + threadIdx.x;
-    // four loads in flight per lane before any is folded
-    for (; k0 + 3 * stride < n4; k0 += 4 * stride) {
-        const float4 q0 = c4[k0], q1 = c4[k0 + stride], q2 = c4[k0 + 2 * stride],
-                     q3 = c4[k0 + 3 * stride];
-        visit(q0.x); visit(q0.y); visit(q0.z); visit(q0.w);
-        visit(q1.x); visit(q1.y); visit(q1.z); visit(q1.w);
-        visit(q2.x); visit(q2.y); visit(q2.z); visit(q2.w);
-        visit(q3.x); visit(q3.y); visit(q3.z); visit(q3.w);
+    // eight loads in flight per lane before any is folded (C2: each lane's
+    // whole share of the 16 MiB in two rounds)
+    constexpr int kInFlight = 8;
+    for (; k0 + (kInFlight - 1) * stride < n4; k0 += kInFlight * stride) {
+        float4 q[kInFlight];
+#pragma unroll
+        for (int u = 0; u < kInFlight; ++u)
+            q[u] = c4[k0 + u * stride];
+#pragma unroll
+        for (int u = 0; u < kInFlight; ++u) {
+            visit(q[u].x);
+            visit(q[u].y);
+            visit(q[u].z);
+            visit(q[u].w);
+        }
     }
     for (; k0 < n4; k0 += stride) {
         const float4 q = c4[k0];
