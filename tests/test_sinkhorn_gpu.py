@@ -61,6 +61,10 @@ CASES = [
     (1, 48, 4100, 0.05, 40),
     (1, 32, 16384, 0.05, 30),
     (1, 16, 40000, 0.1, 20),
+    # fewer rows than a block's row groups / waves
+    (1, 1, 256, 0.05, 20),
+    (2, 3, 1024, 0.05, 20),
+    (1, 2, 9000, 0.05, 20),
 ]
 
 
