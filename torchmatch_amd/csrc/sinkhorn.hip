@@ -773,11 +773,13 @@ sk_col_merge(const float2 *__restrict__ colpart, const float *__restrict__ log_n
 //           relative precision as long as it neither overflows nor underflows,
 //           and the merge accepts a column only when its total lies in
 //           [2^-16, 2^16] (so |LSE - c_j| <= 16 and log2 of the total adds at
-//           most 1e-6 of rounding); any other column, every column of the first
-//           step, is recomputed exactly from K by the merge.  This is three
-//           VALU ops and one exp per value instead of the eight of an exact
-//           running max; the pass is VALU-bound (two quarter-rate exps per
-//           element), so that is what sets its speed.
+//           most 1e-6 of rounding); any other column is recomputed exactly
+//           from K by the merge.  Three VALU ops and one exp per value
+//           instead of the eight of an exact running max.  The first step,
+//           and the first after K changes, have no shift and take the exact
+//           running fold (EXACT instances).
+// v_exp_f32 issues at half the FMA rate; the pass needs about half of its
+// time in VALU issue and is bound by the rows in flight, not by arithmetic.
 
 constexpr float kFltMaxNeg = -3.402823466e38f;
 constexpr float kShiftWindow = 16.f;  // accepted |LSE - shift|, base 2
