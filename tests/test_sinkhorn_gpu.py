@@ -110,7 +110,7 @@ STEP_SHAPES = [
     (None, (2, 150, 1500)),
     ("0", (2, 150, 1500)),
     (None, (1, 40, 12000)),
-    ("16x1x4", (1, 40, 12000)),
+    ("8x1x8", (1, 40, 12000)),
     ("0", (1, 40, 12000)),
 ]
 

@@ -23,6 +23,7 @@
 //                       step) or float2 (max, sum) pairs (exact fused step,
 //                       two-sweep column sweep with chunked rows)
 //   lse2_col (B, M)     each column's base-2 LSE of the previous fused step
+//   lse2_row (B, N)     each row's, the same
 //
 // One step, in one of two forms:
 //   fused (sk_fused_step + sk_col_merge_blk; 128 <= M <= 16384, M % 4 == 0):
@@ -130,15 +131,18 @@ struct SinkhornLayout {
     int fz_chunk, fz_rows;       // its row chunks per batch and rows per chunk
     int fz_interleave;           // chunks take every n_chunk-th row (else a range)
     size_t off_k, off_logmu, off_lognu, off_infrow, off_infcol, off_colpart, off_lse2col,
-        off_stats, total;
+        off_lse2row, off_stats, total;
 };
 
 __host__ __device__ inline size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
 // sk_fused_step instantiations: (W waves per row, RW row groups, NV float4
 // per lane), chosen by row length; resident blocks per CU from their VGPR and
-// LDS use (65 / 120 / 146 / 146 / 184 / 94 VGPRs; 16 / 32 / 33 / 66 / 131 /
-// 131 KiB of LDS; the short-row shapes are far below both limits).
+// LDS use (69 / 197 / 100 / 100 / 140 / 85 VGPRs; 16 / 32 / 33 / 66 / 131 /
+// 131 KiB of LDS; the short-row shapes are far below both limits).  Rows
+// longer than 8192 columns take 16 waves of 1024 columns (C5: 193 us per
+// iteration against 215 for 8 waves of 2048; with the rows' sums added in
+// LDS instead of merged as (max, sum) pairs, the smaller shape is faster).
 enum FusedVariant {
     kFzNone = 0, kFz1x4x4, kFz1x4x8, kFz2x1x8, kFz4x1x8, kFz8x1x8, kFz16x1x4, kFz1x4x1, kFz1x4x2
 };
@@ -163,13 +167,13 @@ void choose_fused(SinkhornLayout &L) {
               : M <= 2048 ? kFz1x4x8
               : M <= 4096 ? kFz2x1x8
               : M <= 8192 ? kFz4x1x8
-                          : kFz8x1x8;
+                          : kFz16x1x4;
     if (const char *env = getenv("TORCHMATCH_AMD_SINKHORN_FUSED")) {
-        // "0": the two-sweep step; "16x1x4": that long-row shape
+        // "0": the two-sweep step; "8x1x8": that long-row shape
         if (strcmp(env, "0") == 0)
             L.fused = kFzNone;
-        else if (strcmp(env, "16x1x4") == 0 && M > 8192)
-            L.fused = kFz16x1x4;
+        else if (strcmp(env, "8x1x8") == 0 && M > 8192)
+            L.fused = kFz8x1x8;
         if (L.fused == kFzNone)
             return;
     }
@@ -233,6 +237,9 @@ SinkhornLayout make_layout(int64_t B, int64_t N, int64_t M) {
     L.off_lse2col = off;
     if (L.fused)
         off = align_up(off + sizeof(float) * (size_t)(B * M), 256);
+    L.off_lse2row = off;
+    if (L.fused)
+        off = align_up(off + sizeof(float) * (size_t)(B * N), 256);
     L.off_stats = off;
     off += 256;
     L.total = off;
@@ -829,13 +836,15 @@ __device__ __forceinline__ Lse fold_partial(float m, float s) {
 // byte offsets (the saddr form of the load).  Lanes past the row end read its
 // last float4 again (offsets clamped); their log_v in LDS is -inf, which
 // keeps them out of the row LSE, and their column sums are never stored.
-// The row's flag, log marginal and current log_u are loaded with it: a load
+// The row's flag, log marginal, current log_u and previous base-2 LSE (its
+// shift) are loaded with it: a load
 // issued later would make the wait for it a wait for every row in flight.
 template <int NV>
-__device__ __forceinline__ void fz_load(vf4 (&dst)[NV], float &mu, float &u, int &skip,
+__device__ __forceinline__ void fz_load(vf4 (&dst)[NV], float &mu, float &u, float &rs, int &skip,
                                         const vf4 *__restrict__ row4, const uint32_t (&qb)[NV],
                                         int64_t r, const float *__restrict__ log_mu,
                                         const float *__restrict__ log_u,
+                                        const float *__restrict__ lse2_row,
                                         const uint8_t *__restrict__ inf_row) {
     const char *base = reinterpret_cast<const char *>(row4);
 #pragma unroll
@@ -844,22 +853,16 @@ __device__ __forceinline__ void fz_load(vf4 (&dst)[NV], float &mu, float &u, int
     skip = inf_row[r];
     mu = log_mu[r];
     u = log_u[r];
+    rs = lse2_row[r];
 }
 
-// One row (batch-flat index r) of the fused step: base-2 row LSE (the W waves
-// of a row merge their partials in LDS slot `par`), the log_u update, then the
-// column sums against the shifts in LDS.  Returns the slot parity for the next
-// row.
-template <int W, int NV, bool EXACT>
-__device__ __forceinline__ int fz_row(const vf4 (&kk)[NV], float mu_r, float u_r, int skip,
-                                      const vf4 *lv_s, const vf4 *cs_s, float2 (*rowpart)[W],
-                                      int par, int w, int lane, int64_t r,
-                                      float *__restrict__ log_u, float damp, int unbalanced,
-                                      float (&cm)[EXACT ? 4 * NV : 1], float (&cs)[4 * NV]) {
-    // u_r was read with the row, before the row barrier after which wave 0
-    // rewrites log_u[r]
-    if (skip)
-        return par;  // lse = -inf: log_u keeps its value, and K is -inf on the row
+// Exact base-2 LSE of one row (two passes over the row in registers: max,
+// then sum of 2^(y - max)); the W waves of a row merge their (max, sum) pairs
+// in LDS slot `par`.  Returns the slot parity for the next use.
+template <int W, int NV>
+__device__ __forceinline__ int fz_row_exact(const vf4 (&kk)[NV], const vf4 *lv_s,
+                                            float2 (*rowpart)[W], int par, int w, int lane,
+                                            Lse &tot) {
     float m = -f_inf();
 #pragma unroll
     for (int k = 0; k < NV; ++k) {
@@ -882,7 +885,7 @@ __device__ __forceinline__ int fz_row(const vf4 (&kk)[NV], float mu_r, float u_r
         s += __builtin_amdgcn_exp2f(fmaf(kk[k].w, kLog2e, lv.w) - sh);
     }
     s = wave_sum_all(s);
-    Lse tot{m, s};
+    tot = Lse{m, s};
     if constexpr (W > 1) {
         if (lane == 0)
             rowpart[par][w] = make_float2(m, s);
@@ -893,9 +896,61 @@ __device__ __forceinline__ int fz_row(const vf4 (&kk)[NV], float mu_r, float u_r
             tot = lse2_merge(tot, Lse{rowpart[par][k].x, rowpart[par][k].y});
         par ^= 1;
     }
-    const float lu = update_potential(lse2_log2(tot) * kLn2, mu_r, u_r, damp, unbalanced != 0);
-    if (w == 0 && lane == 0)
+    return par;
+}
+
+// One row (batch-flat index r) of the fused step: its base-2 LSE, the log_u
+// update, then the column fold.  The LSE is summed against the row's LSE of
+// the previous step (rs) in one pass and accepted in the same window as the
+// column sums; otherwise, and on EXACT steps, it is the exact two-pass.
+// Returns the LDS slot parity for the next row.
+template <int W, int NV, bool EXACT>
+__device__ __forceinline__ int fz_row(const vf4 (&kk)[NV], float mu_r, float u_r, float rs,
+                                      int skip, const vf4 *lv_s, const vf4 *cs_s,
+                                      float2 (*rowpart)[W], int par, int w, int lane, int64_t r,
+                                      float *__restrict__ log_u, float *__restrict__ lse2_row,
+                                      float sum_lo, float sum_hi, float damp, int unbalanced,
+                                      float (&cm)[EXACT ? 4 * NV : 1], float (&cs)[4 * NV]) {
+    // u_r and rs were read with the row, before the row barrier after which
+    // wave 0 rewrites log_u[r] and lse2_row[r]
+    if (skip)
+        return par;  // lse = -inf: log_u keeps its value, and K is -inf on the row
+    Lse tot{0.f, 0.f};
+    bool have = false;
+    if constexpr (!EXACT) {
+        float s = 0.f;
+#pragma unroll
+        for (int k = 0; k < NV; ++k) {
+            const vf4 lv = lv_s[(k * W + w) * 64 + lane];
+            s += __builtin_amdgcn_exp2f(fmaf(kk[k].x, kLog2e, lv.x) - rs);
+            s += __builtin_amdgcn_exp2f(fmaf(kk[k].y, kLog2e, lv.y) - rs);
+            s += __builtin_amdgcn_exp2f(fmaf(kk[k].z, kLog2e, lv.z) - rs);
+            s += __builtin_amdgcn_exp2f(fmaf(kk[k].w, kLog2e, lv.w) - rs);
+        }
+        s = wave_sum_all(s);
+        if constexpr (W > 1) {  // the W waves' sums, added in LDS in wave order
+            if (lane == 0)
+                rowpart[par][w].x = s;
+            __syncthreads();
+            s = rowpart[par][0].x;
+#pragma unroll
+            for (int k = 1; k < W; ++k)
+                s += rowpart[par][k].x;
+            par ^= 1;
+        }
+        if (s >= sum_lo && s <= sum_hi) {  // block-uniform; false for NaN
+            tot = Lse{rs, s};
+            have = true;
+        }
+    }
+    if (!have)
+        par = fz_row_exact<W, NV>(kk, lv_s, rowpart, par, w, lane, tot);
+    const float lse2 = lse2_log2(tot);
+    const float lu = update_potential(lse2 * kLn2, mu_r, u_r, damp, unbalanced != 0);
+    if (w == 0 && lane == 0) {
         log_u[r] = lu;
+        lse2_row[r] = lse2;
+    }
     const float lu2 = lu * kLog2e;
     if constexpr (EXACT) {
 #pragma unroll
@@ -936,10 +991,11 @@ __device__ __forceinline__ int fz_row(const vf4 (&kk)[NV], float mu_r, float u_r
 template <int W, int RW, int NV, int NB, bool EXACT>
 __global__ void __launch_bounds__(W * RW * 64)
 sk_fused_step(const float *__restrict__ K, const float *__restrict__ log_v,
-              const float *__restrict__ lse2_col, const float *__restrict__ log_mu,
-              const uint8_t *__restrict__ inf_row, float *__restrict__ log_u,
-              float2 *__restrict__ colpart, int64_t N, int64_t M, int n_chunk,
-              int rows_per_chunk, int interleave, float damp, int unbalanced) {
+              const float *__restrict__ lse2_col, float *__restrict__ lse2_row,
+              const float *__restrict__ log_mu, const uint8_t *__restrict__ inf_row,
+              float *__restrict__ log_u, float2 *__restrict__ colpart, int64_t N, int64_t M,
+              int n_chunk, int rows_per_chunk, int interleave, float sum_lo, float sum_hi,
+              float damp, int unbalanced) {
     static_assert(W == 1 || RW == 1, "a row is split over waves only with one row group");
     constexpr int MV = W * 64 * NV;  // float4 per row at most
     __shared__ vf4 lv_s[MV];         // log_v * log2(e) of the batch, -inf past M
@@ -983,11 +1039,11 @@ sk_fused_step(const float *__restrict__ K, const float *__restrict__ log_v,
     // NB row buffers: a wave keeps NB - 1 rows' loads in flight while it
     // reduces one (NB = 1: the next row's loads go out once a row is folded)
     vf4 kr[NB][NV];
-    float rmu[NB], ru[NB];
+    float rmu[NB], ru[NB], rls[NB];
     int rskip[NB];
-#define TM_FZ_LOAD(P_, I_)                                                                   \
-    fz_load<NV>(kr[P_], rmu[P_], ru[P_], rskip[P_], Kb4 + (I_) * m4, qb, rb + (I_), log_mu, \
-                log_u, inf_row)
+#define TM_FZ_LOAD(P_, I_)                                                                    \
+    fz_load<NV>(kr[P_], rmu[P_], ru[P_], rls[P_], rskip[P_], Kb4 + (I_) * m4, qb, rb + (I_), \
+                log_mu, log_u, lse2_row, inf_row)
     if constexpr (NB == 1) {
         if (i < end)
             TM_FZ_LOAD(0, i);
@@ -1009,8 +1065,9 @@ sk_fused_step(const float *__restrict__ K, const float *__restrict__ log_v,
 
     if constexpr (NB == 1) {
         for (; i < end; i += step) {
-            par = fz_row<W, NV, EXACT>(kr[0], rmu[0], ru[0], rskip[0], lv_s, cs_s, rowpart,
-                                       par, w, lane, rb + i, log_u, damp, unbalanced, cm, cs);
+            par = fz_row<W, NV, EXACT>(kr[0], rmu[0], ru[0], rls[0], rskip[0], lv_s, cs_s,
+                                       rowpart, par, w, lane, rb + i, log_u, lse2_row, sum_lo,
+                                       sum_hi, damp, unbalanced, cm, cs);
             if (i + step < end)
                 TM_FZ_LOAD(0, i + step);
         }
@@ -1022,9 +1079,10 @@ sk_fused_step(const float *__restrict__ K, const float *__restrict__ log_v,
                     const int64_t ia = i + (int64_t)(NB - 1) * step;
                     if (ia < end)
                         TM_FZ_LOAD((p + NB - 1) % NB, ia);
-                    par = fz_row<W, NV, EXACT>(kr[p], rmu[p], ru[p], rskip[p], lv_s, cs_s,
-                                               rowpart, par, w, lane, rb + i, log_u, damp,
-                                               unbalanced, cm, cs);
+                    par = fz_row<W, NV, EXACT>(kr[p], rmu[p], ru[p], rls[p], rskip[p], lv_s,
+                                               cs_s, rowpart, par, w, lane, rb + i, log_u,
+                                               lse2_row, sum_lo, sum_hi, damp, unbalanced, cm,
+                                               cs);
                     i += step;
                 }
             }
@@ -1276,16 +1334,25 @@ int launch_log_kernel(const float *cost, const uint8_t *keep, float *K, int64_t 
 }
 
 int launch_fused_step(const SinkhornLayout &L, bool exact, const float *K, float *log_v,
-                      float *lse2_col, const float *log_mu, const uint8_t *inf_row,
-                      float *log_u, const float *log_nu, const uint8_t *inf_col,
-                      float2 *colpart, float damp, int ub, hipStream_t stream) {
+                      float *lse2_col, float *lse2_row, const float *log_mu,
+                      const uint8_t *inf_row, float *log_u, const float *log_nu,
+                      const uint8_t *inf_col, float2 *colpart, float damp, int ub,
+                      hipStream_t stream) {
+    // TORCHMATCH_AMD_SINKHORN_SHIFT_WINDOW narrows the accepted |LSE - shift|
+    // of rows and columns (base 2; default 16): "0" sends every row through
+    // the exact two-pass and every column through the exact recompute, which
+    // is how the tests reach those paths
+    float win = kShiftWindow;
+    if (const char *env = getenv("TORCHMATCH_AMD_SINKHORN_SHIFT_WINDOW"))
+        win = fminf(kShiftWindow, fmaxf(0.f, (float)atof(env)));
+    const float sum_lo = exp2f(-win), sum_hi = win > 0.f ? exp2f(win) : 0.f;
     const dim3 grid((unsigned)L.fz_chunk, (unsigned)L.B);
     const FusedShape &f = kFusedShapes[L.fused];
     const dim3 block(f.W * f.RW * 64);
 #define TM_FUSED1(W_, RW_, NV_, NB_, EX_)                                                  \
     TM_LAUNCH((sk_fused_step<W_, RW_, NV_, NB_, EX_>), grid, block, 0, stream, K, log_v,     \
-              lse2_col, log_mu, inf_row, log_u, colpart, L.N, L.M, L.fz_chunk, L.fz_rows,    \
-              L.fz_interleave, damp, ub)
+              lse2_col, lse2_row, log_mu, inf_row, log_u, colpart, L.N, L.M, L.fz_chunk,     \
+              L.fz_rows, L.fz_interleave, sum_lo, sum_hi, damp, ub)
 #define TM_FUSED(W_, RW_, NV_, NB_)                                                         \
     do {                                                                                    \
         if (exact)                                                                          \
@@ -1307,13 +1374,6 @@ int launch_fused_step(const SinkhornLayout &L, bool exact, const float *K, float
 #undef TM_FUSED
 #undef TM_FUSED1
     const dim3 mgrid((unsigned)((L.M + 63) / 64), (unsigned)L.B);
-    // TORCHMATCH_AMD_SINKHORN_SHIFT_WINDOW narrows the accepted |LSE - shift|
-    // (base 2; default 16): "0" sends every column through the exact
-    // recompute, which is how the tests reach that path
-    float win = kShiftWindow;
-    if (const char *env = getenv("TORCHMATCH_AMD_SINKHORN_SHIFT_WINDOW"))
-        win = fminf(kShiftWindow, fmaxf(0.f, (float)atof(env)));
-    const float sum_lo = exp2f(-win), sum_hi = win > 0.f ? exp2f(win) : 0.f;
     if (L.fz_chunk > 64)  // C5: 256 chunks, 10.2 us with 16 waves against 11.3 with 4
         TM_LAUNCH(sk_col_merge_blk<16>, mgrid, dim3(16 * 64), 0, stream, colpart, K, log_u,
                   log_nu, inf_col, log_v, lse2_col, L.N, L.M, L.fz_chunk, exact ? 1 : 0, sum_lo,
@@ -1459,6 +1519,7 @@ extern "C" int tm_sinkhorn_iterate_f32(const float *cost, const uint8_t *keep, i
     TM_LAUNCH(sk_fill, dim3(grid_for(B * M, kMapBlock, 1 << 30)), dim3(kMapBlock), 0, stream,
               log_v, B * M, 0.f);
     float *lse2_col = reinterpret_cast<float *>(ws + L.off_lse2col);
+    float *lse2_row = reinterpret_cast<float *>(ws + L.off_lse2row);
     if (fused)  // no column shift yet (the first step folds exactly)
         TM_LAUNCH(sk_fill, dim3(grid_for(B * M, kMapBlock, 1 << 30)), dim3(kMapBlock), 0,
                   stream, lse2_col, B * M, __builtin_nanf(""));
@@ -1483,8 +1544,8 @@ extern "C" int tm_sinkhorn_iterate_f32(const float *cost, const uint8_t *keep, i
         }
         const float damp = unbalanced ? (float)(1.0 / (1.0 + eps_sched[s] / rho)) : 1.f;
         if (fused) {
-            const int rc = launch_fused_step(L, exact, K, log_v, lse2_col, log_mu, inf_row,
-                                             log_u, log_nu, inf_col, colpart, damp,
+            const int rc = launch_fused_step(L, exact, K, log_v, lse2_col, lse2_row, log_mu,
+                                             inf_row, log_u, log_nu, inf_col, colpart, damp,
                                              unbalanced ? 1 : 0, stream);
             if (rc != TM_OK)
                 return rc;
