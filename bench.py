@@ -54,9 +54,9 @@ MEASURED_TRAFFIC = {
     # jv_stats_kernel + jv_solve_kernel on C2
     "jv_c2": int(((8244.0 + 8304.0) * 2 + 8.0 + 512.0) * 1024),
     # sk_fused_step + sk_col_merge_blk per C4 iteration (K once, column sums twice)
-    "sinkhorn_c4": int(((132478.9 + 2309.5) * 2 + 4261.6 + 256.0) * 1024),
+    "sinkhorn_c4": int(((132587.2 + 2309.5) * 2 + 4433.7 + 256.0) * 1024),
     # the same pair per C5 iteration
-    "sinkhorn_c5": int(((525713.1 + 8357.5) * 2 + 16920.6 + 128.0) * 1024),
+    "sinkhorn_c5": int(((525987.7 + 8359.5) * 2 + 17528.6 + 128.0) * 1024),
 }
 
 
