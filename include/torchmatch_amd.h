@@ -144,7 +144,10 @@ enum {
     TM_SK_FLAG_ANY_FINITE = 16u   /* the masked cost holds a finite entry */
 };
 
-/* Device workspace the Sinkhorn calls below need. */
+/* Device workspace the Sinkhorn calls below need.  The size depends on the
+ * step form chosen for the shape (TORCHMATCH_AMD_SINKHORN_FUSED); keep that
+ * variable unchanged between this query and the calls that use the
+ * workspace (a smaller workspace is refused with TM_ERR_WORKSPACE). */
 size_t tm_sinkhorn_workspace_bytes(int64_t B, int64_t N, int64_t M);
 
 /* First half of a solve: one pass over the (B, N, M) float32 cost and the
