@@ -244,6 +244,32 @@ def test_eps_scaling_and_mask_on_fused_step(N, M, device):
     assert pr <= REL_TOL
 
 
+@pytest.mark.parametrize("groups", ["1", "2", "3", "4"])
+def test_batch_groups_match_oracle(groups, device, monkeypatch):
+    """The fused step runs batch groups on separate streams (two by default).
+    Every group count, including uneven splits of B = 5, gives the oracle's
+    plan under epsilon scaling (K rebuilt between segments of steps), and the
+    same bits as one group: each batch's arithmetic does not depend on the
+    split."""
+    B, N, M = 5, 120, 1028
+    cost = workloads.sinkhorn_points(B, N, M, 8, seed=31)
+    cost[2, 4, :] = float("inf")
+    a = workloads.dirichlet(B, N, 1.0, seed=32)
+    b = workloads.dirichlet(B, M, 1.0, seed=33)
+    ref_plan = sk.log_sinkhorn_plan(cost, eps=0.05, n_iter=30, a=a, b=b, scaling=0.5)[0]
+    args = (cost.to(device),)
+    kw = dict(reg=0.05, n_iter=30, a=a.to(device), b=b.to(device), scaling=0.5)
+    monkeypatch.setenv("TORCHMATCH_AMD_SINKHORN_GROUPS", groups)
+    plan = solve(*args, **kw)
+    monkeypatch.setenv("TORCHMATCH_AMD_SINKHORN_GROUPS", "1")
+    one = solve(*args, **kw)
+    torch.cuda.synchronize()
+    pr = _plan_rel(plan, ref_plan)
+    print(f"groups {groups} plan rel {pr:.3e}", flush=True)
+    assert pr <= REL_TOL
+    assert torch.equal(plan, one)
+
+
 def test_uniform_cost_gives_uniform_plan(device):
     """test_transport_log_sinkhorn.py:12-21 (closed form)."""
     cost = torch.ones(4, 4, device=device)
