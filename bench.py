@@ -53,10 +53,11 @@ JV_BYTES_PER_RELAXATION = 12
 MEASURED_TRAFFIC = {
     # jv_stats_kernel + jv_solve_kernel on C2
     "jv_c2": int(((8244.0 + 8304.0) * 2 + 8.0 + 512.0) * 1024),
-    # sk_fused_step + sk_col_merge_blk per C4 iteration (K once, column sums twice)
-    "sinkhorn_c4": int(((132587.2 + 2309.5) * 2 + 4433.7 + 256.0) * 1024),
-    # the same pair per C5 iteration
-    "sinkhorn_c5": int(((525987.7 + 8359.5) * 2 + 17528.6 + 128.0) * 1024),
+    # sk_fused_step + sk_col_merge_blk per C4 iteration: two batch groups of 8,
+    # each one pass + one merge (K once, column sums twice)
+    "sinkhorn_c4": int(2 * ((66321.6 + 1173.5) * 2 + 2176.0 + 128.0) * 1024),
+    # the same pair per C5 iteration (one group)
+    "sinkhorn_c5": int(((525986.7 + 8358.5) * 2 + 17530.0 + 128.0) * 1024),
 }
 
 
