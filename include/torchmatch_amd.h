@@ -186,10 +186,14 @@ int tm_sinkhorn_read_stats(const void *workspace, int64_t B, int64_t N, int64_t 
  *   log_u, log_v  device (B, N), (B, M) outputs: the final scaling
  *              potentials (f = -eps * log_u, g = -eps * log_v)
  * With B >= 2 the steps of part of the batch run on a side stream of the
- * library's own (created on the first such call per device, default
- * priority), forked from and joined back into `stream` with events: the call
- * stays stream-ordered on `stream`.  TORCHMATCH_AMD_SINKHORN_GROUPS=1 keeps
- * every launch on `stream`. */
+ * library's own (created on the first such call per device of `stream`,
+ * default priority), forked from and joined back into `stream` with events:
+ * the call stays stream-ordered on `stream`.  TORCHMATCH_AMD_SINKHORN_GROUPS=1
+ * keeps every launch on `stream`, and so does a `stream` under graph capture.
+ * Threading: calls from several host threads, on the same or different
+ * streams, are safe; each call holds a per-device lock from its fork to its
+ * join, so the side streams never serve two callers' segments interleaved.
+ * Calls that share a workspace must be ordered by the caller. */
 int tm_sinkhorn_iterate_f32(const float *cost, const uint8_t *keep, int64_t B, int64_t N,
                             int64_t M, const double *eps_sched, int32_t n_iter, double rho,
                             float k_eps, float *log_plan, float *log_u, float *log_v,

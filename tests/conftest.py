@@ -4,7 +4,8 @@ Markers:
   gpu -- needs a ROCm device (MI355X); run with ``-m gpu`` on the GPU box.
 
 The repository root is put on sys.path so ``oracle`` (the parity checkers)
-and ``torchmatch_amd`` import from the tree.
+and ``torchmatch_amd`` import from the tree, and ``tests/`` so the shared
+helpers (``sk_parity``) import by name.
 """
 
 from __future__ import annotations
@@ -15,8 +16,9 @@ from pathlib import Path
 import pytest
 
 ROOT = Path(__file__).resolve().parents[1]
-if str(ROOT) not in sys.path:
-    sys.path.insert(0, str(ROOT))
+for _p in (ROOT, ROOT / "tests"):
+    if str(_p) not in sys.path:
+        sys.path.insert(0, str(_p))
 
 
 def pytest_configure(config):

@@ -165,3 +165,77 @@ def test_schedule_flat_and_geometric():
 def test_schedule_errors(kw, msg):
     with pytest.raises(ValueError, match=msg):
         build_eps_schedule(cost=torch.ones(2, 2), **kw)
+
+
+# ---- the order of the two half-steps, fixed by the mathematics ---------------
+# (_log_sinkhorn.py:194-215: the row half-step first, with the previous log_v,
+# then the column half-step with the new log_u)
+
+
+def _small_problem(seed, B=2, N=7, M=5):
+    g = torch.Generator().manual_seed(seed)
+    cost = torch.rand(B, N, M, generator=g, dtype=torch.float64) * 3
+    a = torch.rand(B, N, generator=g, dtype=torch.float64) + 0.1
+    b = torch.rand(B, M, generator=g, dtype=torch.float64) + 0.1
+    b = b / b.sum(-1, keepdim=True) * a.sum(-1, keepdim=True)   # balanced masses
+    return cost, a, b
+
+
+@pytest.mark.parametrize("seed", [0, 1])
+def test_one_iteration_closed_form(seed):
+    """n_iter = 1 from log_u = log_v = 0: log_u = log a - LSE_j(-C/eps), then
+    log_v = log b - LSE_i(-C/eps + log_u), written out with plain exp/log
+    sums per entry.  Swapping the half-steps, dropping log_u from the column
+    update or using the row update's old log_v all change the result."""
+    cost, a, b = _small_problem(seed)
+    eps = 0.3
+    _, _, _, lu, lv = sk.log_sinkhorn_plan(cost, eps=eps, n_iter=1, a=a, b=b)
+    B, N, M = cost.shape
+    for k in range(B):
+        c = cost[k].numpy()
+        for i in range(N):
+            want = math.log(a[k, i].item()) - math.log(sum(math.exp(-c[i, j] / eps)
+                                                            for j in range(M)))
+            assert abs(lu[k, i].item() - want) < 1e-12
+        for j in range(M):
+            s = sum(math.exp(-c[i, j] / eps + lu[k, i].item()) for i in range(N))
+            want = math.log(b[k, j].item()) - math.log(s)
+            assert abs(lv[k, j].item() - want) < 1e-12
+
+
+def test_one_iteration_unbalanced_closed_form():
+    """Same, with the damping 1 / (1 + eps / rho) of _unbalanced_sinkhorn.py:71
+    applied to each half-step's update."""
+    cost, a, b = _small_problem(3)
+    eps, rho = 0.3, 0.8
+    damp = 1.0 / (1.0 + eps / rho)
+    _, lu, lv = sk.unbalanced_sinkhorn_plan(cost, eps=eps, n_iter=1, rho=rho, a=a, b=b)
+    B, N, M = cost.shape
+    for k in range(B):
+        c = cost[k].numpy()
+        for i in range(N):
+            lse = math.log(sum(math.exp(-c[i, j] / eps) for j in range(M)))
+            assert abs(lu[k, i].item() - damp * (math.log(a[k, i].item()) - lse)) < 1e-12
+        for j in range(M):
+            lse = math.log(sum(math.exp(-c[i, j] / eps + lu[k, i].item()) for i in range(N)))
+            assert abs(lv[k, j].item() - damp * (math.log(b[k, j].item()) - lse)) < 1e-12
+
+
+@pytest.mark.parametrize("n_iter", [1, 2, 3, 7])
+def test_column_marginals_exact_after_any_iteration(n_iter):
+    """The balanced step ends with the column half-step, so after ANY number
+    of iterations the plan's column sums equal b (to float64 rounding) while
+    the row sums do not yet equal a (far from converged at these n_iter).
+    A restatement with the half-steps swapped has it the other way round."""
+    cost, a, b = _small_problem(5, B=2, N=9, M=6)
+    eps = 0.2
+    plan = sk.log_sinkhorn_plan(cost, eps=eps, n_iter=n_iter, a=a, b=b)[0].exp()
+    col_err = (plan.sum(1) - b).abs().max().item()
+    row_err = (plan.sum(2) - a).abs().max().item()
+    assert col_err < 1e-12
+    assert row_err > 1e-6
+    lp = numpy_sinkhorn(cost.numpy(), a.numpy(), b.numpy(), [eps] * n_iter,
+                        swap_halves=True)
+    swapped = np.exp(lp)
+    assert np.abs(swapped.sum(2) - a.numpy()).max() < 1e-12      # rows exact instead
+    assert np.abs(swapped.sum(1) - b.numpy()).max() > 1e-6

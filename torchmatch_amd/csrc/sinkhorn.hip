@@ -70,13 +70,39 @@ constexpr int64_t kColBlocksTarget = 5 * 256;  // column-sweep blocks to aim for
 constexpr int kColU = 8;              // rows per group fold
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
+// 1 / kLog2e as an unevaluated sum hi + lo (hi is the float nearest ln 2).  The
+// one-read step works in base-2 units, y = kLog2e * (K + log_v), and converts
+// each LSE back with this pair: kLn2 * kLog2e = 1 - 1.06e-8, so converting
+// with kLn2 alone scales every update by that factor, a bias that the
+// potentials' neutral mode (log_u + c, log_v - c) accumulates step after step
+// (C4: 3.4e-5 in log_u after 200 iterations against 1.8e-6 for the float32
+// reference); the pair leaves 2e-16.
+constexpr float kInvLog2eHi = 0.693147182464599609375f;   // 0x3f317218
+constexpr float kInvLog2eLo = 7.348693209507928e-09f;     // 0x31fc7fca
 
 __device__ __forceinline__ float f_inf() { return __int_as_float(0x7f800000); }
 
+// log2 e and ln 2 as hi + lo float pairs (hi = the float constants above):
+// the two-sweep step's exp and log go through base 2 on every element and
+// row, and a constant's rounding would bias each update by ~1e-8 relative,
+// which the potentials' neutral mode accumulates over the iterations
+constexpr float kLog2eLo = 1.925963033500011e-08f;  // 0x32a57060
+constexpr float kLn2Lo = -1.9046542121259336e-09f;  // 0xb102e308
+
 // e^(x) for x <= 0 (or -inf) on the native base-2 unit
-__device__ __forceinline__ float exp_nonpos(float x) { return __builtin_amdgcn_exp2f(x * kLog2e); }
+__device__ __forceinline__ float exp_nonpos(float x) {
+    return __builtin_amdgcn_exp2f(fmaf(x, kLog2e, x * kLog2eLo));
+}
 // natural log of s >= 0 (log(0) = -inf)
-__device__ __forceinline__ float ln(float s) { return __builtin_amdgcn_logf(s) * kLn2; }
+__device__ __forceinline__ float ln(float s) {
+    const float l2 = __builtin_amdgcn_logf(s);
+    return fmaf(l2, kLn2, l2 * kLn2Lo);
+}
+
+// natural-unit LSE from a base-2 LSE of kLog2e-scaled values
+__device__ __forceinline__ float ln_of_lse2(float l2) {
+    return fmaf(l2, kInvLog2eHi, l2 * kInvLog2eLo);
+}
 
 __device__ __forceinline__ float lse_shift(float m) { return isinf(m) ? 0.f : m; }
 
@@ -948,7 +974,7 @@ __device__ __forceinline__ int fz_row(const vf4 (&kk)[NV], float mu_r, float u_r
     if (!have)
         par = fz_row_exact<W, NV>(kk, lv_s, rowpart, par, w, lane, tot);
     const float lse2 = lse2_log2(tot);
-    const float lu = update_potential(lse2 * kLn2, mu_r, u_r, damp, unbalanced != 0);
+    const float lu = update_potential(ln_of_lse2(lse2), mu_r, u_r, damp, unbalanced != 0);
     if (w == 0 && lane == 0) {
         log_u[r] = lu;
         lse2_row[r] = lse2;
@@ -1244,7 +1270,7 @@ sk_col_merge_blk(const float2 *__restrict__ colpart, const float *__restrict__ K
     if (w != 0 || !live)
         return;
     lse2_col[t] = lse2;
-    log_v[t] = update_potential(lse2 * kLn2, nu_t, v_t, damp, unbalanced != 0);
+    log_v[t] = update_potential(ln_of_lse2(lse2), nu_t, v_t, damp, unbalanced != 0);
 }
 
 // ---- final plan -------------------------------------------------------------------
@@ -1396,7 +1422,13 @@ int launch_fused_step(const SinkhornLayout &L, bool exact, const float *K, float
 // the batch can be split into groups that run their steps on separate streams:
 // one group's merge launch and pass tail then overlap another group's pass.
 // The side streams (default priority, non-blocking) and the fork / join events
-// are created once per device and kept until the process ends.
+// are created once per device (the device of the caller's stream) and kept
+// until the process ends.  Every caller on a device shares them, so a caller
+// holds the device's lock from the fork (event recorded on its stream, side
+// streams wait on it) through its launches to the join (its stream waits on
+// the side streams' events): another caller's fork can never land between
+// them.  A stream under graph capture runs one group on that stream only, so
+// the shared side streams are never pulled into a capture.
 constexpr int kMaxGroups = 4;
 constexpr int kMaxDevices = 64;
 
@@ -1405,27 +1437,40 @@ struct SideStreams {
     hipEvent_t fork;
     hipEvent_t join[kMaxGroups - 1];
     bool ready;
+    std::mutex mu;  // held across one fork -> launches -> join segment
 };
 SideStreams g_side[kMaxDevices];
-std::mutex g_side_mu;
+std::mutex g_side_init_mu;
 
-int side_streams(SideStreams **out) {
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+int side_streams(hipStream_t stream, SideStreams **out) {
+    hipDevice_t dev = 0;
+    if (hipStreamGetDevice(stream, &dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
         return TM_ERR_LAUNCH;
-    std::lock_guard<std::mutex> lock(g_side_mu);
+    std::lock_guard<std::mutex> lock(g_side_init_mu);
     SideStreams &ss = g_side[dev];
     if (!ss.ready) {
-        if (hipEventCreateWithFlags(&ss.fork, hipEventDisableTiming) != hipSuccess)
+        int cur = 0;
+        if (hipGetDevice(&cur) != hipSuccess)
             return TM_ERR_LAUNCH;
-        for (int g = 0; g < kMaxGroups - 1; ++g)
-            if (hipStreamCreateWithFlags(&ss.s[g], hipStreamNonBlocking) != hipSuccess ||
-                hipEventCreateWithFlags(&ss.join[g], hipEventDisableTiming) != hipSuccess)
-                return TM_ERR_LAUNCH;
+        if (cur != dev && hipSetDevice(dev) != hipSuccess)
+            return TM_ERR_LAUNCH;
+        bool ok = hipEventCreateWithFlags(&ss.fork, hipEventDisableTiming) == hipSuccess;
+        for (int g = 0; ok && g < kMaxGroups - 1; ++g)
+            ok = hipStreamCreateWithFlags(&ss.s[g], hipStreamNonBlocking) == hipSuccess &&
+                 hipEventCreateWithFlags(&ss.join[g], hipEventDisableTiming) == hipSuccess;
+        if (cur != dev && hipSetDevice(cur) != hipSuccess)
+            ok = false;
+        if (!ok)
+            return TM_ERR_LAUNCH;
         ss.ready = true;
     }
     *out = &ss;
     return TM_OK;
+}
+
+bool stream_capturing(hipStream_t stream) {
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+    return hipStreamIsCapturing(stream, &st) == hipSuccess && st != hipStreamCaptureStatusNone;
 }
 
 // Batch groups for the fused step: two when B >= 2 (C4: 41.9 us per
@@ -1590,10 +1635,10 @@ extern "C" int tm_sinkhorn_iterate_f32(const float *cost, const uint8_t *keep, i
         // steps run in segments of one epsilon (K rebuilt on the caller's
         // stream before a segment); within a segment each batch group runs its
         // steps on its own stream
-        const int G = fused_groups(L);
+        const int G = stream_capturing(stream) ? 1 : fused_groups(L);
         SideStreams *ss = nullptr;
         if (G > 1) {
-            const int rc = side_streams(&ss);
+            const int rc = side_streams(stream, &ss);
             if (rc != TM_OK)
                 return rc;
         }
@@ -1610,7 +1655,9 @@ extern "C" int tm_sinkhorn_iterate_f32(const float *cost, const uint8_t *keep, i
             int32_t s1 = s0 + 1;
             while (s1 < n_iter && (float)eps_sched[s1] == e)
                 ++s1;
+            std::unique_lock<std::mutex> segment;
             if (G > 1) {
+                segment = std::unique_lock<std::mutex>(ss->mu);
                 if (hipEventRecord(ss->fork, stream) != hipSuccess)
                     return TM_ERR_LAUNCH;
                 for (int g = 1; g < G; ++g)
