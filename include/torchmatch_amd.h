@@ -109,6 +109,15 @@ int tm_jv_compact_batch_f32(const float *costs, int64_t B, int32_t N, int32_t M,
                             void *workspace, size_t workspace_bytes, uint32_t *d_status,
                             hipStream_t stream);
 
+/* Problems of the last tm_jv_dense_batch_f32 / tm_jv_compact_batch_f32 call on
+ * `workspace` (K <= 64) whose certified shortest-path solve did not prove a
+ * unique optimum and that were solved again by the exact replay of the
+ * reference's order (ties, near-ties).  Copies one word to *count and
+ * synchronises `stream`.  A diagnostic with no counterpart in the reference.
+ * TORCHMATCH_AMD_JV_CERTIFY=0 in the environment switches the certified path
+ * off (every problem replays). */
+int tm_jv_read_replays(const void *workspace, uint32_t *count, hipStream_t stream);
+
 /* Copy the two status words to the host and synchronise `stream` (the only
  * host sync of the JV path, mirroring the reference's validation readback,
  * cuda_common.cuh:241-249).  Returns TM_OK, TM_ERR_NAN, TM_ERR_NEG_INF,

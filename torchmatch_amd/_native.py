@@ -43,6 +43,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [_VP, ctypes.c_int64, ctypes.c_int32, ctypes.c_int32, _VP, _VP, ctypes.c_size_t, _VP, _VP],
     ),
     "tm_jv_check_status": (ctypes.c_int, [_VP, _VP]),
+    "tm_jv_read_replays": (ctypes.c_int, [_VP, ctypes.POINTER(ctypes.c_uint32), _VP]),
     "tm_jv_status_code": (ctypes.c_int, [_VP]),
     "tm_jv_unpack_i64": (
         ctypes.c_int,

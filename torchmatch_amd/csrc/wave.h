@@ -36,6 +36,14 @@ __device__ __forceinline__ float readlane_f(float x, int lane) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), lane));
 }
 __device__ __forceinline__ int uniform_i(int x) { return __builtin_amdgcn_readfirstlane(x); }
+
+// v_writelane_b32: `old` with lane `lane` (uniform) replaced by `val` (uniform).
+// This clang has no builtin; the intrinsic is declared by its LLVM name.
+extern "C" __device__ int tmamd_llvm_writelane_i32(int val, int lane, int old) __asm(
+    "llvm.amdgcn.writelane.i32");
+__device__ __forceinline__ uint32_t writelane_i(int val, int lane, uint32_t old) {
+    return (uint32_t)tmamd_llvm_writelane_i32(val, lane, (int)old);
+}
 __device__ __forceinline__ float uniform_f(float x) {
     return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(x)));
 }
@@ -142,6 +150,13 @@ __device__ __forceinline__ int fkey(float f) {
 }
 constexpr int kKeyNone = 0x7fffffff;  // a NaN bit pattern: above every key
 
+// fkey without the -0.0 fold: order-preserving for every non-NaN float, with
+// -0.0 just below +0.0 (for minima whose ties need not be exact)
+__device__ __forceinline__ int fkey_signed(float f) {
+    const int b = __float_as_int(f);
+    return b ^ ((b >> 31) & 0x7fffffff);
+}
+
 // DPP move for patterns in which every lane has a source lane (quad_perm,
 // row mirrors), so the old value never shows and the move can fold into the
 // consuming ALU op.
@@ -193,6 +208,20 @@ __device__ __forceinline__ int wave_min_key(int key) {
     return min((int)s[0], (int)s[1]);
 }
 
+// Smallest key of the wave as a scalar: the four 16-lane rows reduce with DPP,
+// then the scalar unit takes the minimum of the rows' results (shorter than
+// the row swaps when the result is wanted in an SGPR anyway).
+__device__ __forceinline__ int wave_min_key_s(int key) {
+    int a = key;
+    a = min(a, dpp_full<kDppQuadXor1>(a));
+    a = min(a, dpp_full<kDppQuadXor2>(a));
+    a = min(a, dpp_full<kDppRowHalfMirror>(a));
+    a = min(a, dpp_full<kDppRowMirror>(a));
+    const int r0 = __builtin_amdgcn_readlane(a, 0), r1 = __builtin_amdgcn_readlane(a, 16);
+    const int r2 = __builtin_amdgcn_readlane(a, 32), r3 = __builtin_amdgcn_readlane(a, 48);
+    return min(min(r0, r1), min(r2, r3));
+}
+
 // Inclusive prefix minimum of keys across lanes 0..63.
 __device__ __forceinline__ int wave_prefix_min_key(int x) {
     const int none = kKeyNone;
@@ -216,9 +245,25 @@ typedef float f32x32 __attribute__((ext_vector_type(32)));
 struct Col64 {
     f32x32 lo, hi;
     __device__ __forceinline__ float get(int i) const {  // i uniform, 0 <= i < 64
-        return (i < 32) ? lo[i] : hi[i - 32];
+        const int k = i & 31;
+        const float a = lo[k], b = hi[k];
+        return (i < 32) ? a : b;
+    }
+    __device__ __forceinline__ void set(int i, float x) {  // i a constant, 0 <= i < 64
+        if (i < 32)
+            lo[i] = x;
+        else
+            hi[i - 32] = x;
     }
 };
+
+// Lane `lane` (uniform) of a float64.
+__device__ __forceinline__ double readlane_d(double x, int lane) {
+    const long long b = __double_as_longlong(x);
+    const int lo = __builtin_amdgcn_readlane((int)(b & 0xffffffffll), lane);
+    const int hi = __builtin_amdgcn_readlane((int)(b >> 32), lane);
+    return __longlong_as_double(((long long)hi << 32) | (unsigned int)lo);
+}
 
 } // namespace tmamd
 
