@@ -48,7 +48,7 @@ namespace tmamd {
 namespace {
 
 constexpr int kTile = 64;                // K <= 64 path
-constexpr int kStatsBlock = 256;
+constexpr int kStatsBlock = 1024;  // 16 waves: four per SIMD while the pass streams
 
 // ---------------------------------------------------------------------------
 // 1. statistics pass
@@ -79,9 +79,9 @@ jv_stats_kernel(const float *__restrict__ costs, int64_t n, JvStats *__restrict_
         }
     };
     int64_t k0 = (int64_t)blockIdx.x * kStatsBlock + threadIdx.x;
-    // eight loads in flight per lane before any is folded (C2: each lane's
-    // whole share of the 16 MiB in two rounds)
-    constexpr int kInFlight = 8;
+    // four loads in flight per lane before any is folded (C2: each lane's
+    // whole share of the 16 MiB in one round)
+    constexpr int kInFlight = 4;
     for (; k0 + (kInFlight - 1) * stride < n4; k0 += kInFlight * stride) {
         float4 q[kInFlight];
 #pragma unroll
@@ -560,7 +560,7 @@ __device__ __forceinline__ void column_reduction(const int K, WaveLds &L, Row ro
         const int own = readlane_i(x, i);
         const float r = row(i) - v;
         const int key = (live && lane != own) ? fkey(r) : kKeyNone;
-        const int kmin = uniform_i(wave_min_key(key));
+        const int kmin = wave_min_key_s(key);
         float mn = start_min;
         if (kmin < large_key)
             mn = readlane_f(r, first_lane(ballot(key == kmin)));
@@ -980,19 +980,31 @@ __device__ __forceinline__ bool certified_solve(const int K, WaveLds &L, const C
     // One shortest path per free row.  Lane j holds column j: its distance d,
     // its order key (kKeyNone once scanned, and on dead lanes), its
     // predecessor row and its cost column in registers (col.get(i) = c[i][j],
-    // an indexed VGPR move).
+    // an indexed VGPR move).  The key of a distance is its raw bits: d >= 0
+    // up to rounding, and a misorder among rounding-size negatives only picks
+    // another column of the same distance.  Lane r also holds
+    // u_r = c[r][x_r] - v[x_r] (fixed during a search), so the step's offset
+    // h = c[i][j*] - v[j*] - level (the scanned column j* is row i's own)
+    // comes from one read of lane i, alongside the row's gather.
     int pred = 0;
+    float u = 0.f;
+    auto refresh_u = [&]() {
+        const int xs = x < 0 ? lane : x;
+        const float vx = __int_as_float(__builtin_amdgcn_ds_bpermute(xs * 4, __float_as_int(v)));
+        u = L.c[lane * kTile + xs] - vx;
+    };
+    refresh_u();
     for (int f = 0; f < n_free; ++f) {
         const int start = readlane_i(fr, f);
         float d = col.get(start) - v;
-        int key = live ? fkey_signed(d) : kKeyNone;
+        int key = live ? __float_as_int(d) : kKeyNone;
         pred = start;
         int jf = -1;
         float level = 0.f;
         // each step retires one lane for good (its key becomes kKeyNone), so
         // the loop ends within K steps
         while (true) {
-            const int kmin = uniform_i(wave_min_key(key));
+            const int kmin = wave_min_key_s(key);
             if (kmin == kKeyNone)
                 break;
             const int js = first_lane(ballot(key == kmin));
@@ -1004,14 +1016,12 @@ __device__ __forceinline__ bool certified_solve(const int K, WaveLds &L, const C
             }
             // relax through row `is` (scan_dense: h = c[i][jp] - v[jp] - level,
             // r = c[i][j] - v[j] - h)
-            const float tv = col.get(is) - v;
-            const float h = readlane_f(tv, js) - level;
-            const float r = tv - h;
-            const int kr = fkey_signed(r);
+            const float h = readlane_f(u, is) - level;
+            const float r = (col.get(is) - v) - h;
             const bool upd = (key != kKeyNone) & (r < d);
             d = upd ? r : d;
             pred = upd ? is : pred;
-            const int nk = upd ? kr : key;
+            const int nk = upd ? __float_as_int(r) : key;
             key = lane == js ? kKeyNone : nk;
         }
         if (jf < 0)
@@ -1030,6 +1040,7 @@ __device__ __forceinline__ bool certified_solve(const int K, WaveLds &L, const C
                 break;
             j = prev;
         }
+        refresh_u();
     }
     if (ballot(live && (x < 0 || y < 0)))
         return false;

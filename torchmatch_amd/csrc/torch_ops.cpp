@@ -64,6 +64,38 @@ void check_rc(int rc, const char *op_name) {
     }
 }
 
+// Two host-mapped pinned status words per device and host thread, allocated
+// on the thread's first call for that device and kept until the process ends
+// (a call synchronises before it returns, so the thread's next call may
+// reuse them).  Saves the pinned allocation and the device-pointer lookup of
+// every call.
+struct StatusSlot {
+    uint32_t *host = nullptr;
+    uint32_t *dev = nullptr;
+};
+
+const StatusSlot *status_slot(int device) {
+    constexpr int kMaxDevices = 64;
+    thread_local StatusSlot slots[kMaxDevices];
+    thread_local bool tried[kMaxDevices] = {};
+    if (device < 0 || device >= kMaxDevices)
+        return nullptr;
+    StatusSlot &s = slots[device];
+    if (!tried[device]) {
+        tried[device] = true;
+        void *h = nullptr;
+        void *d = nullptr;
+        if (hipHostMalloc(&h, 2 * sizeof(uint32_t), hipHostMallocMapped) == hipSuccess &&
+            hipHostGetDevicePointer(&d, h, 0) == hipSuccess) {
+            s.host = static_cast<uint32_t *>(h);
+            s.dev = static_cast<uint32_t *>(d);
+        } else {
+            (void)hipGetLastError();
+        }
+    }
+    return s.dev != nullptr ? &s : nullptr;
+}
+
 using JvSolver = int (*)(const float *, int64_t, int32_t, int32_t, int64_t *, void *, size_t,
                         uint32_t *, hipStream_t);
 
@@ -100,24 +132,17 @@ at::Tensor jv_batch_hip(const at::Tensor &costs, JvSolver solver, int64_t max_k,
     auto ws = at::empty({(int64_t)ws_bytes}, costs.options().dtype(at::kByte));
     // The status words go to pinned host memory the kernels write directly,
     // so the readback is the stream synchronisation alone (no copy command);
-    // device memory and a copy when the pinned block cannot be mapped.
-    auto hstatus = at::empty({2}, at::TensorOptions().dtype(at::kInt).pinned_memory(true));
-    void *mapped = nullptr;
-    if (hipHostGetDevicePointer(&mapped, hstatus.data_ptr(), 0) != hipSuccess) {
-        (void)hipGetLastError();
-        mapped = nullptr;
-    }
-    if (mapped != nullptr) {
+    // device memory and a copy when no pinned block can be mapped.
+    if (const StatusSlot *slot = status_slot(costs.get_device())) {
         int rc = solver(cf.data_ptr<float>(), B, (int32_t)N, (int32_t)M,
-                        out.data_ptr<int64_t>(), ws.data_ptr(), ws_bytes,
-                        static_cast<uint32_t *>(mapped), stream);
-        // synchronise before any error leaves: a launched kernel must not
-        // write the pinned words after they went back to the allocator
+                        out.data_ptr<int64_t>(), ws.data_ptr(), ws_bytes, slot->dev, stream);
+        // synchronise before any error leaves: the next call on this thread
+        // reuses the words
         const hipError_t se = hipStreamSynchronize(stream);
         check_rc(rc, op_name);
         TORCH_CHECK(se == hipSuccess, op_name, ": stream synchronisation failed: ",
                     hipGetErrorString(se));
-        rc = tm_jv_status_code(reinterpret_cast<const uint32_t *>(hstatus.data_ptr<int32_t>()));
+        rc = tm_jv_status_code(slot->host);
         check_rc(rc, op_name);
         return out;
     }
