@@ -37,6 +37,10 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         ctypes.c_int,
         [_VP, ctypes.c_int64, ctypes.c_int32, ctypes.c_int32, _VP, _VP, ctypes.c_size_t, _VP, _VP],
     ),
+    "tm_jv_dense_batch_f32_noalloc": (
+        ctypes.c_int, [_VP, ctypes.c_int64, ctypes.c_int32, ctypes.c_int32, _VP, _VP, _VP]
+    ),
+    "tm_jv_noalloc_scratch_bytes": (ctypes.c_size_t, []),
     "tm_jv_compact_max_k": (ctypes.c_int32, []),
     "tm_jv_compact_batch_f32": (
         ctypes.c_int,

@@ -35,6 +35,7 @@
 // algorithm instead, so the mapping stays exact for every finite input.
 #include <hip/hip_runtime.h>
 #include <math.h>
+#include <mutex>
 #include <stdint.h>
 #include <stdlib.h>
 #include <string.h>
@@ -1355,6 +1356,69 @@ extern "C" int tm_jv_compact_batch_f32(const float *costs, int64_t B, int32_t N,
                        replay_counter(workspace));
     e = hipGetLastError();
     return e == hipSuccess ? kTmOk : kTmErrLaunch;
+}
+
+// ---------------------------------------------------------------------------
+// Entry point that allocates nothing (no counterpart in the reference): for
+// callers that cannot allocate device memory (code under graph capture, tight
+// serving loops).  Its workspace is `scratch`, a file-scope device array of a
+// fixed size (each GPU the library runs on keeps its own copy until the
+// process ends); every call on one GPU shares it, so calls that overlap on
+// one GPU race.  Nothing in it needs clearing between calls: the statistics
+// pass writes every partial record and zeroes the guard word and the replay
+// counter before the solve reads them.
+// ---------------------------------------------------------------------------
+namespace {
+constexpr size_t kScratchBytes = 8192;  // >= tm_jv_workspace_bytes(B, N, M) for every shape
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+constexpr int kScratchMaxDevices = 64;
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[kScratchMaxDevices] = {};
+
+// The device address of `scratch` on the device of `stream`, looked up once
+// per device with that device current (in host code the array's name is not
+// a device address).
+int scratch_address(hipStream_t stream, void **out) {
+    hipDevice_t dev = 0;
+    if (hipStreamGetDevice(stream, &dev) != hipSuccess || dev < 0 || dev >= kScratchMaxDevices)
+        return TM_ERR_HIP;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch_ptr[dev] == nullptr) {
+        int cur = 0;
+        if (hipGetDevice(&cur) != hipSuccess)
+            return TM_ERR_HIP;
+        if (cur != dev && hipSetDevice(dev) != hipSuccess)
+            return TM_ERR_HIP;
+        void *p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (cur != dev && hipSetDevice(cur) != hipSuccess)
+            return TM_ERR_HIP;
+        if (e != hipSuccess || p == nullptr)
+            return TM_ERR_HIP;
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return TM_OK;
+}
+} // namespace
+
+extern "C" size_t tm_jv_noalloc_scratch_bytes(void) { return kScratchBytes; }
+
+extern "C" int tm_jv_dense_batch_f32_noalloc(const float *costs, int64_t B, int32_t N,
+                                             int32_t M, int64_t *out, uint32_t *d_status,
+                                             hipStream_t stream) {
+    if (B < 0 || N < 0 || M < 0)
+        return kTmErrInvalidArgument;
+    if (B == 0 || N == 0 || M == 0)
+        return kTmOk;  // caller fills -1
+    if (tm_jv_workspace_bytes(B, N, M) > kScratchBytes)
+        return kTmErrWorkspace;
+    void *ws = nullptr;
+    const int rc = scratch_address(stream, &ws);
+    if (rc != TM_OK)
+        return rc;
+    return tm_jv_dense_batch_f32(costs, B, N, M, out, ws, kScratchBytes, d_status, stream);
 }
 
 extern "C" int32_t tm_jv_max_k(void) { return jv_large_max_k(); }
