@@ -6,29 +6,35 @@
 
 Prints ONE JSON line.  ``value`` is the BASELINE metric's lead figure:
 batched JV solves/s on C2 = float32 (1024, 64, 64) i.i.d. U[0,1), one step =
-one ``torch.ops.assignment.jonker_dense_batch`` call (pre-pass, solve, the
-validation readback the op performs), inputs resident in HBM before timing.
-The Sinkhorn leg (C4 = (16, 2048, 2048), reg 0.05, 200 iterations) reports
-iterations/s and HBM GB/s from the slope between 200- and 20-iteration runs:
-one step of this build reads K once (B*N*M*4 algorithmic bytes per
-iteration); the rate the reference's two-read formulation would need for the
-same iterations/s is reported beside it.  The CPU baseline runs the
-reference's own JV solver (oracle/_ref, compiled from its source) or, where
-absent, the C restatement, on this host's cores, rank 0 only, on a bounded
-sample; Sinkhorn's CPU baseline is the op-for-op torch restatement.
-Extra legs (skipped by --no-extra): C3 = JV on (64, 512, 768) with 20% +inf
-(solves/s), C5 = unbalanced Sinkhorn on (1, 16384, 16384) (iterations/s,
-HBM GB/s) and jonker_compact_batch on the C2 input (solves/s, with the
-reference's compact solver as its CPU baseline).  --copy-calibration runs
-only a 256 MiB device copy, the known traffic that profiler byte counters
-are scaled against.
+one ``torch.ops.assignment.jonker_dense_batch`` call (statistics pass, solve,
+the validation readback the op performs), inputs resident in HBM before
+timing.  The Sinkhorn leg (C4 = (16, 2048, 2048), reg 0.05, 200 iterations)
+reports iterations/s and HBM GB/s from the slope between 200- and
+20-iteration runs; one step of this build reads K once (B*N*M*4 algorithmic
+bytes per iteration).  Beside it, the same kernel shape at B = 64 (1 GiB of
+K, four times the 256 MB Infinity Cache) shows the rate without cache
+residency.
+
+CPU baselines run on this host's cores, rank 0 only, on bounded samples: JV
+(C2 on all threads and on one thread, C3, the compact solver) on the
+reference's own solver compiled from its source (oracle/_ref) or, where
+absent, the C restatement; Sinkhorn (C4, C5) on the op-for-op torch
+restatement.  Extra legs (skipped by --no-extra): C3 = JV on (64, 512, 768)
+with 20% +inf, C5 = unbalanced Sinkhorn on (1, 16384, 16384) and
+jonker_compact_batch on the C2 input.  --copy-calibration runs only a 256 MiB
+device copy, the known traffic that profiler byte counters are scaled
+against.  ``host`` records the CPU model, core counts and versions;
+``inputs`` the seed and sha256 of every input.
 """
 
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import os
+import platform
+import subprocess
 import sys
 import time
 from pathlib import Path
@@ -47,9 +53,15 @@ HBM_PEAK_GBS = 8000.0  # MI355X published HBM3E bandwidth
 JV_C2_RELAXATIONS = 28_681_299
 JV_BYTES_PER_RELAXATION = 12
 
+# The device kernel's certified path on the C2 seed-0 batch: its slowest
+# problem (544) takes 364 sequential steps (rows scanned + paths) in the
+# shortest-path searches, each needing one wave-wide argmin before the next
+# (oracle.jv.sap_batch_counted; tests/test_oracle_jv.py recomputes it).
+JV_C2_CRITICAL_STEPS = 364
+
 # HBM bytes per launch from rocprofv3 --pmc FETCH_SIZE (x2.00, the factor a
 # 256 MiB device copy calibrates) and WRITE_SIZE (x1.00), per dispatch; the
-# runs and commands are recorded in profiles/kernels_bench_default.md.
+# runs and commands are recorded in the profiles/ summaries.
 MEASURED_TRAFFIC = {
     # jv_stats_kernel + jv_solve_kernel on C2
     "jv_c2": int(((8244.0 + 8304.0) * 2 + 8.0 + 512.0) * 1024),
@@ -71,6 +83,60 @@ def _events_time_ms(fn, steps: int, stream) -> float:
     end.record(stream)
     torch.cuda.synchronize()
     return start.elapsed_time(end)
+
+
+def _probe_lib():
+    from torchmatch_amd import _build
+
+    if not _build.PROBE_SO.exists():
+        return None
+    lib = ctypes.CDLL(str(_build.PROBE_SO))
+    lib.tm_probe_lds_read.restype = ctypes.c_int64
+    lib.tm_probe_lds_read.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
+                                      ctypes.c_void_p]
+    lib.tm_probe_argmin_chain.restype = ctypes.c_int
+    lib.tm_probe_argmin_chain.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int,
+                                          ctypes.c_void_p]
+    return lib
+
+
+def lds_read_peak(device, iters: int = 4096, reps: int = 5) -> dict | None:
+    """LDS read bandwidth of the whole chip (bench_probes.so): 8 workgroups
+    of 256 lanes per CU stream conflict-free 16-byte LDS reads."""
+    lib = _probe_lib()
+    if lib is None:
+        return None
+    cus = torch.cuda.get_device_properties(device).multi_processor_count
+    blocks = 8 * cus
+    sink = torch.zeros(blocks, dtype=torch.int32, device=device)
+    stream = torch.cuda.current_stream(device)
+    run = lambda: lib.tm_probe_lds_read(sink.data_ptr(), blocks, iters, stream.cuda_stream)
+    nbytes = run()
+    if nbytes <= 0:
+        return None
+    best = min(_events_time_ms(run, 1, stream) for _ in range(reps))
+    return {"gbs": nbytes / (best * 1e-3) / 1e9, "cus": cus,
+            "probe": f"{blocks} workgroups x 256 lanes x {iters} ds_read_b128"}
+
+
+def argmin_chain(device, iters: int = 20000) -> dict | None:
+    """Cycles per dependent wave-wide (minimum, argmin lane) round and the
+    shader clock, from one wave (bench_probes.so)."""
+    lib = _probe_lib()
+    if lib is None:
+        return None
+    x = torch.rand(64, device=device)
+    out = torch.zeros(3, dtype=torch.int64, device=device)
+    stream = torch.cuda.current_stream(device).cuda_stream
+    best = None
+    for _ in range(3):
+        if lib.tm_probe_argmin_chain(x.data_ptr(), out.data_ptr(), iters, stream) != 0:
+            return None
+        cycles, ticks = (int(v) for v in out[:2].cpu())
+        if best is None or cycles < best[0]:
+            best = (cycles, ticks)
+    cycles, ticks = best
+    return {"cycles_per_round": cycles / iters, "clock_ghz": cycles / (ticks * 10.0)}
 
 
 def bench_jv(steps: int, warmup: int, device) -> dict:
@@ -109,15 +175,20 @@ def bench_jv(steps: int, warmup: int, device) -> dict:
     kernel_ms = _events_time_ms(launch, kreps, stream) / kreps
     assert lib.tm_jv_check_status(status.data_ptr(), sp) == 0
     assert torch.equal(outk, out)
+    replays = ctypes.c_uint32(0)
+    lib.tm_jv_read_replays(ctypes.c_void_p(ws.data_ptr()), ctypes.byref(replays),
+                           ctypes.c_void_p(sp))
+
     bytes_per_launch = B * N * M * 4 + B * N * 8
     achieved = bytes_per_launch / (kernel_ms * 1e-3) / 1e9
-    # LDS roofline of the solve: algorithmic LDS bytes (12 per relaxation) over
-    # the launch time, against the measured LDS read peak
+    # LDS roofline: algorithmic LDS bytes (12 per relaxation of the reference
+    # algorithm) over the launch time, against the measured LDS read peak
     lds_bytes = JV_C2_RELAXATIONS * JV_BYTES_PER_RELAXATION
     lds_achieved = lds_bytes / (kernel_ms * 1e-3) / 1e9
     peak = lds_read_peak(device)
     lds_roofline = {
         "bound": "lds",
+        "binding": False,
         "achieved": round(lds_achieved, 1),
         "peak": round(peak["gbs"], 1) if peak else None,
         "unit": "GB/s",
@@ -126,60 +197,72 @@ def bench_jv(steps: int, warmup: int, device) -> dict:
         "relaxations_per_solve": round(JV_C2_RELAXATIONS / B, 1),
         "peak_probe": peak["probe"] if peak else "probe library not built",
     }
+    # The binding resource: each problem is a chain of dependent steps and a
+    # launch waits for its slowest problem.  Floor: the slowest problem's
+    # sequential search steps, each at least one dependent wave-wide argmin
+    # (measured live), against the launch time.
+    chain = argmin_chain(device)
+    latency = None
+    if chain:
+        floor_us = JV_C2_CRITICAL_STEPS * chain["cycles_per_round"] / (chain["clock_ghz"] * 1e3)
+        latency = {
+            "bound": "latency",
+            "binding": True,
+            "achieved": round(kernel_ms * 1e3, 2),
+            "floor": round(floor_us, 2),
+            "unit": "us per launch",
+            "frac": round(floor_us / (kernel_ms * 1e3), 4),
+            "critical_problem_steps": JV_C2_CRITICAL_STEPS,
+            "argmin_cycles": round(chain["cycles_per_round"], 1),
+            "clock_ghz": round(chain["clock_ghz"], 3),
+            "note": "floor = slowest problem's search steps x one dependent wave-wide "
+                    "argmin; achieved = statistics pass + solve launch",
+        }
+    # other seeds: problems that fail the certificate replay the reference
+    # order, so batches differ in time
+    seeds = {}
+    for seed in (1, 2, 3):
+        c = workloads.jv_uniform(B, N, M, seed=seed).to(device)
+        op(c)
+        torch.cuda.synchronize()
+        seeds[str(seed)] = round(sorted(_events_time_ms(lambda: op(c), 1, stream)
+                                        for _ in range(5))[2], 4)
     return {
         "solves_per_s": B / (ms_per_step * 1e-3),
         "ms_per_step": ms_per_step,
         "wall_s": wall,
         "kernel_ms": kernel_ms,
         "kernel_solves_per_s": B / (kernel_ms * 1e-3),
+        "replays": replays.value,
+        "other_seeds_op_ms": seeds,
         "roofline": {
             "bound": "hbm",
+            "binding": False,
             "achieved": round(achieved, 3),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 6),
             "traffic": MEASURED_TRAFFIC["jv_c2"],
-            "note": "stats pre-pass + LDS-resident solve per launch; the solve is a "
-                    "latency-bound sequential chain per problem, HBM is not binding",
+            "note": "statistics pass + LDS-resident solve per launch; HBM is not binding, "
+                    "the per-problem dependency chain is (latency_roofline)",
         },
         "lds_roofline": lds_roofline,
+        "latency_roofline": latency,
         "cost_sha256": workloads.sha256(cost_cpu),
         "out": out,
     }
 
 
-def lds_read_peak(device, iters: int = 4096, reps: int = 5) -> dict | None:
-    """LDS read bandwidth of the whole chip (lib/libtm_lds_probe.so): 8
-    workgroups of 256 lanes per CU stream conflict-free 16-byte LDS reads."""
-    import ctypes
-
-    from torchmatch_amd import _build
-
-    if not _build.PROBE_SO.exists():
-        return None
-    lib = ctypes.CDLL(str(_build.PROBE_SO))
-    lib.tm_probe_lds_read.restype = ctypes.c_int64
-    lib.tm_probe_lds_read.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
-                                      ctypes.c_void_p]
-    cus = torch.cuda.get_device_properties(device).multi_processor_count
-    blocks = 8 * cus
-    sink = torch.zeros(blocks, dtype=torch.int32, device=device)
-    stream = torch.cuda.current_stream(device)
-    run = lambda: lib.tm_probe_lds_read(sink.data_ptr(), blocks, iters, stream.cuda_stream)
-    nbytes = run()
-    if nbytes <= 0:
-        return None
-    best = min(_events_time_ms(run, 1, stream) for _ in range(reps))
-    return {"gbs": nbytes / (best * 1e-3) / 1e9, "cus": cus,
-            "probe": f"{blocks} workgroups x 256 lanes x {iters} ds_read_b128"}
-
-
-def bench_sinkhorn(device, n_long: int = 200, n_short: int = 20, reps: int = 3) -> dict:
+def bench_sinkhorn(device, B: int = 16, n_long: int = 200, n_short: int = 20,
+                   reps: int = 3) -> dict:
     from torchmatch_amd import workloads
 
-    B, N, M = 16, 2048, 2048
+    N = M = 2048
     reg = 0.05
-    cost = workloads.sinkhorn_points(B, N, M, 8, seed=0).to(device)
+    cost_cpu = workloads.sinkhorn_points(B, N, M, 8, seed=0)
+    sha = workloads.sha256(cost_cpu)
+    cost = cost_cpu.to(device)
+    del cost_cpu
     a = torch.full((B, N), 1.0 / N, device=device)
     b = torch.full((B, M), 1.0 / M, device=device)
     op = torch.ops.transport.log_sinkhorn
@@ -188,29 +271,27 @@ def bench_sinkhorn(device, n_long: int = 200, n_short: int = 20, reps: int = 3) 
     torch.cuda.synchronize()
 
     def best(n_iter):
-        times = []
-        for _ in range(reps):
-            times.append(_events_time_ms(lambda: op(cost, reg, n_iter, a, b), 1, stream))
-        return min(times)
+        return min(_events_time_ms(lambda: op(cost, reg, n_iter, a, b), 1, stream)
+                   for _ in range(reps))
 
     t_long = best(n_long)
     t_short = best(n_short)
     per_iter_ms = (t_long - t_short) / (n_long - n_short)
+    traffic = MEASURED_TRAFFIC.get("sinkhorn_c4") if B == 16 else None
     return {
-        "config": {"workload": "log_sinkhorn C4", "B": B, "N": N, "M": M, "reg": reg,
-                   "n_iter": n_long},
+        "config": {"workload": "log_sinkhorn C4" if B == 16 else "log_sinkhorn C4 shape",
+                   "B": B, "N": N, "M": M, "reg": reg, "n_iter": n_long},
         "iters_per_s": 1e3 / per_iter_ms,
         "ms_per_iter": per_iter_ms,
-        "op_ms_200_iters": t_long,
-        **_sinkhorn_roofline(B, N, M, per_iter_ms, MEASURED_TRAFFIC.get("sinkhorn_c4")),
+        f"op_ms_{n_long}_iters": t_long,
+        "cost_sha256": sha,
+        **_sinkhorn_roofline(B, N, M, per_iter_ms, traffic),
     }
 
 
 def _sinkhorn_roofline(B, N, M, per_iter_ms, traffic) -> dict:
     """One step of this build reads K once (row LSE and the column sums come
-    from the same registers): B*N*M*4 algorithmic bytes per iteration.  The
-    reference's formulation reads K once per half-step; the rate it would need
-    for the same iterations/s is reported beside it."""
+    from the same registers): B*N*M*4 algorithmic bytes per iteration."""
     one_read = B * N * M * 4
     gbs = one_read / (per_iter_ms * 1e-3) / 1e9
     return {
@@ -224,7 +305,6 @@ def _sinkhorn_roofline(B, N, M, per_iter_ms, traffic) -> dict:
             "bytes_per_iter": one_read,
             "note": "fused step: one read of K per iteration (+ column partials)",
         },
-        "two_pass_equiv_gbs": round(2 * one_read / (per_iter_ms * 1e-3) / 1e9, 1),
     }
 
 
@@ -232,13 +312,23 @@ def bench_jv_c3(device, reps: int = 3) -> dict:
     """C3: (64, 512, 768) squared distances + jitter, 20% +inf (K = 768 kernel)."""
     from torchmatch_amd import workloads
 
-    cost = workloads.jv_rect_masked().to(device)
+    cost_cpu = workloads.jv_rect_masked()
+    cost = cost_cpu.to(device)
     op = torch.ops.assignment.jonker_dense_batch
     op(cost)
     torch.cuda.synchronize()
     ms = _events_time_ms(lambda: op(cost), reps, torch.cuda.current_stream(device)) / reps
-    return {"config": {"workload": "jonker_dense_batch C3", "B": 64, "N": 512, "M": 768},
-            "solves_per_s": 64 / (ms * 1e-3), "ms_per_batch": ms}
+    B, N, M = cost.shape
+    nbytes = B * N * M * 4 + B * N * 8
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {"config": {"workload": "jonker_dense_batch C3", "B": B, "N": N, "M": M},
+            "solves_per_s": B / (ms * 1e-3), "ms_per_batch": ms,
+            "cost_sha256": workloads.sha256(cost_cpu),
+            "roofline": {"bound": "hbm", "binding": False, "achieved": round(gbs, 3),
+                         "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(gbs / HBM_PEAK_GBS, 6), "traffic": None,
+                         "note": "one wave per problem walks a dependency chain over an "
+                                 "L2 / Infinity-Cache resident tile; HBM is not binding"}}
 
 
 def bench_jv_compact(device, reps: int = 20) -> dict:
@@ -256,14 +346,26 @@ def bench_jv_compact(device, reps: int = 20) -> dict:
             "solves_per_s": 1024 / (ms * 1e-3), "ms_per_batch": ms}
 
 
+def _c5_inputs():
+    from torchmatch_amd import workloads
+
+    N = 16384
+    cost = workloads.sinkhorn_points(1, N, N, 8, seed=0)
+    a = workloads.dirichlet(1, N, 1.0, seed=1)
+    b = workloads.dirichlet(1, N, 1.3, seed=2)
+    return cost, a, b
+
+
 def bench_unbalanced_c5(device, n_long: int = 100, n_short: int = 20) -> dict:
     """C5: unbalanced Sinkhorn on (1, 16384, 16384), reg 0.02, rho 1 (slope)."""
     from torchmatch_amd import workloads
 
-    N = 16384
-    cost = workloads.sinkhorn_points(1, N, N, 8, seed=0).to(device)
-    a = workloads.dirichlet(1, N, 1.0, seed=1).to(device)
-    b = workloads.dirichlet(1, N, 1.3, seed=2).to(device)
+    cost_cpu, a_cpu, b_cpu = _c5_inputs()
+    shas = {"cost": workloads.sha256(cost_cpu), "a": workloads.sha256(a_cpu),
+            "b": workloads.sha256(b_cpu)}
+    N = cost_cpu.shape[1]
+    cost, a, b = cost_cpu.to(device), a_cpu.to(device), b_cpu.to(device)
+    del cost_cpu
     op = torch.ops.transport.unbalanced_sinkhorn
     stream = torch.cuda.current_stream(device)
     op(cost, 0.02, n_short, 1.0, a, b)
@@ -276,6 +378,7 @@ def bench_unbalanced_c5(device, n_long: int = 100, n_short: int = 20) -> dict:
     return {"config": {"workload": "unbalanced_sinkhorn C5", "B": 1, "N": N, "M": N,
                        "reg": 0.02, "rho": 1.0},
             "iters_per_s": 1e3 / per_iter_ms, "ms_per_iter": per_iter_ms,
+            "input_sha256": shas,
             **_sinkhorn_roofline(1, N, N, per_iter_ms, MEASURED_TRAFFIC.get("sinkhorn_c5"))}
 
 
@@ -290,31 +393,37 @@ def copy_calibration(device, mib: int = 256, reps: int = 5) -> dict:
     return {"copy_bytes_each_way": n * 4, "reps": reps}
 
 
-def cpu_baseline_jv(budget_s: float = 10.0, compact: bool = False) -> dict:
+def _time_median(fn, budget_s: float, min_runs: int = 5) -> tuple[float, int]:
+    fn()  # warm-up
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while time.perf_counter() < t_end or len(times) < min_runs:
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    return times[len(times) // 2], len(times)
+
+
+def cpu_baseline_jv(budget_s: float = 10.0, compact: bool = False, threads: int | None = None,
+                    cost=None, label: str = "C2 (1024,64,64) seed 0") -> dict:
     from oracle import jv
     from torchmatch_amd import workloads
 
-    cost = workloads.jv_uniform(1024, 64, 64, seed=0).numpy()
-    threads = jv.default_threads()
+    if cost is None:
+        cost = workloads.jv_uniform(1024, 64, 64, seed=0).numpy()
+    threads = jv.default_threads() if threads is None else threads
     if jv.ref_available():
         fn, kind = (jv.ref_jv_compact_batch if compact else jv.ref_jv_dense_batch), "reference"
     else:
         fn, kind = (jv.jv_compact_batch if compact else jv.jv_dense_batch), "port"
-    fn(cost, threads)  # warm-up
-    times = []
-    t_end = time.perf_counter() + budget_s
-    while time.perf_counter() < t_end or len(times) < 5:
-        t0 = time.perf_counter()
-        fn(cost, threads)
-        times.append(time.perf_counter() - t0)
-    times.sort()
-    med = times[len(times) // 2]
+    med, runs = _time_median(lambda: fn(cost, threads), budget_s)
     return {
-        "value": 1024 / med,
+        "value": cost.shape[0] / med,
         "unit": "solves/s",
         "cores": threads,
         "kind": kind,
-        "sample": f"C2 (1024,64,64) seed 0, {len(times)} runs over ~{budget_s:.0f}s, median",
+        "sample": f"{label}, {runs} runs over ~{budget_s:.0f}s, median",
     }
 
 
@@ -338,6 +447,56 @@ def cpu_baseline_sinkhorn(n_iter: int = 3) -> dict:
         "kind": "port",
         "sample": f"C4 (16,2048,2048) reg 0.05, slope of {1 + n_iter} vs 1 iterations",
     }
+
+
+def cpu_baseline_unbalanced_c5(n_iter: int = 2) -> dict:
+    from oracle import sinkhorn as sk
+
+    cost, a, b = _c5_inputs()
+    t0 = time.perf_counter()
+    sk.unbalanced_sinkhorn_plan(cost, eps=0.02, n_iter=1, rho=1.0, a=a, b=b)
+    t1 = time.perf_counter()
+    sk.unbalanced_sinkhorn_plan(cost, eps=0.02, n_iter=1 + n_iter, rho=1.0, a=a, b=b)
+    t2 = time.perf_counter()
+    per_iter = ((t2 - t1) - (t1 - t0)) / n_iter
+    return {
+        "value": 1.0 / per_iter if per_iter > 0 else None,
+        "unit": "iters/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": f"C5 (1,16384,16384) reg 0.02 rho 1, slope of {1 + n_iter} vs 1 iterations",
+    }
+
+
+def host_facts() -> dict:
+    model = platform.processor() or None
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for ln in out.splitlines():
+            if ln.startswith("Model name:"):
+                model = ln.split(":", 1)[1].strip()
+    except (OSError, subprocess.SubprocessError):
+        pass
+    hipcc = None
+    try:
+        out = subprocess.run(["hipcc", "--version"], capture_output=True, text=True,
+                             timeout=30).stdout
+        hipcc = next((ln.strip() for ln in out.splitlines() if "HIP version" in ln), None)
+    except (OSError, subprocess.SubprocessError):
+        pass
+    return {
+        "cpu_model": model,
+        "os_cpu_count": os.cpu_count(),
+        "torch_threads": torch.get_num_threads(),
+        "torch": torch.__version__,
+        "hip": torch.version.hip,
+        "hipcc": hipcc,
+        "gpu": torch.cuda.get_device_name(0),
+    }
+
+
+def _round(d: dict, nd: int) -> dict:
+    return {k: (round(v, nd) if isinstance(v, float) else v) for k, v in d.items()}
 
 
 def main() -> int:
@@ -366,6 +525,8 @@ def main() -> int:
         print(json.dumps(copy_calibration(device)), flush=True)
         return 0
     jv_res = bench_jv(args.steps, args.warmup, device)
+    inputs = {"C2": {"generator": "torch.rand U[0,1)", "seed": 0,
+                     "sha256": jv_res["cost_sha256"]}}
     line = {
         "metric": "batched JV solves/s (B=1024,N=64) + log_sinkhorn iters/s & HBM GB/s, 1 GPU",
         "value": round(jv_res["solves_per_s"], 1),
@@ -383,27 +544,48 @@ def main() -> int:
         "config": {"workload": "jonker_dense_batch C2", "B": 1024, "N": 64, "M": 64,
                    "parallelism": "single GPU, one problem per 64-lane workgroup"},
         "kernel": {"ms_per_launch": round(jv_res["kernel_ms"], 5),
-                   "solves_per_s": round(jv_res["kernel_solves_per_s"], 1)},
+                   "solves_per_s": round(jv_res["kernel_solves_per_s"], 1),
+                   "replays": jv_res["replays"],
+                   "other_seeds_op_ms": jv_res["other_seeds_op_ms"]},
         "roofline": jv_res["roofline"],
         "lds_roofline": jv_res["lds_roofline"],
+        "latency_roofline": jv_res["latency_roofline"],
     }
     if not args.no_sinkhorn:
         sk = bench_sinkhorn(device)
-        line["sinkhorn"] = {k: (round(v, 4) if isinstance(v, float) else v)
-                            for k, v in sk.items()}
+        inputs["C4"] = {"generator": "sinkhorn_points D=8 / global max, a=b=1/2048",
+                        "seed": 0, "sha256": sk.pop("cost_sha256")}
+        line["sinkhorn"] = _round(sk, 4)
+        # the same kernel shape at B = 64: 1 GiB of K cannot stay in the
+        # 256 MB Infinity Cache between iterations
+        ctl = bench_sinkhorn(device, B=64, n_long=60, n_short=10)
+        ctl.pop("cost_sha256")
+        line["sinkhorn_b64_control"] = _round(ctl, 4)
     if not args.no_extra:
-        line["jv_c3"] = {k: (round(v, 3) if isinstance(v, float) else v)
-                         for k, v in bench_jv_c3(device).items()}
-        line["unbalanced_c5"] = {k: (round(v, 4) if isinstance(v, float) else v)
-                                 for k, v in bench_unbalanced_c5(device).items()}
-        line["jv_compact_c2"] = {k: (round(v, 4) if isinstance(v, float) else v)
-                                 for k, v in bench_jv_compact(device).items()}
+        c3 = bench_jv_c3(device)
+        inputs["C3"] = {"generator": "jv_rect_masked D=16, 20% +inf", "seed": 0,
+                        "sha256": c3.pop("cost_sha256")}
+        line["jv_c3"] = _round(c3, 3)
+        c5 = bench_unbalanced_c5(device)
+        inputs["C5"] = {"generator": "sinkhorn_points D=8; Dirichlet(1) x 1.0 / 1.3",
+                        "seeds": {"cost": 0, "a": 1, "b": 2}, "sha256": c5.pop("input_sha256")}
+        line["unbalanced_c5"] = _round(c5, 4)
+        line["jv_compact_c2"] = _round(bench_jv_compact(device), 4)
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline_jv()
+        line["cpu_baseline_single_thread"] = cpu_baseline_jv(3.0, threads=1)
         if not args.no_extra:
+            from torchmatch_amd import workloads
+
             line["jv_compact_c2"]["cpu_baseline"] = cpu_baseline_jv(5.0, compact=True)
+            line["jv_c3"]["cpu_baseline"] = cpu_baseline_jv(
+                5.0, cost=workloads.jv_rect_masked().numpy(),
+                label="C3 (64,512,768) 20% +inf seed 0")
+            line["unbalanced_c5"]["cpu_baseline"] = cpu_baseline_unbalanced_c5()
         if not args.no_sinkhorn:
             line["sinkhorn"]["cpu_baseline"] = cpu_baseline_sinkhorn()
+    line["host"] = host_facts()
+    line["inputs"] = inputs
     print(json.dumps(line), flush=True)
     return 0
 

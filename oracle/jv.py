@@ -58,6 +58,8 @@ def oracle_lib() -> ctypes.CDLL:
         _F32P, ctypes.c_int64, ctypes.c_int32, ctypes.c_int32, _I64P, _I64P,
     ]
     lib.jvo_dense_batch_counted.restype = ctypes.c_int
+    lib.jvo_sap_batch_counted.argtypes = lib.jvo_dense_batch_counted.argtypes
+    lib.jvo_sap_batch_counted.restype = ctypes.c_int
     lib.jvo_compact_batch.argtypes = lib.jvo_dense_batch.argtypes
     lib.jvo_compact_batch.restype = ctypes.c_int
     lib.jvo_sentinel.argtypes = [_F32P, ctypes.c_int64, ctypes.c_int32, _F32P]
@@ -131,6 +133,23 @@ def jv_dense_batch_counted(costs) -> tuple[np.ndarray, np.ndarray]:
     out = np.empty((b, n), dtype=np.int64)
     counts = np.zeros((max(b, 1), 3), dtype=np.int64)
     rc = oracle_lib().jvo_dense_batch_counted(
+        arr.ctypes.data_as(_F32P), b, n, m, out.ctypes.data_as(_I64P),
+        counts.ctypes.data_as(_I64P),
+    )
+    _raise(rc)
+    return out, counts[:b]
+
+
+def sap_batch_counted(costs) -> tuple[np.ndarray, np.ndarray]:
+    """Work model of the device's certified path (column reduction, then
+    shortest augmenting paths, no row reduction): mapping and per-problem
+    counts (B, 3) as :func:`jv_dense_batch_counted`.  Not a reference
+    function; its scanned rows + paths are the path's sequential steps."""
+    arr = _prep(costs)
+    b, n, m = arr.shape
+    out = np.empty((b, n), dtype=np.int64)
+    counts = np.zeros((max(b, 1), 3), dtype=np.int64)
+    rc = oracle_lib().jvo_sap_batch_counted(
         arr.ctypes.data_as(_F32P), b, n, m, out.ctypes.data_as(_I64P),
         counts.ctypes.data_as(_I64P),
     )

@@ -317,6 +317,18 @@ static void jvo_square(uint32_t n, const float *c, jvo_scratch *s, jvo_counts *c
         jvo_augment(n, c, (uint32_t)n_free, s, cnt);
 }
 
+/* Work model of the device kernel's certified path (not a reference
+ * function): the same column reduction, then one shortest augmenting path per
+ * free row with no augmenting row reduction.  Counted per problem, the
+ * searches' scanned rows + paths are the sequential steps that path takes on
+ * the device.  Its mapping equals the reference's whenever the optimum is
+ * unique (the device keeps it only then). */
+static void jvo_sap_square(uint32_t n, const float *c, jvo_scratch *s, jvo_counts *cnt) {
+    const int32_t n_free = jvo_column_reduction(n, c, s, cnt);
+    if (n_free > 0)
+        jvo_augment(n, c, (uint32_t)n_free, s, cnt);
+}
+
 /* ---- jonker_compact_batch: the square JV of jonker_compact_core.h ---------- */
 
 #define JVOC_FLT_MAX 3.402823466e38f /* numeric_limits<float>::max() */
@@ -640,6 +652,22 @@ int jvo_dense_batch_counted(const float *costs, int64_t B, int32_t N, int32_t M,
     if (!cnt)
         return JVO_ERR_ALLOC;
     const int rc = jvo_batch_impl(costs, B, N, M, out, 1, cnt, jvo_square);
+    for (int64_t b = 0; b < B; ++b) {
+        counts3[3 * b + 0] = cnt[b].relax;
+        counts3[3 * b + 1] = cnt[b].paths;
+        counts3[3 * b + 2] = cnt[b].scans;
+    }
+    free(cnt);
+    return rc;
+}
+
+/* jvo_sap_square over a batch, single-threaded, with the same counters. */
+int jvo_sap_batch_counted(const float *costs, int64_t B, int32_t N, int32_t M, int64_t *out,
+                          int64_t *counts3) {
+    jvo_counts *cnt = (jvo_counts *)calloc((size_t)(B > 0 ? B : 1), sizeof(jvo_counts));
+    if (!cnt)
+        return JVO_ERR_ALLOC;
+    const int rc = jvo_batch_impl(costs, B, N, M, out, 1, cnt, jvo_sap_square);
     for (int64_t b = 0; b < B; ++b) {
         counts3[3 * b + 0] = cnt[b].relax;
         counts3[3 * b + 1] = cnt[b].paths;

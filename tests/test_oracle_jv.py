@@ -155,6 +155,23 @@ def test_bench_relaxation_count():
     assert (counts[:, 0] >= 64 * 64).all()
 
 
+def test_bench_critical_steps():
+    """bench.py floors the JV launch at the slowest C2 seed-0 problem's
+    sequential search steps under the kernel's certified path; the work model
+    gives the same mappings as the reference on that batch (its optimum is
+    unique everywhere) and the constant bench.py carries."""
+    import bench
+
+    c = workloads.jv_uniform(1024, 64, 64, seed=0).numpy()
+    out, counts = jv.sap_batch_counted(c)
+    np.testing.assert_array_equal(out, jv.jv_dense_batch(c))
+    steps = counts[:, 1] + counts[:, 2]
+    assert int(steps.max()) == bench.JV_C2_CRITICAL_STEPS
+    # the reference order's augmenting row reduction is skipped: fewer
+    # relaxations than the reference's count
+    assert int(counts[:, 0].sum()) < bench.JV_C2_RELAXATIONS
+
+
 def test_unpack_restatement_known_cases():
     """Hand-worked unpacks (ops.cpp:387-414): row order of matches, increasing
     unmatched rows / columns, -1 padding."""

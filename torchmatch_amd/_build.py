@@ -6,9 +6,10 @@ Produces, next to this file:
   the HIP kernels in ``csrc/*.hip``, compiled by ``hipcc --offload-arch=gfx950``;
 * ``_C.so`` -- torch dispatcher registrations (``csrc/torch_ops.cpp``) linked
   against the C-ABI library; loaded with ``torch.ops.load_library``;
-* ``lib/libtm_lds_probe.so`` -- the LDS read-bandwidth microbenchmark
-  (``csrc/lds_probe.hip``) that ``bench.py`` prices the JV kernels against;
-  measurement support, not part of the C ABI.
+* ``bench_probes.so`` at the repository root -- the microbenchmarks
+  ``bench.py`` prices the JV kernels against (``bench_probes.hip``: LDS read
+  bandwidth, wave-wide argmin latency); measurement support for the
+  benchmark, not part of the package or the C ABI.
 
 ``python torchmatch_amd/_build.py`` runs it; ``__graft_entry__.build()`` calls
 :func:`build` too.  hipcc cross-compiles, so no GPU is needed.
@@ -29,7 +30,8 @@ INCLUDE = PKG.parent / "include"
 LIB_DIR = PKG / "lib"
 CABI_SO = LIB_DIR / "libtorchmatch_amd.so"
 OPS_SO = PKG / "_C.so"
-PROBE_SO = LIB_DIR / "libtm_lds_probe.so"
+PROBE_SRC = PKG.parent / "bench_probes.hip"
+PROBE_SO = PKG.parent / "bench_probes.so"
 
 HIP_SOURCES = ["jv_batch.hip", "jv_large.hip", "jv_unpack.hip", "sinkhorn.hip"]
 ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
@@ -79,11 +81,10 @@ def build_cabi(verbose: bool = True) -> Path:
 
 
 def build_probe(verbose: bool = True) -> Path:
-    """Compile the LDS bandwidth probe into lib/libtm_lds_probe.so."""
-    LIB_DIR.mkdir(exist_ok=True)
+    """Compile the benchmark's microbenchmarks into bench_probes.so."""
     tmp = PROBE_SO.with_suffix(".so.tmp")
-    _run(["hipcc", *HIPCC_FLAGS, "-shared", "-o", str(tmp), str(CSRC / "lds_probe.hip"),
-          f"-Wl,-rpath,{ROCM / 'lib'}"], verbose)
+    _run(["hipcc", *HIPCC_FLAGS, "-I", str(PKG.parent), "-shared", "-o", str(tmp),
+          str(PROBE_SRC), f"-Wl,-rpath,{ROCM / 'lib'}"], verbose)
     os.replace(tmp, PROBE_SO)
     return PROBE_SO
 
