@@ -64,12 +64,12 @@ JV_C2_CRITICAL_STEPS = 364
 # runs and commands are recorded in the profiles/ summaries.
 MEASURED_TRAFFIC = {
     # jv_stats_kernel + jv_solve_kernel on C2
-    "jv_c2": int(((8244.0 + 8304.0) * 2 + 8.0 + 512.0) * 1024),
+    "jv_c2": int(((8230.5 + 8351.5) * 2 + 8.1 + 512.0) * 1024),
     # sk_fused_step + sk_col_merge_blk per C4 iteration: two batch groups of 8,
     # each one pass + one merge (K once, column sums twice)
-    "sinkhorn_c4": int(2 * ((66321.6 + 1173.5) * 2 + 2176.0 + 128.0) * 1024),
+    "sinkhorn_c4": int(2 * ((66330.7 + 1173.5) * 2 + 2176.1 + 128.0) * 1024),
     # the same pair per C5 iteration (one group)
-    "sinkhorn_c5": int(((525986.7 + 8358.5) * 2 + 17530.0 + 128.0) * 1024),
+    "sinkhorn_c5": int(((525986.8 + 8354.5) * 2 + 17532.1 + 128.0) * 1024),
 }
 
 
@@ -469,6 +469,9 @@ def cpu_baseline_unbalanced_c5(n_iter: int = 2) -> dict:
 
 
 def host_facts() -> dict:
+    """CPU model, core counts and versions.  Runs lscpu and hipcc as child
+    processes, so main() calls it before anything touches the GPU (a child
+    forked from a process with the GPU initialised must not exec)."""
     model = platform.processor() or None
     try:
         out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
@@ -491,7 +494,6 @@ def host_facts() -> dict:
         "torch": torch.__version__,
         "hip": torch.version.hip,
         "hipcc": hipcc,
-        "gpu": torch.cuda.get_device_name(0),
     }
 
 
@@ -511,6 +513,7 @@ def main() -> int:
     p.add_argument("--copy-calibration", action="store_true",
                    help="only run a 256 MiB device copy (profiler counter calibration)")
     args = p.parse_args()
+    host = None if args.copy_calibration else host_facts()  # before the GPU is touched
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU only (each box has one MI355X); "
               "run with --gpus 1", file=sys.stderr)
@@ -584,7 +587,8 @@ def main() -> int:
             line["unbalanced_c5"]["cpu_baseline"] = cpu_baseline_unbalanced_c5()
         if not args.no_sinkhorn:
             line["sinkhorn"]["cpu_baseline"] = cpu_baseline_sinkhorn()
-    line["host"] = host_facts()
+    host["gpu"] = torch.cuda.get_device_name(0)
+    line["host"] = host
     line["inputs"] = inputs
     print(json.dumps(line), flush=True)
     return 0
