@@ -35,8 +35,10 @@
  *                           those checks, one synchronisation for all.
  *   tm_sinkhorn_iterate_f32 sources/torchmatch/transport/matrix/_log_sinkhorn.py:136-221
  *   tm_sinkhorn_f32         (log_sinkhorn_plan) and
- *                           transport/matrix/_unbalanced_sinkhorn.py:30-103
- *                           (unbalanced_sinkhorn_plan).
+ *   tm_sinkhorn_f64         transport/matrix/_unbalanced_sinkhorn.py:30-103
+ *                           (unbalanced_sinkhorn_plan); the f64 entry for
+ *                           float64 costs, which the reference iterates in
+ *                           float64.
  */
 #ifndef TORCHMATCH_AMD_H
 #define TORCHMATCH_AMD_H
@@ -232,6 +234,23 @@ int tm_sinkhorn_iterate_f32(const float *cost, const uint8_t *keep, int64_t B, i
 int tm_sinkhorn_f32(const float *cost, const float *a, const float *b, int64_t B, int64_t N,
                     int64_t M, const double *eps_sched, int32_t n_iter, double rho,
                     float *log_plan, float *log_u, float *log_v, void *workspace,
+                    size_t workspace_bytes, hipStream_t stream);
+
+/* ---- float64 Sinkhorn ---------------------------------------------------
+ * The reference iterates in the cost's dtype (transport/matrix/
+ * _log_sinkhorn.py:184,191, _unbalanced_sinkhorn.py:60,67): a float64 cost
+ * is solved in float64, with the same recurrence, shift rule, keep-previous
+ * rule, damping and plan expression as tm_sinkhorn_iterate_f32.  The caller
+ * validates the cost (no NaN / -inf), fuses any mask into it (+inf) and
+ * builds the schedule; nothing is read back.
+ *   cost, a, b, log_plan, log_u, log_v  device float64 tensors of the shapes
+ *   and meanings of tm_sinkhorn_f32; log_plan may be NULL
+ *   workspace  device, >= tm_sinkhorn_f64_workspace_bytes(B, N, M)
+ * B <= 65535. */
+size_t tm_sinkhorn_f64_workspace_bytes(int64_t B, int64_t N, int64_t M);
+int tm_sinkhorn_f64(const double *cost, const double *a, const double *b, int64_t B,
+                    int64_t N, int64_t M, const double *eps_sched, int32_t n_iter, double rho,
+                    double *log_plan, double *log_u, double *log_v, void *workspace,
                     size_t workspace_bytes, hipStream_t stream);
 
 #ifdef __cplusplus

@@ -204,6 +204,22 @@ def test_solve_dispatch_and_unpack(device):
     assert torchmatch_amd.assignment.resolve_backend(cost.to(device)) == "jonker_dense_batch"
 
 
+@pytest.mark.parametrize(("n", "m", "p_inf"), [(12, 20, 0.0), (20, 12, 0.0), (30, 30, 0.6)])
+def test_solve_2d_unpack(n, m, p_inf, device):
+    """2-D solve(unpack=True): the device unpack on a batch of one, trimmed of
+    its -1 padding as the reference's 2-D unpack returns it
+    (assignment/_solve.py:124-164): matches (k, 2), unmatched rows (n - k),
+    unmatched columns (m - k)."""
+    cost = workloads.jv_rect_masked(B=1, N=n, M=m, p_inf=p_inf, seed=n * m)
+    matches, ur, uc, nm = jv.unpack_packed(jv.jv_dense_batch(cost.numpy()), m)
+    k = int(nm[0])
+    got = torchmatch_amd.assignment.solve(cost[0].to(device), unpack=True)
+    assert len(got) == 3
+    np.testing.assert_array_equal(got[0].cpu().numpy(), matches[0, :k])
+    np.testing.assert_array_equal(got[1].cpu().numpy(), ur[0, : n - k])
+    np.testing.assert_array_equal(got[2].cpu().numpy(), uc[0, : m - k])
+
+
 @pytest.mark.parametrize(("b", "n", "m", "p_inf"), [
     (64, 64, 64, 0.0), (32, 40, 64, 0.5), (16, 64, 30, 0.3), (8, 500, 768, 0.2),
     (4, 1, 1, 0.0), (3, 1000, 900, 0.9),

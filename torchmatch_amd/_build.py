@@ -33,7 +33,7 @@ OPS_SO = PKG / "_C.so"
 PROBE_SRC = PKG.parent / "bench_probes.hip"
 PROBE_SO = PKG.parent / "bench_probes.so"
 
-HIP_SOURCES = ["jv_batch.hip", "jv_large.hip", "jv_unpack.hip", "sinkhorn.hip"]
+HIP_SOURCES = ["jv_batch.hip", "jv_large.hip", "jv_unpack.hip", "sinkhorn.hip", "sinkhorn64.hip"]
 ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
 ARCH = "gfx950"
 

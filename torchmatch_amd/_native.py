@@ -86,6 +86,17 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
             _VP, _VP, _VP, _VP, ctypes.c_size_t, _VP,
         ],
     ),
+    "tm_sinkhorn_f64_workspace_bytes": (
+        ctypes.c_size_t, [ctypes.c_int64, ctypes.c_int64, ctypes.c_int64]
+    ),
+    "tm_sinkhorn_f64": (
+        ctypes.c_int,
+        [
+            _VP, _VP, _VP, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64,
+            ctypes.POINTER(ctypes.c_double), ctypes.c_int32, ctypes.c_double,
+            _VP, _VP, _VP, _VP, ctypes.c_size_t, _VP,
+        ],
+    ),
 }
 
 

@@ -82,38 +82,6 @@ def _validate(cost: torch.Tensor) -> None:
         raise RuntimeError(msg)
 
 
-def _unpack_packed_3d(
-    packed: torch.Tensor, m: int
-) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
-    """(matches, unmatched_rows, unmatched_cols, n_matched), as ``_solve.py:124-164``."""
-    b, n = packed.shape
-    device = packed.device
-    matched_mask = packed >= 0
-    n_matched = matched_mask.sum(dim=-1)
-    match_order = torch.argsort((~matched_mask).long(), dim=-1, stable=True)
-    row_idx = torch.arange(n, device=device).expand(b, n)
-    sorted_rows = torch.gather(row_idx, 1, match_order)
-    sorted_cols = torch.gather(packed, 1, match_order)
-    matches = torch.stack([sorted_rows, sorted_cols], dim=-1)
-    unmatched_order = torch.argsort(matched_mask.long(), dim=-1, stable=True)
-    unmatched_rows = torch.gather(row_idx, 1, unmatched_order)
-    col_mask = torch.zeros(b, m, dtype=torch.bool, device=device)
-    col_mask.scatter_(1, packed.clamp(min=0), matched_mask)
-    col_order = torch.argsort(col_mask.long(), dim=-1, stable=True)
-    col_range = torch.arange(m, device=device).expand(b, m)
-    unmatched_cols = torch.gather(col_range, 1, col_order)
-    return matches, unmatched_rows, unmatched_cols, n_matched
-
-
-def _unpack_packed(packed: torch.Tensor, m: int) -> tuple[torch.Tensor, ...]:
-    if packed.ndim == 1:
-        matches3, ur3, uc3, n_matched = _unpack_packed_3d(packed.unsqueeze(0), m)
-        k = int(n_matched.item())
-        n = packed.size(0)
-        return matches3[0, :k], ur3[0, : n - k], uc3[0, : m - k]
-    return _unpack_packed_3d(packed, m)
-
-
 def _dispatch_jonker(cost: torch.Tensor, *, unpack: bool):
     squeeze = cost.ndim == 2
     batch = cost.unsqueeze(0) if squeeze else cost
@@ -124,14 +92,19 @@ def _dispatch_jonker(cost: torch.Tensor, *, unpack: bool):
             f"max(N, M) <= {jv_max_k()}, got shape {tuple(cost.shape)}"
         )
         raise ValueError(msg)
-    if unpack and not squeeze:
+    if unpack:
         # the device unpack, as the reference's native-unpack path
-        # (assignment/_solve.py:207-209) returns the CPU op's tuple
-        return torch.ops.assignment.jonker_dense_batch_unpacked(batch.contiguous())
+        # (assignment/_solve.py:207-209) returns the CPU op's tuple; a 2-D
+        # problem is a batch of one, trimmed of the -1 padding as the
+        # reference's 2-D unpack returns it (:124-164)
+        matches, ur, uc, nm = torch.ops.assignment.jonker_dense_batch_unpacked(
+            batch.contiguous())
+        if not squeeze:
+            return matches, ur, uc, nm
+        k = int(nm[0].item())
+        return matches[0, :k], ur[0, : n - k], uc[0, : m - k]
     packed = torch.ops.assignment.jonker_dense_batch(batch.contiguous())
-    if squeeze:
-        packed = packed[0]
-    return _unpack_packed(packed, m) if unpack else packed
+    return packed[0] if squeeze else packed
 
 
 def solve(

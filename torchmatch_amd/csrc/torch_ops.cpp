@@ -296,6 +296,40 @@ sinkhorn_iterate_hip(const at::Tensor &cost, const c10::optional<at::Tensor> &ke
     return {log_plan, log_u, log_v};
 }
 
+// torchmatch_amd::sinkhorn_f64 -- the whole float64 solve (the reference
+// iterates in the cost's dtype) on a cost already validated and mask-fused by
+// the caller.  Returns (log_plan, log_u, log_v); log_plan is empty when
+// write_plan is false.
+std::tuple<at::Tensor, at::Tensor, at::Tensor>
+sinkhorn_f64_hip(const at::Tensor &cost, const at::Tensor &a, const at::Tensor &b,
+                 at::ArrayRef<double> eps_sched, double rho, bool write_plan) {
+    TORCH_CHECK(cost.is_cuda() && a.is_cuda() && b.is_cuda(),
+                "sinkhorn: cost, a and b must be CUDA tensors");
+    TORCH_CHECK(cost.dim() == 3 && cost.scalar_type() == at::kDouble && cost.is_contiguous(),
+                "sinkhorn: cost must be a contiguous float64 (B, N, M) tensor");
+    TORCH_CHECK(a.scalar_type() == at::kDouble && b.scalar_type() == at::kDouble &&
+                    a.is_contiguous() && b.is_contiguous(),
+                "sinkhorn: a and b must be contiguous float64 tensors");
+    TORCH_CHECK(!eps_sched.empty(), "sinkhorn: empty epsilon schedule");
+    const int64_t B = cost.size(0), N = cost.size(1), M = cost.size(2);
+    TORCH_CHECK(a.dim() == 2 && a.size(0) == B && a.size(1) == N, "sinkhorn: a must be (B, N)");
+    TORCH_CHECK(b.dim() == 2 && b.size(0) == B && b.size(1) == M, "sinkhorn: b must be (B, M)");
+    const c10::DeviceGuard guard(cost.device());
+    auto log_u = at::empty({B, N}, cost.options());
+    auto log_v = at::empty({B, M}, cost.options());
+    at::Tensor log_plan = write_plan ? at::empty({B, N, M}, cost.options())
+                                     : at::empty({0}, cost.options());
+    const size_t ws_bytes = tm_sinkhorn_f64_workspace_bytes(B, N, M);
+    auto ws = at::empty({(int64_t)(ws_bytes > 0 ? ws_bytes : 1)}, cost.options().dtype(at::kByte));
+    const int rc = tm_sinkhorn_f64(
+        cost.data_ptr<double>(), a.data_ptr<double>(), b.data_ptr<double>(), B, N, M,
+        eps_sched.data(), (int32_t)eps_sched.size(), rho,
+        write_plan ? log_plan.data_ptr<double>() : nullptr, log_u.data_ptr<double>(),
+        log_v.data_ptr<double>(), ws.data_ptr(), ws_bytes, current_stream(cost));
+    check_rc(rc, "sinkhorn_f64");
+    return {log_plan, log_u, log_v};
+}
+
 } // namespace
 
 TORCH_LIBRARY_IMPL(assignment, CUDA, m) {
@@ -310,9 +344,12 @@ TORCH_LIBRARY(torchmatch_amd, m) {
           "bool read_stats) -> (Tensor, Tensor)");
     m.def("sinkhorn_iterate(Tensor cost, Tensor? keep, Tensor ws, float[] eps_sched, "
           "float rho, float k_eps, bool write_plan) -> (Tensor, Tensor, Tensor)");
+    m.def("sinkhorn_f64(Tensor cost, Tensor a, Tensor b, float[] eps_sched, float rho, "
+          "bool write_plan) -> (Tensor, Tensor, Tensor)");
 }
 
 TORCH_LIBRARY_IMPL(torchmatch_amd, CUDA, m) {
     m.impl("sinkhorn_prepare", &sinkhorn_prepare_hip);
     m.impl("sinkhorn_iterate", &sinkhorn_iterate_hip);
+    m.impl("sinkhorn_f64", &sinkhorn_f64_hip);
 }

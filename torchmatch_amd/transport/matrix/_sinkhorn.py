@@ -18,9 +18,10 @@ NaN / -inf, negative marginals, the largest finite cost, fetched with one
 host synchronisation) and ``torchmatch_amd::sinkhorn_iterate``.  A mask is
 fused in the kernels (the fused cost is never materialised).  This module
 raises the reference's errors from the returned flags, builds the epsilon
-schedule and shapes the results.  The kernels compute in float32 (float64
-input is validated by torch in float64, solved in float32 and the result
-cast back).  Device
+schedule and shapes the results.  Like the reference, the iteration runs in
+the cost's dtype: float32 costs take the kernels above; float64 costs are
+validated by torch and solved by the float64 kernels of
+``csrc/sinkhorn64.hip`` (``torchmatch_amd::sinkhorn_f64``).  Device
 tensors only: there is no host or torch-eager fallback.  Autograd through the
 kernel is not provided (the reference's ``solve`` differentiates through
 torch eager code instead).
@@ -124,6 +125,12 @@ def _device_solve(  # noqa: PLR0913
             plan = cost.new_empty(b_size, rows, cols) if write_plan else None
             return schedule, plan, cost.new_empty(b_size, rows), cost.new_empty(b_size, cols)
         _require_device(cost, a, b, who)
+        if cost.dtype == torch.float64:
+            # the reference iterates in the cost's dtype: float64 kernels
+            log_plan, log_u, log_v = torch.ops.torchmatch_amd.sinkhorn_f64(
+                cost.contiguous(), a.to(torch.float64).contiguous(),
+                b.to(torch.float64).contiguous(), schedule, float(rho), write_plan)
+            return schedule, (log_plan if write_plan else None), log_u, log_v
     c32 = cost.to(torch.float32).contiguous()
     a32 = a.to(torch.float32).contiguous()
     b32 = b.to(torch.float32).contiguous()
