@@ -104,13 +104,13 @@ int tm_jv_dense_batch_f32(const float *costs, int64_t B, int32_t N, int32_t M, i
  * allocation.  No counterpart in the reference: it is for callers that cannot
  * allocate (code under graph capture, tight serving loops, harnesses that
  * forbid hipMalloc).  The workspace is a fixed device array inside the
- * library, tm_jv_noalloc_scratch_bytes() bytes per GPU (8 KiB), held from the
+ * library, tm_jv_noalloc_scratch_bytes() bytes per GPU (35,072), held from the
  * library's load until the process ends; its address is looked up once per
  * device on the first call for that device.  Calls that overlap on one GPU
  * share the array and race: order them (one stream, or events).  Arguments,
  * status words, results and error codes as tm_jv_dense_batch_f32;
  * TM_ERR_WORKSPACE if a shape would need more than the array holds (none
- * does: the workspace size does not depend on the shape). */
+ * does: tm_jv_workspace_bytes never exceeds it). */
 int tm_jv_dense_batch_f32_noalloc(const float *costs, int64_t B, int32_t N, int32_t M,
                                   int64_t *out, uint32_t *d_status, hipStream_t stream);
 

@@ -28,8 +28,14 @@ struct JvStats {
     float max_finite;
     float min_finite;
     uint32_t flags;
-    uint32_t pad;
+    uint32_t info;  // unused (0)
 };
+
+// The fused path also keeps one summary byte per problem: bits 0-4 the
+// TM_JV_FLAG_* of its tile, then the bits below.
+constexpr uint32_t kJvRecDeferred = 1u << 5;  // holds +inf: solved once the batch is folded
+constexpr uint32_t kJvRecReplayed = 1u << 6;  // left the certified path for the exact replay
+constexpr uint32_t kJvRecGuard = 1u << 7;     // a solve hit its iteration guard
 
 // K in (64, jv_large_max_k()]: one workgroup per problem, cost read from
 // global memory (jv_large.hip).

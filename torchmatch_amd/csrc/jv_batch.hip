@@ -134,7 +134,7 @@ jv_stats_kernel(const float *__restrict__ costs, int64_t n, JvStats *__restrict_
         partial[blockIdx.x].max_finite = mx;
         partial[blockIdx.x].min_finite = mn;
         partial[blockIdx.x].flags = f;
-        partial[blockIdx.x].pad = 0;
+        partial[blockIdx.x].info = 0;
     }
 }
 
@@ -351,7 +351,7 @@ __device__ __forceinline__ void swap_lanes(PosState &st, int a, int b) {
     }
 }
 
-struct WaveLds {
+struct alignas(16) WaveLds {
     float c[kTile * kTile];  // row-major tile, stride 64
     int32_t xmax[kTile];     // column-reduction claims
     int32_t claims[kTile];
@@ -508,15 +508,14 @@ __device__ __forceinline__ CacheFill cache_fill(float crow, float v, int y, bool
 // (last / first), (c) the dual update's operand order, and (d) the starting
 // minimum of the reduction transfer (LARGE / FLT_MAX, which only matters for
 // K = 1); everything else is shared.
-// Column reduction of ccrrt_dense (jonker_dense_flat.h:124-176; the compact
-// solver's jonker_compact_core.h:77-120 differs only in the transfer's
-// starting minimum).  (v, y) arrive as this lane's column minimum and its
-// first arg-min row; on return v holds the column duals after the reduction
-// transfer, y the column's row (-1: free), x the lane's row's column (-1:
-// free), lane k of fr the k-th free row (increasing) and n_free their count.
-template <bool COMPACT, typename Row>
-__device__ __forceinline__ void column_reduction(const int K, WaveLds &L, Row row, float &v,
-                                                 int &y, int &x, int &fr, int &n_free) {
+// Claim step of the column reduction (jonker_dense_flat.h:146-160): (v, y)
+// arrive as this lane's column minimum and its first arg-min row; the
+// highest column claiming a row keeps it.  On return y is the column's row
+// (-1: free), x the lane's row's column (-1: free), lane k of fr the k-th free
+// row (increasing), n_free their count; the result says whether the lane's
+// row was claimed by one column only (the rows the transfer visits).
+__device__ __forceinline__ bool column_claim(const int K, WaveLds &L, float &v, int &y, int &x,
+                                             int &fr, int &n_free) {
     const int lane = lane_id();
     const bool live = lane < K;
     if (live) {
@@ -537,18 +536,26 @@ __device__ __forceinline__ void column_reduction(const int K, WaveLds &L, Row ro
         v = finf();
         y = -1;
     }
+    // lane k holds free_rows[k]: each free row writes itself at its rank
+    const uint64_t m = ballot(live && x < 0);
+    n_free = __builtin_popcountll(m);
+    if ((m >> lane) & 1ull)
+        L.pbuf[__builtin_popcountll(m & ((1ull << lane) - 1ull))] = lane;
+    __syncthreads();
+    fr = lane < n_free ? L.pbuf[lane] : 0;
+    return unique_row;
+}
 
-    // free rows (in increasing row order) and reduction transfer
-    fr = 0;       // lane k holds free_rows[k]
-    n_free = 0;
-    uint64_t m = ballot(live && x < 0);
-    while (m) {
-        const int row = first_lane(m);
-        m &= m - 1;
-        if (lane == n_free)
-            fr = row;
-        ++n_free;
-    }
+// Column reduction of ccrrt_dense (jonker_dense_flat.h:124-176; the compact
+// solver's jonker_compact_core.h:77-120 differs only in the transfer's
+// starting minimum): the claim above, then the reduction transfer.  On
+// return v holds the column duals after the transfer.
+template <bool COMPACT, typename Row>
+__device__ __forceinline__ void column_reduction(const int K, WaveLds &L, Row row, float &v,
+                                                 int &y, int &x, int &fr, int &n_free) {
+    const int lane = lane_id();
+    const bool live = lane < K;
+    const bool unique_row = column_claim(K, L, v, y, x, fr, n_free);
     // reduction transfer, unique rows in increasing order: each one sees
     // the v lowered by the rows before it; mn starts at LARGE and keeps
     // the first (lowest column) minimum, as the sequential scan does
@@ -568,6 +575,50 @@ __device__ __forceinline__ void column_reduction(const int K, WaveLds &L, Row ro
         if (lane == own)
             v -= mn;
     }
+}
+
+// The same claim with the transfer done for every unique row at once, from
+// the column minima (the duals before any transfer): lane i scans row i of
+// the LDS tile, skewed by its own index so the lanes read different banks,
+// and the row's column takes v -= min over the other columns of c - v.
+// Every dual only falls, so each row's minimum taken from the earlier duals
+// is at most its minimum under the final ones and the duals stay feasible
+// (c - v >= the row's own reduced cost); the sequential transfer of the
+// reference is one feasible choice among these.  For the certified path,
+// whose answer does not depend on the starting duals.
+__device__ __forceinline__ void column_reduction_parallel(const int K, WaveLds &L, float &v,
+                                                          int &y, int &x, int &fr,
+                                                          int &n_free, float start_min) {
+    const int lane = lane_id();
+    const bool live = lane < K;
+    const bool unique_row = column_claim(K, L, v, y, x, fr, n_free);
+    const bool transfer = live && x >= 0 && unique_row;
+    // columns beyond K read as c - (-inf) = +inf and never win (their tile
+    // entries are 0)
+    L.vbuf[lane] = live ? v : -finf();
+    __syncthreads();
+    float mn = start_min;
+    if (transfer) {
+        const float4 *crow = reinterpret_cast<const float4 *>(L.c + lane * kTile);
+        const float4 *vb = reinterpret_cast<const float4 *>(L.vbuf);
+#pragma unroll
+        for (int t = 0; t < kTile / 4; ++t) {
+            const int q = (lane + t) & (kTile / 4 - 1);
+            const float4 a = crow[q], b = vb[q];
+            const int j = 4 * q;
+            const float r0 = a.x - b.x, r1 = a.y - b.y, r2 = a.z - b.z, r3 = a.w - b.w;
+            mn = (j != x && r0 < mn) ? r0 : mn;
+            mn = (j + 1 != x && r1 < mn) ? r1 : mn;
+            mn = (j + 2 != x && r2 < mn) ? r2 : mn;
+            mn = (j + 3 != x && r3 < mn) ? r3 : mn;
+        }
+    }
+    // column lane j takes the minimum of its row y_j
+    const uint64_t moved = ballot(transfer);
+    const int src = y < 0 ? lane : y;
+    const float mrow = __int_as_float(__builtin_amdgcn_ds_bpermute(src * 4, __float_as_int(mn)));
+    if (live && y >= 0 && ((moved >> y) & 1ull))
+        v -= mrow;
 }
 
 template <bool COMPACT>
@@ -976,7 +1027,7 @@ __device__ __forceinline__ bool certified_solve(const int K, WaveLds &L, const C
     const int lane = lane_id();
     const bool live = lane < K;
     int x, fr, n_free;
-    column_reduction<COMPACT>(K, L, [col](int i) { return col.get(i); }, v, y, x, fr, n_free);
+    column_reduction_parallel(K, L, v, y, x, fr, n_free, COMPACT ? kFltMax : kLarge);
 
     // One shortest path per free row.  Lane j holds column j: its distance d,
     // its order key (kKeyNone once scanned, and on dead lanes), its
@@ -1003,7 +1054,12 @@ __device__ __forceinline__ bool certified_solve(const int K, WaveLds &L, const C
         int jf = -1;
         float level = 0.f;
         // each step retires one lane for good (its key becomes kKeyNone), so
-        // the loop ends within K steps
+        // the loop ends within K steps.  The step loop is placed at a fixed
+        // offset from a 64-byte instruction-cache line (the padding runs once
+        // per search): its speed otherwise moves by several percent with the
+        // size of the code before it.  Four words past the line was the
+        // fastest of the offsets 0-14 measured on the C2 batches.
+        asm volatile(".p2align 6\n\ts_nop 0\n\ts_nop 0\n\ts_nop 0\n\ts_nop 0" ::: "memory");
         while (true) {
             const int kmin = wave_min_key_s(key);
             if (kmin == kKeyNone)
@@ -1049,23 +1105,25 @@ __device__ __forceinline__ bool certified_solve(const int K, WaveLds &L, const C
     // certificate: u of each column's row goes to the LDS, then row by row
     // every lane forms r_ij for its column (float64); lane i collects the
     // near-tight columns of row i, and lane c then takes those of its row y_c
-    if (live)
-        L.ubuf[y] = (double)L.c[y * kTile + lane] - (double)v;
+    // Rows >= K get u = -inf and lanes >= K v = -inf, so every entry outside
+    // the K x K tile reads r = +inf (never tight, never negative) and the
+    // loop needs no row or lane masks.
+    const double ninf = -__builtin_inf();
+    L.ubuf[live ? y : lane] = live ? (double)L.c[y * kTile + lane] - (double)v : ninf;
     __syncthreads();
-    const double vd = (double)v;
+    const double vd = live ? (double)v : ninf;
     const double td = (double)tau;
-    bool neg = false;
+    uint64_t neg = 0;
     uint32_t row_lo = 0, row_hi = 0;  // lane i: near-tight columns of row i
 #pragma unroll
     for (int i = 0; i < kTile; ++i) {
-        const bool row_live = i < K;
         const double r = ((double)col.get(i) - L.ubuf[i]) - vd;
-        neg |= row_live && live && r < 0.0;
-        const uint64_t tight = ballot(row_live && live && r <= td);
+        neg |= ballot(r < 0.0);
+        const uint64_t tight = ballot(r <= td);
         row_lo = writelane_i((int)(uint32_t)tight, i, row_lo);
         row_hi = writelane_i((int)(uint32_t)(tight >> 32), i, row_hi);
     }
-    if (ballot(neg))
+    if (neg)
         return false;
     // the row's own column is tight (r = 0): not an edge
     uint64_t row_adj = ((uint64_t)row_hi << 32) | row_lo;
@@ -1100,13 +1158,141 @@ __device__ __forceinline__ bool certified_solve(const int K, WaveLds &L, const C
 // so its mappings differ on ties.  wave_solve<true> above follows them on the
 // wave path; inputs outside its range take compact_serial (jv_compact.h).
 
+// Statistics of one 64 x 64 tile held as 16 float4 per lane, reduced over
+// the wave: the flags of jv_stats_kernel and the largest / smallest finite
+// value.  All-finite tiles (the usual case) take integer max / min folds of
+// the raw bits; a tile holding +-inf or NaN takes the per-value path.
+__device__ __forceinline__ void tile_stats_wide(const float4 (&q)[16], float &mx, float &mn,
+                                                uint32_t &flags) {
+    uint32_t amax_bits = 0;  // largest |x| as raw bits (>= 0x7f800000: inf or NaN)
+    int smin_bits = 0x7fffffff;  // smallest raw bits as a signed int (INT_MIN: -0.0)
+    float hi = -finf(), lo = finf();
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+        const float e[4] = {q[k].x, q[k].y, q[k].z, q[k].w};
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const uint32_t u = __float_as_uint(e[t]);
+            amax_bits = max(amax_bits, u & 0x7fffffffu);
+            smin_bits = min(smin_bits, (int)u);
+            hi = __builtin_elementwise_maximum(hi, e[t]);
+            lo = __builtin_elementwise_minimum(lo, e[t]);
+        }
+    }
+    const bool clean = !ballot(amax_bits >= 0x7f800000u);
+    if (clean) {
+        mx = wave_max(hi);
+        mn = wave_min(lo);
+        flags = kJvFlagAnyFinite | (ballot(smin_bits == (int)0x80000000) ? kJvFlagNegZero : 0u);
+        return;
+    }
+    float fmx = -finf(), fmn = finf();
+    uint32_t f = 0;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+        const float e[4] = {q[k].x, q[k].y, q[k].z, q[k].w};
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const float x = e[t];
+            if (isnan(x)) {
+                f |= kJvFlagNan;
+            } else if (isinf(x)) {
+                f |= (x < 0.f) ? kJvFlagNegInf : kJvFlagPosInf;
+            } else {
+                f |= kJvFlagAnyFinite;
+                if (__float_as_uint(x) == 0x80000000u)
+                    f |= kJvFlagNegZero;
+                fmx = fmaxf(fmx, x);
+                fmn = fminf(fmn, x);
+            }
+        }
+    }
+    mx = wave_max(fmx);
+    mn = wave_min(fmn);
+    flags = 0;
+#pragma unroll
+    for (int bit = 0; bit < 5; ++bit)
+        if (ballot((f >> bit) & 1u))
+            flags |= 1u << bit;
+}
+
+// Launch modes of jv_solve_kernel.
+//   kJvStandalone: after jv_stats_kernel; every workgroup folds its partials
+//     (the batch statistics), block 0 publishes the flags, every problem is
+//     solved here.
+//   kJvFusedSolve: no statistics pass.  Each workgroup takes its own tile's
+//     statistics and writes them to its record, and its summary byte (flags
+//     and kJvRec* bits).  A tile
+//     without +inf, NaN or -inf needs nothing batch-wide (the sentinel only
+//     replaces +inf, and the wave paths' range tests concern the tile's own
+//     values), so it is solved here; a tile with +inf is deferred.  Block 0
+//     clears the guard word.
+//   kJvFusedFinish: the launch after kJvFusedSolve.  Block 0 folds every
+//     record into the status words and the replay count and, for a batch
+//     holding NaN or -inf, writes -1 to every output.  Deferred problems fold
+//     the records (the batch statistics of the standalone mode) and are solved
+//     with the batch-wide sentinel; the other workgroups return at once.
+enum JvMode { kJvStandalone = 0, kJvFusedSolve = 1, kJvFusedFinish = 2 };
+
+// Block 0 of kJvFusedFinish: status words, replay count, -1 fill on error,
+// from the summary bytes (B of them, read as 32-bit words, eight per lane in
+// flight).
+__device__ __forceinline__ void finish_records(const uint8_t *__restrict__ summary, int64_t B,
+                                               int N, int64_t *__restrict__ out,
+                                               uint32_t *__restrict__ status,
+                                               uint32_t *__restrict__ replays) {
+    const int lane = lane_id();
+    const uint32_t *words = reinterpret_cast<const uint32_t *>(summary);
+    const int64_t n_words = (B + 3) / 4;
+    uint32_t f = 0, nrep = 0;
+    for (int64_t w0 = lane; w0 < n_words; w0 += 64 * 8) {
+        uint32_t w[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int64_t k = w0 + 64 * u;
+            w[u] = k < n_words ? words[k] : 0u;
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int64_t k = w0 + 64 * u;
+            const int64_t valid = B - 4 * k;  // bytes of this word that belong to problems
+            const uint32_t mask = valid >= 4 ? 0xffffffffu
+                                  : valid <= 0 ? 0u : (1u << (8 * valid)) - 1u;
+            const uint32_t x = w[u] & mask;
+            f |= x;
+            nrep += (uint32_t)__builtin_popcount(x & 0x40404040u);
+        }
+    }
+    f |= f >> 16;
+    f |= f >> 8;
+    uint32_t bits = 0;
+#pragma unroll
+    for (int bit = 0; bit < 8; ++bit)
+        if (ballot((f >> bit) & 1u))
+            bits |= 1u << bit;
+    nrep = (uint32_t)wave_sum_all((float)nrep);  // exact: at most 2^24 problems
+    const uint32_t flags = bits & 0x1fu;
+    if (lane == 0) {
+        status[0] = flags;
+        *replays = nrep;
+        if (bits & kJvRecGuard)
+            raise_guard(status);
+    }
+    if (flags & (kJvFlagNan | kJvFlagNegInf)) {
+        for (int64_t k = lane; k < B * (int64_t)N; k += 64)
+            out[k] = -1;
+    }
+}
+
 // One problem per 64-lane workgroup; COMPACT selects the solver of
 // assignment::jonker_compact_batch instead of jonker_dense_batch (same
-// statistics, sentinel, padding and output rules, ops.cpp:176-289).
-template <bool COMPACT>
+// statistics, sentinel, padding and output rules, ops.cpp:176-289).  `stats`
+// holds the statistics partials (kJvStandalone, n_stats of them) or the
+// per-problem records (fused modes, B of them).
+template <bool COMPACT, int MODE>
 __global__ void __launch_bounds__(64)
 jv_solve_kernel(const float *__restrict__ costs, int64_t B, int N, int M,
-                const JvStats *__restrict__ partial, int n_partial,
+                JvStats *__restrict__ stats, int n_stats, uint8_t *__restrict__ summary,
                 int64_t *__restrict__ out, uint32_t *__restrict__ status, int certify,
                 uint32_t *__restrict__ replays) {
     __shared__ WaveLds L;
@@ -1114,6 +1300,18 @@ jv_solve_kernel(const float *__restrict__ costs, int64_t B, int N, int M,
     const int lane = lane_id();
     const int K = N > M ? N : M;
     const int64_t b = blockIdx.x;
+    int64_t *ob = out + b * N;
+
+    if constexpr (MODE == kJvFusedFinish) {
+        if (b == 0)
+            finish_records(summary, B, N, out, status, replays);
+        if ((summary[b] & kJvRecDeferred) == 0)
+            return;
+    }
+    if constexpr (MODE == kJvFusedSolve) {
+        if (b == 0 && lane == 0)
+            status[1] = 0;  // raised by kJvFusedFinish only
+    }
 
     float mx, mn;
     uint32_t flags;
@@ -1128,16 +1326,76 @@ jv_solve_kernel(const float *__restrict__ costs, int64_t B, int N, int M,
         for (int k = 0; k < 16; ++k)
             q[k] = src4[k * 64 + lane];
     }
-    fold_stats(partial, n_partial, mx, mn, flags);
-    if (b == 0 && lane == 0)
-        status[0] = flags;
-    const bool bad = (flags & (kJvFlagNan | kJvFlagNegInf)) != 0;
-    int64_t *ob = out + b * N;
-    if (bad) {
-        for (int i = lane; i < N; i += 64)
-            ob[i] = -1;
-        return;
+    uint32_t info = 0;  // kJvFusedSolve: this problem's record bits
+    if constexpr (MODE == kJvFusedSolve) {
+        if (wide) {
+            tile_stats_wide(q, mx, mn, flags);
+        } else {
+            float fmx = -finf(), fmn = finf();
+            uint32_t f = 0;
+            for (int i = 0; i < N; ++i) {
+                if (lane < M) {
+                    const float x = src[(int64_t)i * M + lane];
+                    if (isnan(x)) {
+                        f |= kJvFlagNan;
+                    } else if (isinf(x)) {
+                        f |= (x < 0.f) ? kJvFlagNegInf : kJvFlagPosInf;
+                    } else {
+                        f |= kJvFlagAnyFinite;
+                        if (__float_as_uint(x) == 0x80000000u)
+                            f |= kJvFlagNegZero;
+                        fmx = fmaxf(fmx, x);
+                        fmn = fminf(fmn, x);
+                    }
+                }
+            }
+            mx = wave_max(fmx);
+            mn = wave_min(fmn);
+            flags = 0;
+#pragma unroll
+            for (int bit = 0; bit < 5; ++bit)
+                if (ballot((f >> bit) & 1u))
+                    flags |= 1u << bit;
+        }
+        const bool bad = (flags & (kJvFlagNan | kJvFlagNegInf)) != 0;
+        if (bad || (flags & kJvFlagPosInf)) {
+            if (bad) {
+                for (int i = lane; i < N; i += 64)
+                    ob[i] = -1;
+            }
+            if (lane == 0) {
+                stats[b] = JvStats{mx, mn, flags, 0u};
+                summary[b] = (uint8_t)(flags | (bad ? 0u : kJvRecDeferred));
+            }
+            return;
+        }
+    } else {
+        fold_stats(stats, n_stats, mx, mn, flags);
+        if constexpr (MODE == kJvStandalone) {
+            if (b == 0 && lane == 0)
+                status[0] = flags;
+        }
+        if (flags & (kJvFlagNan | kJvFlagNegInf)) {
+            for (int i = lane; i < N; i += 64)
+                ob[i] = -1;
+            return;
+        }
     }
+    // the record of a problem solved in kJvFusedSolve, written last
+    auto finish = [&]() {
+        if constexpr (MODE == kJvFusedSolve) {
+            if (lane == 0) {
+                stats[b] = JvStats{mx, mn, flags, 0u};
+                summary[b] = (uint8_t)(flags | info);
+            }
+        }
+    };
+    auto note_guard = [&]() {
+        if constexpr (MODE == kJvFusedSolve)
+            info |= kJvRecGuard;
+        else if (lane == 0)
+            raise_guard(status);
+    };
     const bool any_finite = (flags & kJvFlagAnyFinite) != 0;
     const float sentinel = any_finite ? (mx + 1.0f) * (float)(K + 1) : 1.0f;
     const bool has_inf = (flags & kJvFlagPosInf) != 0;
@@ -1206,26 +1464,32 @@ jv_solve_kernel(const float *__restrict__ costs, int64_t B, int N, int M,
         if (certified_solve<COMPACT>(K, L, col, vmin, ymin, amax * 0x1p-20f, x)) {
             if (lane < N)
                 ob[lane] = (int64_t)x;
+            finish();
             return;
         }
-        if (lane == 0)
-            atomicAdd(replays, 1u);
+        if constexpr (MODE == kJvFusedSolve) {
+            info |= kJvRecReplayed;
+        } else {
+            if (lane == 0)
+                atomicAdd(replays, 1u);
+        }
         x = -1;
     }
     if constexpr (COMPACT) {
         if (fast && compact_wave_range(any_finite, mx, mn, has_inf, sentinel)) {
             const bool chain = K >= 2 && (flags & kJvFlagNegZero) == 0;
             if (!wave_solve<true>(K, L, vmin, ymin, chain, x)) {
-                if (lane == 0)
-                    raise_guard(status);
+                note_guard();
                 x = -1;
             }
         } else {
             const float *tile = L.c;
             auto cost = [tile](int i, int j) { return tile[i * kTile + j]; };
-            if (lane == 0 && !compact_serial((uint32_t)K, cost, S.x, S.y, S.fr, S.pred, S.cols,
-                                             S.v, S.d))
-                raise_guard(status);
+            bool ok = true;
+            if (lane == 0)
+                ok = compact_serial((uint32_t)K, cost, S.x, S.y, S.fr, S.pred, S.cols, S.v, S.d);
+            if (!__builtin_amdgcn_readfirstlane((int)ok))
+                note_guard();
             __syncthreads();
             if (lane < K)
                 x = S.x[lane];
@@ -1235,8 +1499,7 @@ jv_solve_kernel(const float *__restrict__ costs, int64_t B, int N, int M,
         // read back from its key, which maps -0.0 to +0.0)
         const bool chain = K >= 2 && (flags & kJvFlagNegZero) == 0;
         if (!wave_solve<false>(K, L, vmin, ymin, chain, x)) {
-            if (lane == 0)
-                raise_guard(status);
+            note_guard();
             x = -1;
         }
     } else {
@@ -1248,6 +1511,7 @@ jv_solve_kernel(const float *__restrict__ costs, int64_t B, int N, int M,
     }
     if (lane < N)
         ob[lane] = (x >= 0 && x < M) ? (int64_t)x : (int64_t)-1;
+    finish();
 }
 
 } // namespace
@@ -1258,15 +1522,34 @@ jv_solve_kernel(const float *__restrict__ costs, int64_t B, int N, int M,
 // ---------------------------------------------------------------------------
 using namespace tmamd;
 
-// Workspace: the statistics partials, then (at kReplayOffset) the count of
-// problems the certified path handed to the exact replay.
-constexpr size_t kReplayOffset = sizeof(JvStats) * (size_t)kJvMaxStatBlocks;
+// Workspace: the count of problems the certified path handed to the exact
+// replay at offset 0, then from kStatsOffset the statistics records: the
+// per-block partials of jv_stats_kernel (at most kJvMaxStatBlocks), or, on
+// the fused K <= 64 path (B <= kFusedMaxB), one record per problem.
+constexpr size_t kStatsOffset = 256;
+// Fused path: the summary bytes follow the records.
+size_t summary_offset(int64_t records) { return kStatsOffset + sizeof(JvStats) * (size_t)records; }
+// Largest batch the fused path takes: every deferred (+inf) problem folds all
+// B records, so its cost grows with B * (number of deferred problems).
+constexpr int64_t kFusedMaxB = 2048;
+
+namespace {
+bool fused_path(int64_t B, int32_t N, int32_t M) {
+    const int K = N > M ? N : M;
+    return K <= kTile && B <= kFusedMaxB;
+}
+} // namespace
+
+namespace {
+int64_t record_count(int64_t B, int32_t N, int32_t M) {
+    return (fused_path(B, N, M) && B > kJvMaxStatBlocks) ? B : kJvMaxStatBlocks;
+}
+} // namespace
 
 extern "C" size_t tm_jv_workspace_bytes(int64_t B, int32_t N, int32_t M) {
-    (void)B;
-    (void)N;
-    (void)M;
-    return kReplayOffset + 256;
+    const int64_t records = record_count(B, N, M);
+    const size_t summary = fused_path(B, N, M) ? (size_t)((B + 15) / 16 * 16) : 0;
+    return summary_offset(records) + summary;
 }
 
 namespace {
@@ -1277,16 +1560,68 @@ int certify_enabled() {
     return (env != nullptr && strcmp(env, "0") == 0) ? 0 : 1;
 }
 
-uint32_t *replay_counter(void *workspace) {
-    return reinterpret_cast<uint32_t *>(static_cast<char *>(workspace) + kReplayOffset);
+uint32_t *replay_counter(void *workspace) { return static_cast<uint32_t *>(workspace); }
+
+JvStats *stats_records(void *workspace) {
+    return reinterpret_cast<JvStats *>(static_cast<char *>(workspace) + kStatsOffset);
+}
+
+// The launches of tm_jv_dense_batch_f32 / tm_jv_compact_batch_f32.  K <= 64
+// with B <= kFusedMaxB: the fused solve launch, then the finishing launch (no
+// pass over the input besides the solve's own read).  Otherwise the
+// statistics pass, then the solve (K <= 64) or the large-K kernel.
+template <bool COMPACT>
+int jv_launch(const float *costs, int64_t B, int32_t N, int32_t M, int64_t *out,
+              void *workspace, size_t workspace_bytes, uint32_t *d_status, hipStream_t stream) {
+    if (B < 0 || N < 0 || M < 0)
+        return kTmErrInvalidArgument;
+    if (B == 0 || N == 0 || M == 0)
+        return kTmOk;  // caller fills -1
+    const int K = N > M ? N : M;
+    if (K > (COMPACT ? jv_compact_max_k() : jv_large_max_k()))
+        return kTmErrUnsupportedShape;
+    if (workspace_bytes < tm_jv_workspace_bytes(B, N, M) || workspace == nullptr ||
+        d_status == nullptr)
+        return kTmErrWorkspace;
+    if (B > (int64_t)0x7fffffff)
+        return kTmErrUnsupportedShape;
+    JvStats *stats = stats_records(workspace);
+    uint32_t *replays = replay_counter(workspace);
+    const int certify = certify_enabled();
+    if (fused_path(B, N, M)) {
+        uint8_t *summary = static_cast<uint8_t *>(workspace) + summary_offset(record_count(B, N, M));
+        hipLaunchKernelGGL((jv_solve_kernel<COMPACT, kJvFusedSolve>), dim3((unsigned)B), dim3(64),
+                           0, stream, costs, B, N, M, stats, (int)B, summary, out, d_status,
+                           certify, replays);
+        hipLaunchKernelGGL((jv_solve_kernel<COMPACT, kJvFusedFinish>), dim3((unsigned)B),
+                           dim3(64), 0, stream, costs, B, N, M, stats, (int)B, summary, out,
+                           d_status, certify, replays);
+        return hipGetLastError() == hipSuccess ? kTmOk : kTmErrLaunch;
+    }
+    const int64_t n = B * (int64_t)N * M;
+    int64_t blocks = (n / 4 + kStatsBlock - 1) / kStatsBlock;
+    blocks = blocks < 1 ? 1 : (blocks > kJvMaxStatBlocks ? kJvMaxStatBlocks : blocks);
+    hipLaunchKernelGGL(jv_stats_kernel, dim3((unsigned)blocks), dim3(kStatsBlock), 0, stream,
+                       costs, n, stats, d_status, replays);
+    if (hipGetLastError() != hipSuccess)
+        return kTmErrLaunch;
+    if (K > kTile)
+        return COMPACT ? launch_jv_compact_large(costs, B, N, M, stats, (int)blocks, out,
+                                                 d_status, stream)
+                       : launch_jv_large(costs, B, N, M, stats, (int)blocks, out, d_status,
+                                         stream);
+    hipLaunchKernelGGL((jv_solve_kernel<COMPACT, kJvStandalone>), dim3((unsigned)B), dim3(64), 0,
+                       stream, costs, B, N, M, stats, (int)blocks, nullptr, out, d_status,
+                       certify, replays);
+    return hipGetLastError() == hipSuccess ? kTmOk : kTmErrLaunch;
 }
 } // namespace
 
 extern "C" int tm_jv_read_replays(const void *workspace, uint32_t *count, hipStream_t stream) {
     if (workspace == nullptr || count == nullptr)
         return TM_ERR_INVALID_ARGUMENT;
-    if (hipMemcpyAsync(count, static_cast<const char *>(workspace) + kReplayOffset,
-                       sizeof(uint32_t), hipMemcpyDeviceToHost, stream) != hipSuccess)
+    if (hipMemcpyAsync(count, workspace, sizeof(uint32_t), hipMemcpyDeviceToHost, stream) !=
+        hipSuccess)
         return TM_ERR_HIP;
     return hipStreamSynchronize(stream) == hipSuccess ? TM_OK : TM_ERR_HIP;
 }
@@ -1294,68 +1629,13 @@ extern "C" int tm_jv_read_replays(const void *workspace, uint32_t *count, hipStr
 extern "C" int tm_jv_dense_batch_f32(const float *costs, int64_t B, int32_t N, int32_t M,
                                      int64_t *out, void *workspace, size_t workspace_bytes,
                                      uint32_t *d_status, hipStream_t stream) {
-    if (B < 0 || N < 0 || M < 0)
-        return kTmErrInvalidArgument;
-    if (B == 0 || N == 0 || M == 0)
-        return kTmOk;  // caller fills -1
-    const int K = N > M ? N : M;
-    if (K > jv_large_max_k())
-        return kTmErrUnsupportedShape;
-    if (workspace_bytes < tm_jv_workspace_bytes(B, N, M) || workspace == nullptr ||
-        d_status == nullptr)
-        return kTmErrWorkspace;
-    if (B > (int64_t)0x7fffffff)
-        return kTmErrUnsupportedShape;
-    const int64_t n = B * (int64_t)N * M;
-    int64_t blocks = (n / 4 + kStatsBlock - 1) / kStatsBlock;
-    blocks = blocks < 1 ? 1 : (blocks > kJvMaxStatBlocks ? kJvMaxStatBlocks : blocks);
-    JvStats *partial = static_cast<JvStats *>(workspace);
-    hipLaunchKernelGGL(jv_stats_kernel, dim3((unsigned)blocks), dim3(kStatsBlock), 0, stream,
-                       costs, n, partial, d_status, replay_counter(workspace));
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess)
-        return kTmErrLaunch;
-    if (K > kTile)
-        return launch_jv_large(costs, B, N, M, partial, (int)blocks, out, d_status, stream);
-    hipLaunchKernelGGL(jv_solve_kernel<false>, dim3((unsigned)B), dim3(64), 0, stream, costs, B,
-                       N, M, partial, (int)blocks, out, d_status, certify_enabled(),
-                       replay_counter(workspace));
-    e = hipGetLastError();
-    return e == hipSuccess ? kTmOk : kTmErrLaunch;
+    return jv_launch<false>(costs, B, N, M, out, workspace, workspace_bytes, d_status, stream);
 }
 
 extern "C" int tm_jv_compact_batch_f32(const float *costs, int64_t B, int32_t N, int32_t M,
                                        int64_t *out, void *workspace, size_t workspace_bytes,
                                        uint32_t *d_status, hipStream_t stream) {
-    if (B < 0 || N < 0 || M < 0)
-        return kTmErrInvalidArgument;
-    if (B == 0 || N == 0 || M == 0)
-        return kTmOk;  // caller fills -1
-    const int K = N > M ? N : M;
-    if (K > jv_compact_max_k())
-        return kTmErrUnsupportedShape;
-    if (workspace_bytes < tm_jv_workspace_bytes(B, N, M) || workspace == nullptr ||
-        d_status == nullptr)
-        return kTmErrWorkspace;
-    if (B > (int64_t)0x7fffffff)
-        return kTmErrUnsupportedShape;
-    const int64_t n = B * (int64_t)N * M;
-    int64_t blocks = (n / 4 + kStatsBlock - 1) / kStatsBlock;
-    blocks = blocks < 1 ? 1 : (blocks > kJvMaxStatBlocks ? kJvMaxStatBlocks : blocks);
-    JvStats *partial = static_cast<JvStats *>(workspace);
-    hipLaunchKernelGGL(jv_stats_kernel, dim3((unsigned)blocks), dim3(kStatsBlock), 0, stream,
-                       costs, n, partial, d_status, replay_counter(workspace));
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess)
-        return kTmErrLaunch;
-    if (K > kTile)
-        return launch_jv_compact_large(costs, B, N, M, partial, (int)blocks, out, d_status,
-                                       stream);
-    hipLaunchKernelGGL(jv_solve_kernel<true>, dim3((unsigned)B), dim3(64), 0, stream, costs, B,
-                       N, M, partial, (int)blocks, out, d_status, certify_enabled(),
-                       replay_counter(workspace));
-    e = hipGetLastError();
-    return e == hipSuccess ? kTmOk : kTmErrLaunch;
+    return jv_launch<true>(costs, B, N, M, out, workspace, workspace_bytes, d_status, stream);
 }
 
 // ---------------------------------------------------------------------------
@@ -1364,12 +1644,16 @@ extern "C" int tm_jv_compact_batch_f32(const float *costs, int64_t B, int32_t N,
 // serving loops).  Its workspace is `scratch`, a file-scope device array of a
 // fixed size (each GPU the library runs on keeps its own copy until the
 // process ends); every call on one GPU shares it, so calls that overlap on
-// one GPU race.  Nothing in it needs clearing between calls: the statistics
-// pass writes every partial record and zeroes the guard word and the replay
-// counter before the solve reads them.
+// one GPU race.  Nothing in it needs clearing between calls: every record a
+// launch reads is written earlier in the same call (each problem's record by
+// its fused solve workgroup, or every partial by the statistics pass), and
+// the guard word and the replay counter are set before they are raised or read.
 // ---------------------------------------------------------------------------
 namespace {
-constexpr size_t kScratchBytes = 8192;  // >= tm_jv_workspace_bytes(B, N, M) for every shape
+// >= tm_jv_workspace_bytes(B, N, M) for every shape: kFusedMaxB records and
+// summary bytes
+constexpr size_t kScratchBytes =
+    kStatsOffset + (sizeof(JvStats) + 1) * (size_t)kFusedMaxB;
 static __device__ __align__(256) unsigned char scratch[kScratchBytes];
 
 constexpr int kScratchMaxDevices = 64;
