@@ -70,7 +70,14 @@ enum {
     TM_JV_FLAG_NEG_INF = 2u,
     TM_JV_FLAG_POS_INF = 4u,
     TM_JV_FLAG_ANY_FINITE = 8u,
-    TM_JV_FLAG_NEG_ZERO = 16u   /* input holds -0.0 (informational) */
+    TM_JV_FLAG_NEG_ZERO = 16u,  /* input holds -0.0 (informational) */
+    /* Set in word [0] by the last write of a K <= 64, B <= 2048 launch whose
+     * problems are all solved before its finishing workgroup ends (none holds
+     * +inf): every output and both status words are then final, so a caller
+     * that cleared word [0] before the launch may poll host-mapped status
+     * words for this bit instead of synchronising the stream.  Launches that
+     * do not set it are waited for by synchronising the stream. */
+    TM_JV_FLAG_DONE = 0x80000000u
 };
 
 /* ---- batched Jonker-Volgenant (assignment::jonker_dense_batch) -------- */

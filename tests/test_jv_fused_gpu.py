@@ -11,7 +11,9 @@ status words.  These tests hold that split to the oracle:
 * a workspace full of garbage (the contract says "any contents");
 * NaN / -inf anywhere: the error code, and -1 in every output;
 * the status flags of the whole batch, and the guard word cleared between
-  calls.
+  calls;
+* TM_JV_FLAG_DONE: set by batches whose problems are all solved in the first
+  launch, never by batches that defer a problem or take the statistics pass.
 """
 
 from __future__ import annotations
@@ -31,6 +33,7 @@ pytestmark = pytest.mark.gpu
 FLAG_POS_INF = 4
 FLAG_ANY_FINITE = 8
 FLAG_NEG_ZERO = 16
+FLAG_DONE = 0x80000000
 
 
 def _abi(cost: torch.Tensor, device, compact: bool = False, garbage: bool = True):
@@ -71,6 +74,7 @@ def test_mixed_inf_batches_match_oracle(B, N, M, compact, device):
     print(f"mixed {(B, N, M)} compact={compact}: {len(bad)} problems differ", flush=True)
     assert len(bad) == 0
     assert st[0] & FLAG_POS_INF and st[0] & FLAG_ANY_FINITE and st[1] == 0
+    assert not st[0] & FLAG_DONE  # +inf problems were solved by the finishing launch
 
 
 @pytest.mark.parametrize("B", [64, 2049])
@@ -90,11 +94,15 @@ def test_status_flags_and_guard_cleared(device):
     cost[5, 0, 0] = -0.0
     rc, code, st, got = _abi(cost, device)
     assert rc == _native.TM_OK and code == _native.TM_OK
-    assert st[0] == FLAG_ANY_FINITE | FLAG_NEG_ZERO and st[1] == 0
+    assert st[0] == FLAG_DONE | FLAG_ANY_FINITE | FLAG_NEG_ZERO and st[1] == 0
     assert (got == jv.jv_dense_batch(cost.numpy())).all()
     # a clean call after a batch with +inf reports no +inf
     _abi(_mixed(64, 64, 64, seed=4), device)
     rc, code, st, _ = _abi(torch.rand(64, 64, 64), device)
+    assert rc == _native.TM_OK and code == _native.TM_OK
+    assert st[0] == FLAG_DONE | FLAG_ANY_FINITE and st[1] == 0
+    # the statistics-pass path (B > 2048) never sets the done bit
+    rc, code, st, _ = _abi(torch.rand(2049, 8, 8), device)
     assert rc == _native.TM_OK and code == _native.TM_OK
     assert st[0] == FLAG_ANY_FINITE and st[1] == 0
 

@@ -19,6 +19,7 @@ constexpr uint32_t kJvFlagNegInf = TM_JV_FLAG_NEG_INF;
 constexpr uint32_t kJvFlagPosInf = TM_JV_FLAG_POS_INF;
 constexpr uint32_t kJvFlagAnyFinite = TM_JV_FLAG_ANY_FINITE;
 constexpr uint32_t kJvFlagNegZero = TM_JV_FLAG_NEG_ZERO;
+constexpr uint32_t kJvFlagDone = TM_JV_FLAG_DONE;
 
 // Upper bound on the blocks of the statistics pass (and so on the partial
 // records every solve workgroup folds).

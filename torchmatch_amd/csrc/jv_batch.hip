@@ -1273,7 +1273,6 @@ __device__ __forceinline__ void finish_records(const uint8_t *__restrict__ summa
     nrep = (uint32_t)wave_sum_all((float)nrep);  // exact: at most 2^24 problems
     const uint32_t flags = bits & 0x1fu;
     if (lane == 0) {
-        status[0] = flags;
         *replays = nrep;
         if (bits & kJvRecGuard)
             raise_guard(status);
@@ -1282,6 +1281,11 @@ __device__ __forceinline__ void finish_records(const uint8_t *__restrict__ summa
         for (int64_t k = lane; k < B * (int64_t)N; k += 64)
             out[k] = -1;
     }
+    // the flags last, with the done bit when no deferred problem is left to
+    // solve in this launch: the release orders every write above before it
+    if (lane == 0)
+        __hip_atomic_store(&status[0], flags | ((bits & kJvRecDeferred) ? 0u : kJvFlagDone),
+                           __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
 // One problem per 64-lane workgroup; COMPACT selects the solver of

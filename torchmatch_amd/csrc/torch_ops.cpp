@@ -134,15 +134,31 @@ at::Tensor jv_batch_hip(const at::Tensor &costs, JvSolver solver, int64_t max_k,
     // so the readback is the stream synchronisation alone (no copy command);
     // device memory and a copy when no pinned block can be mapped.
     if (const StatusSlot *slot = status_slot(costs.get_device())) {
+        volatile uint32_t *words = slot->host;
+        words[0] = 0;
         int rc = solver(cf.data_ptr<float>(), B, (int32_t)N, (int32_t)M,
                         out.data_ptr<int64_t>(), ws.data_ptr(), ws_bytes, slot->dev, stream);
-        // synchronise before any error leaves: the next call on this thread
-        // reuses the words
-        const hipError_t se = hipStreamSynchronize(stream);
+        // Wait for TM_JV_FLAG_DONE (written last by launches that set it) or,
+        // for launches that do not, for the stream; synchronise before any
+        // error leaves, since the next call on this thread reuses the words.
+        hipError_t se = hipSuccess;
+        if (rc == TM_OK) {
+            for (uint32_t spin = 1;; ++spin) {
+                if (words[0] & TM_JV_FLAG_DONE)
+                    break;
+                if ((spin & 4095u) == 0 && hipStreamQuery(stream) != hipErrorNotReady) {
+                    se = hipStreamSynchronize(stream);
+                    break;
+                }
+            }
+        } else {
+            se = hipStreamSynchronize(stream);
+        }
         check_rc(rc, op_name);
         TORCH_CHECK(se == hipSuccess, op_name, ": stream synchronisation failed: ",
                     hipGetErrorString(se));
-        rc = tm_jv_status_code(slot->host);
+        uint32_t seen[2] = {words[0], words[1]};
+        rc = tm_jv_status_code(seen);
         check_rc(rc, op_name);
         return out;
     }
