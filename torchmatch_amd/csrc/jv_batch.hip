@@ -1216,6 +1216,30 @@ __device__ __forceinline__ void tile_stats_wide(const float4 (&q)[16], float &mx
             flags |= 1u << bit;
 }
 
+// Lane j's column of the LDS tile into registers, with its minimum and first
+// arg-min row (strict '<' from LARGE, jonker_dense_flat.h:136-144) and the
+// largest |value|.  FULL (K = 64) has no row tests: a run-time bound on the
+// unrolled rows costs a scalar mask and a branch per row.
+template <bool FULL>
+__device__ __forceinline__ void load_columns(const int K, const WaveLds &L, Col64 &col,
+                                             float &vmin, int &ymin, float &amax) {
+    const int lane = lane_id();
+    vmin = kLarge;
+    ymin = 0;
+    amax = 0.f;
+#pragma unroll
+    for (int i = 0; i < kTile; ++i) {
+        const bool row = FULL || i < K;
+        const float val = row ? L.c[i * kTile + lane] : 0.f;
+        col.set(i, val);
+        amax = fmaxf(amax, fabsf(val));
+        if (row && val < vmin) {
+            vmin = val;
+            ymin = i;
+        }
+    }
+}
+
 // Launch modes of jv_solve_kernel.
 //   kJvStandalone: after jv_stats_kernel; every workgroup folds its partials
 //     (the batch statistics), block 0 publishes the flags, every problem is
@@ -1444,20 +1468,13 @@ jv_solve_kernel(const float *__restrict__ costs, int64_t B, int N, int M,
     }
     __syncthreads();
     // (lane j also keeps its column in registers for the certified path)
-    float vmin = kLarge;
-    int ymin = 0;
-    float amax = 0.f;
+    float vmin, amax;
+    int ymin;
     Col64 col;
-#pragma unroll
-    for (int i = 0; i < kTile; ++i) {
-        const float val = i < K ? L.c[i * kTile + lane] : 0.f;
-        col.set(i, val);
-        amax = fmaxf(amax, fabsf(val));
-        if (i < K && val < vmin) {
-            vmin = val;
-            ymin = i;
-        }
-    }
+    if (K == kTile)
+        load_columns<true>(K, L, col, vmin, ymin, amax);
+    else
+        load_columns<false>(K, L, col, vmin, ymin, amax);
 
     int x = -1;
     // certified shortest paths first (square, finite, S in [1e-30, 1e15]);
