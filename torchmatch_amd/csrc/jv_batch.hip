@@ -1065,16 +1065,16 @@ __device__ __forceinline__ bool certified_solve(const int K, WaveLds &L, const C
             if (kmin == kKeyNone)
                 break;
             const int js = first_lane(ballot(key == kmin));
-            level = readlane_f(d, js);
+            level = __int_as_float(kmin);  // an open column's key is its distance's bits
             const int is = readlane_i(y, js);
             if (is < 0) {
                 jf = js;  // unassigned column: the path ends
                 break;
             }
-            // relax through row `is` (scan_dense: h = c[i][jp] - v[jp] - level,
-            // r = c[i][j] - v[j] - h)
-            const float h = readlane_f(u, is) - level;
-            const float r = (col.get(is) - v) - h;
+            // relax through row `is`: r = c[i][j] - v[j] - (u_i - level), as
+            // scan_dense's c[i][j] - v[j] - h, associated so that each step
+            // of the sum takes one scalar
+            const float r = ((col.get(is) - v) - readlane_f(u, is)) + level;
             const bool upd = (key != kKeyNone) & (r < d);
             d = upd ? r : d;
             pred = upd ? is : pred;
