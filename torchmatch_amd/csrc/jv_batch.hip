@@ -1437,7 +1437,12 @@ jv_solve_kernel(const float *__restrict__ costs, int64_t B, int N, int M,
     // for its minimum and first arg-min row (strict '<' from LARGE,
     // jonker_dense_flat.h:136-144)
     bool inf_here = false;  // this problem holds +inf (the sentinel is in the tile)
-    if (wide) {
+    if (wide && MODE == kJvFusedSolve) {
+        // a tile solved in this mode holds no +inf: stored as loaded
+#pragma unroll
+        for (int k = 0; k < 16; ++k)
+            reinterpret_cast<float4 *>(L.c)[k * 64 + lane] = q[k];
+    } else if (wide) {
         auto fix = [&](float x) {
             const bool f = isfinite(x);
             inf_here |= !f;
