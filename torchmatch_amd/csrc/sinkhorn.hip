@@ -174,6 +174,9 @@ __host__ __device__ inline size_t align_up(size_t x, size_t a) { return (x + a -
 enum FusedVariant {
     kFzNone = 0, kFz1x4x4, kFz1x4x8, kFz2x1x8, kFz4x1x8, kFz8x1x8, kFz16x1x4, kFz1x4x1, kFz1x4x2
 };
+// K sizes above which the fused step streams K with non-temporal loads.
+constexpr size_t kNonTemporalBytes = (size_t)384 << 20;
+
 struct FusedShape {
     int W, RW, NV, blocks_per_cu;
 };
@@ -867,7 +870,11 @@ __device__ __forceinline__ Lse fold_partial(float m, float s) {
 // The row's flag, log marginal, current log_u and previous base-2 LSE (its
 // shift) are loaded with it: a load
 // issued later would make the wait for it a wait for every row in flight.
-template <int NV>
+// NT: non-temporal loads, for a K larger than the last-level (Infinity)
+// cache, which each step streams once and would only evict what the next
+// step reads (C5, 1 GiB: 187.9 against 193.7 us per step; C4's 256 MiB, which
+// the cache partly keeps between steps, is faster with ordinary loads).
+template <int NV, bool NT>
 __device__ __forceinline__ void fz_load(vf4 (&dst)[NV], float &mu, float &u, float &rs, int &skip,
                                         const vf4 *__restrict__ row4, const uint32_t (&qb)[NV],
                                         int64_t r, const float *__restrict__ log_mu,
@@ -875,9 +882,15 @@ __device__ __forceinline__ void fz_load(vf4 (&dst)[NV], float &mu, float &u, flo
                                         const float *__restrict__ lse2_row,
                                         const uint8_t *__restrict__ inf_row) {
     const char *base = reinterpret_cast<const char *>(row4);
+    if constexpr (NT) {
 #pragma unroll
-    for (int k = 0; k < NV; ++k)
-        dst[k] = *reinterpret_cast<const vf4 *>(base + qb[k]);
+        for (int k = 0; k < NV; ++k)
+            dst[k] = __builtin_nontemporal_load(reinterpret_cast<const vf4 *>(base + qb[k]));
+    } else {
+#pragma unroll
+        for (int k = 0; k < NV; ++k)
+            dst[k] = *reinterpret_cast<const vf4 *>(base + qb[k]);
+    }
     skip = inf_row[r];
     mu = log_mu[r];
     u = log_u[r];
@@ -1016,7 +1029,7 @@ __device__ __forceinline__ int fz_row(const vf4 (&kk)[NV], float mu_r, float u_r
 // exact running (max, sum) pair of col_fold2 (the first step, and the first
 // after an epsilon change, have no usable shift).  Requires M % 4 == 0,
 // M <= 256*W*NV, 16-byte aligned K and log_v.
-template <int W, int RW, int NV, int NB, bool EXACT>
+template <int W, int RW, int NV, int NB, bool EXACT, bool NT>
 __global__ void __launch_bounds__(W * RW * 64)
 sk_fused_step(const float *__restrict__ K, const float *__restrict__ log_v,
               const float *__restrict__ lse2_col, float *__restrict__ lse2_row,
@@ -1070,8 +1083,8 @@ sk_fused_step(const float *__restrict__ K, const float *__restrict__ log_v,
     float rmu[NB], ru[NB], rls[NB];
     int rskip[NB];
 #define TM_FZ_LOAD(P_, I_)                                                                    \
-    fz_load<NV>(kr[P_], rmu[P_], ru[P_], rls[P_], rskip[P_], Kb4 + (I_) * m4, qb, rb + (I_), \
-                log_mu, log_u, lse2_row, inf_row)
+    fz_load<NV, NT>(kr[P_], rmu[P_], ru[P_], rls[P_], rskip[P_], Kb4 + (I_) * m4, qb,        \
+                    rb + (I_), log_mu, log_u, lse2_row, inf_row)
     if constexpr (NB == 1) {
         if (i < end)
             TM_FZ_LOAD(0, i);
@@ -1379,17 +1392,23 @@ int launch_fused_step(const SinkhornLayout &L, bool exact, const float *K, float
     const float sum_lo = exp2f(-win), sum_hi = win > 0.f ? exp2f(win) : 0.f;
     const dim3 grid((unsigned)L.fz_chunk, (unsigned)L.B);
     const FusedShape &f = kFusedShapes[L.fused];
+    // K past the 256 MiB Infinity Cache: streamed with non-temporal loads
+    const bool nontemporal = (size_t)(L.B * L.N * L.M) * sizeof(float) > kNonTemporalBytes;
     const dim3 block(f.W * f.RW * 64);
-#define TM_FUSED1(W_, RW_, NV_, NB_, EX_)                                                  \
-    TM_LAUNCH((sk_fused_step<W_, RW_, NV_, NB_, EX_>), grid, block, 0, stream, K, log_v,     \
+#define TM_FUSED1(W_, RW_, NV_, NB_, EX_, NT_)                                             \
+    TM_LAUNCH((sk_fused_step<W_, RW_, NV_, NB_, EX_, NT_>), grid, block, 0, stream, K, log_v, \
               lse2_col, lse2_row, log_mu, inf_row, log_u, colpart, L.N, L.M, L.fz_chunk,     \
               L.fz_rows, L.fz_interleave, sum_lo, sum_hi, damp, ub)
 #define TM_FUSED(W_, RW_, NV_, NB_)                                                         \
     do {                                                                                    \
-        if (exact)                                                                          \
-            TM_FUSED1(W_, RW_, NV_, NB_, true);                                             \
+        if (exact && nontemporal)                                                           \
+            TM_FUSED1(W_, RW_, NV_, NB_, true, true);                                       \
+        else if (exact)                                                                     \
+            TM_FUSED1(W_, RW_, NV_, NB_, true, false);                                      \
+        else if (nontemporal)                                                               \
+            TM_FUSED1(W_, RW_, NV_, NB_, false, true);                                      \
         else                                                                                \
-            TM_FUSED1(W_, RW_, NV_, NB_, false);                                            \
+            TM_FUSED1(W_, RW_, NV_, NB_, false, false);                                     \
     } while (0)
     switch (L.fused) {
     case kFz1x4x4: TM_FUSED(1, 4, 4, 1); break;
