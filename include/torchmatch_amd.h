@@ -107,6 +107,29 @@ int tm_jv_dense_batch_f32(const float *costs, int64_t B, int32_t N, int32_t M, i
                           void *workspace, size_t workspace_bytes, uint32_t *d_status,
                           hipStream_t stream);
 
+/* tm_jv_dense_batch_f32, then the wait for its result, in one call: returns
+ * once every output is final for work that follows on `stream`, with the
+ * batch's status decoded (TM_OK, TM_ERR_NAN, TM_ERR_NEG_INF, TM_ERR_INTERNAL,
+ * or a launch / HIP error); the replacement for the reference's launch plus
+ * its status readback (dispatch.cu:137-177, cuda_common.cuh:241-249).  For
+ * K <= 64 and B <= 2048 every solve workgroup also writes its problem's
+ * summary to pinned host memory the library holds per host thread and
+ * device, and the host folds those as they arrive, so a batch with no +inf,
+ * NaN or -inf returns without a second launch or a stream synchronisation.
+ * `replays` (host, may be NULL) receives the number of problems that left
+ * the certified path for the exact replay on that path (0 otherwise).  Calls
+ * on one host thread must not overlap (each returns before the next starts).
+ * Same arguments, workspace and results as tm_jv_dense_batch_f32; no status
+ * words are passed. */
+int tm_jv_dense_batch_f32_sync(const float *costs, int64_t B, int32_t N, int32_t M,
+                               int64_t *out, void *workspace, size_t workspace_bytes,
+                               uint32_t *replays, hipStream_t stream);
+
+/* The same for tm_jv_compact_batch_f32. */
+int tm_jv_compact_batch_f32_sync(const float *costs, int64_t B, int32_t N, int32_t M,
+                                 int64_t *out, void *workspace, size_t workspace_bytes,
+                                 uint32_t *replays, hipStream_t stream);
+
 /* tm_jv_dense_batch_f32 without a workspace argument and without any device
  * allocation.  No counterpart in the reference: it is for callers that cannot
  * allocate (code under graph capture, tight serving loops, harnesses that

@@ -13,7 +13,10 @@ status words.  These tests hold that split to the oracle:
 * the status flags of the whole batch, and the guard word cleared between
   calls;
 * TM_JV_FLAG_DONE: set by batches whose problems are all solved in the first
-  launch, never by batches that defer a problem or take the statistics pass.
+  launch, never by batches that defer a problem or take the statistics pass;
+* the synchronous entry points (tm_jv_*_batch_f32_sync), which fold the
+  problems' summaries on the host: the same mappings and error codes, -1 in
+  every output on NaN / -inf, and the replay count.
 """
 
 from __future__ import annotations
@@ -116,3 +119,51 @@ def test_all_inf_problem_uses_batch_sentinel(device):
     rc, code, _, got = _abi(cost, device)
     assert rc == _native.TM_OK and code == _native.TM_OK
     assert (got == jv.jv_dense_batch(cost.numpy())).all()
+
+
+def _sync(cost: torch.Tensor, device, compact: bool = False):
+    """(status code, replays, mapping) through the synchronous C ABI."""
+    lib = _native.lib()
+    c = cost.to(device).contiguous()
+    B, N, M = c.shape
+    out = torch.full((B, N), 12345, dtype=torch.int64, device=device)
+    nbytes = lib.tm_jv_workspace_bytes(B, N, M)
+    ws = torch.full((nbytes,), 0xA5, dtype=torch.uint8, device=device)
+    stream = ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+    fn = lib.tm_jv_compact_batch_f32_sync if compact else lib.tm_jv_dense_batch_f32_sync
+    replays = ctypes.c_uint32(77)
+    code = fn(ctypes.c_void_p(c.data_ptr()), B, N, M, ctypes.c_void_p(out.data_ptr()),
+              ctypes.c_void_p(ws.data_ptr()), nbytes, ctypes.byref(replays), stream)
+    return code, replays.value, out.cpu().numpy()
+
+
+@pytest.mark.parametrize("compact", [False, True])
+@pytest.mark.parametrize(("B", "N", "M", "frac_inf"), [(300, 64, 64, 0.0), (300, 48, 48, 0.5),
+                                                       (200, 30, 41, 0.0), (2049, 16, 16, 0.3)])
+def test_sync_entry_matches_oracle(B, N, M, frac_inf, compact, device):
+    cost = _mixed(B, N, M, seed=7 * B + N, frac_inf=frac_inf)
+    code, replays, got = _sync(cost, device, compact=compact)
+    assert code == _native.TM_OK
+    want = (jv.jv_compact_batch if compact else jv.jv_dense_batch)(cost.numpy())
+    assert (got == want).all()
+    assert replays <= B
+
+
+def test_sync_replay_count_and_errors(device):
+    # integer ties: every square problem fails the certificate and replays
+    g = torch.Generator().manual_seed(5)
+    cost = torch.randint(0, 4, (256, 32, 32), generator=g).float()
+    code, replays, got = _sync(cost, device)
+    assert code == _native.TM_OK and replays >= 250
+    assert (got == jv.jv_dense_batch(cost.numpy())).all()
+    for value, err in ((float("nan"), _native.TM_ERR_NAN), (float("-inf"), _native.TM_ERR_NEG_INF)):
+        bad = torch.rand(128, 64, 64, generator=g)
+        bad[77, 3, 9] = value
+        code, _, got = _sync(bad, device)
+        assert code == err
+        assert (got == -1).all()
+    # a clean call right after an error call
+    clean = torch.rand(128, 64, 64, generator=g)
+    code, _, got = _sync(clean, device)
+    assert code == _native.TM_OK
+    assert (got == jv.jv_dense_batch(clean.numpy())).all()

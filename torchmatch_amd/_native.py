@@ -27,6 +27,7 @@ TM_JV_FLAG_NEG_INF = 2
 TM_JV_FLAG_POS_INF = 4
 TM_JV_FLAG_ANY_FINITE = 8
 TM_JV_FLAG_NEG_ZERO = 16
+TM_JV_FLAG_DONE = 0x80000000
 
 # symbol -> (restype, argtypes); the declarations of include/torchmatch_amd.h
 _VP = ctypes.c_void_p
@@ -36,6 +37,16 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "tm_jv_dense_batch_f32": (
         ctypes.c_int,
         [_VP, ctypes.c_int64, ctypes.c_int32, ctypes.c_int32, _VP, _VP, ctypes.c_size_t, _VP, _VP],
+    ),
+    "tm_jv_dense_batch_f32_sync": (
+        ctypes.c_int,
+        [_VP, ctypes.c_int64, ctypes.c_int32, ctypes.c_int32, _VP, _VP, ctypes.c_size_t,
+         ctypes.POINTER(ctypes.c_uint32), _VP],
+    ),
+    "tm_jv_compact_batch_f32_sync": (
+        ctypes.c_int,
+        [_VP, ctypes.c_int64, ctypes.c_int32, ctypes.c_int32, _VP, _VP, ctypes.c_size_t,
+         ctypes.POINTER(ctypes.c_uint32), _VP],
     ),
     "tm_jv_dense_batch_f32_noalloc": (
         ctypes.c_int, [_VP, ctypes.c_int64, ctypes.c_int32, ctypes.c_int32, _VP, _VP, _VP]

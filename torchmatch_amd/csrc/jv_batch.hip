@@ -35,6 +35,7 @@
 // algorithm instead, so the mapping stays exact for every finite input.
 #include <hip/hip_runtime.h>
 #include <math.h>
+#include <atomic>
 #include <mutex>
 #include <stdint.h>
 #include <stdlib.h>
@@ -1312,6 +1313,17 @@ __device__ __forceinline__ void finish_records(const uint8_t *__restrict__ summa
                            __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
+// kJvFusedSolve with host_tags (host-mapped pinned words): problem b's
+// summary byte also goes to host_tags[b] as (tag << 8) | byte, the
+// workgroup's last write, so a host waiting for the launch can fold the
+// batch itself as the tags arrive (tm_jv_dense_batch_f32_sync).
+__device__ __forceinline__ void publish_tag(uint32_t *host_tags, int64_t b, uint32_t tag,
+                                            uint32_t byte) {
+    if (host_tags != nullptr)
+        __hip_atomic_store(&host_tags[b], (tag << 8) | byte, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
 // One problem per 64-lane workgroup; COMPACT selects the solver of
 // assignment::jonker_compact_batch instead of jonker_dense_batch (same
 // statistics, sentinel, padding and output rules, ops.cpp:176-289).  `stats`
@@ -1322,7 +1334,7 @@ __global__ void __launch_bounds__(64)
 jv_solve_kernel(const float *__restrict__ costs, int64_t B, int N, int M,
                 JvStats *__restrict__ stats, int n_stats, uint8_t *__restrict__ summary,
                 int64_t *__restrict__ out, uint32_t *__restrict__ status, int certify,
-                uint32_t *__restrict__ replays) {
+                uint32_t *__restrict__ replays, uint32_t *__restrict__ host_tags, uint32_t tag) {
     __shared__ WaveLds L;
     __shared__ SerialScratch S;
     const int lane = lane_id();
@@ -1392,8 +1404,10 @@ jv_solve_kernel(const float *__restrict__ costs, int64_t B, int N, int M,
                     ob[i] = -1;
             }
             if (lane == 0) {
+                const uint32_t byte = flags | (bad ? 0u : kJvRecDeferred);
                 stats[b] = JvStats{mx, mn, flags, 0u};
-                summary[b] = (uint8_t)(flags | (bad ? 0u : kJvRecDeferred));
+                summary[b] = (uint8_t)byte;
+                publish_tag(host_tags, b, tag, byte);
             }
             return;
         }
@@ -1415,6 +1429,7 @@ jv_solve_kernel(const float *__restrict__ costs, int64_t B, int N, int M,
             if (lane == 0) {
                 stats[b] = JvStats{mx, mn, flags, 0u};
                 summary[b] = (uint8_t)(flags | info);
+                publish_tag(host_tags, b, tag, flags | info);
             }
         }
     };
@@ -1598,7 +1613,8 @@ JvStats *stats_records(void *workspace) {
 // statistics pass, then the solve (K <= 64) or the large-K kernel.
 template <bool COMPACT>
 int jv_launch(const float *costs, int64_t B, int32_t N, int32_t M, int64_t *out,
-              void *workspace, size_t workspace_bytes, uint32_t *d_status, hipStream_t stream) {
+              void *workspace, size_t workspace_bytes, uint32_t *d_status, hipStream_t stream,
+              uint32_t *host_tags = nullptr, uint32_t tag = 0) {
     if (B < 0 || N < 0 || M < 0)
         return kTmErrInvalidArgument;
     if (B == 0 || N == 0 || M == 0)
@@ -1618,10 +1634,12 @@ int jv_launch(const float *costs, int64_t B, int32_t N, int32_t M, int64_t *out,
         uint8_t *summary = static_cast<uint8_t *>(workspace) + summary_offset(record_count(B, N, M));
         hipLaunchKernelGGL((jv_solve_kernel<COMPACT, kJvFusedSolve>), dim3((unsigned)B), dim3(64),
                            0, stream, costs, B, N, M, stats, (int)B, summary, out, d_status,
-                           certify, replays);
+                           certify, replays, host_tags, tag);
+        if (host_tags != nullptr)  // the caller folds the tags, then finishes if needed
+            return hipGetLastError() == hipSuccess ? kTmOk : kTmErrLaunch;
         hipLaunchKernelGGL((jv_solve_kernel<COMPACT, kJvFusedFinish>), dim3((unsigned)B),
                            dim3(64), 0, stream, costs, B, N, M, stats, (int)B, summary, out,
-                           d_status, certify, replays);
+                           d_status, certify, replays, nullptr, 0u);
         return hipGetLastError() == hipSuccess ? kTmOk : kTmErrLaunch;
     }
     const int64_t n = B * (int64_t)N * M;
@@ -1638,7 +1656,7 @@ int jv_launch(const float *costs, int64_t B, int32_t N, int32_t M, int64_t *out,
                                          stream);
     hipLaunchKernelGGL((jv_solve_kernel<COMPACT, kJvStandalone>), dim3((unsigned)B), dim3(64), 0,
                        stream, costs, B, N, M, stats, (int)blocks, nullptr, out, d_status,
-                       certify, replays);
+                       certify, replays, nullptr, 0u);
     return hipGetLastError() == hipSuccess ? kTmOk : kTmErrLaunch;
 }
 } // namespace
@@ -1662,6 +1680,150 @@ extern "C" int tm_jv_compact_batch_f32(const float *costs, int64_t B, int32_t N,
                                        int64_t *out, void *workspace, size_t workspace_bytes,
                                        uint32_t *d_status, hipStream_t stream) {
     return jv_launch<true>(costs, B, N, M, out, workspace, workspace_bytes, d_status, stream);
+}
+
+// ---------------------------------------------------------------------------
+// Synchronous entry points: the launch, the wait and the status in one call,
+// for callers that wait for the result anyway (the torch ops).  On the fused
+// path (K <= 64, B <= kFusedMaxB) every solve workgroup publishes its summary
+// byte to host-mapped pinned memory under a tag unique to the call; the host
+// folds them as they arrive, so a batch with no +inf, NaN or -inf needs no
+// finishing launch and returns as soon as its last problem is solved.  Other
+// batches run the finishing launch (deferred problems, the -1 fill) or the
+// statistics-pass path, and the host synchronises the stream.
+// ---------------------------------------------------------------------------
+namespace {
+// Pinned words per host thread and device: the two status words, then one
+// tag word per problem (kFusedMaxB of them), zero-filled when allocated.
+struct HostWords {
+    uint32_t *host = nullptr;
+    uint32_t *dev = nullptr;
+};
+
+HostWords *host_words(hipStream_t stream) {
+    constexpr int kMaxDevices = 64;
+    thread_local HostWords slots[kMaxDevices];
+    thread_local bool tried[kMaxDevices] = {};
+    hipDevice_t dev = 0;
+    if (hipStreamGetDevice(stream, &dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+        return nullptr;
+    HostWords &w = slots[dev];
+    if (!tried[dev]) {
+        tried[dev] = true;
+        const size_t bytes = sizeof(uint32_t) * (2 + (size_t)kFusedMaxB);
+        void *h = nullptr;
+        void *d = nullptr;
+        if (hipHostMalloc(&h, bytes, hipHostMallocMapped) == hipSuccess &&
+            hipHostGetDevicePointer(&d, h, 0) == hipSuccess) {
+            memset(h, 0, bytes);
+            w.host = static_cast<uint32_t *>(h);
+            w.dev = static_cast<uint32_t *>(d);
+        } else {
+            (void)hipGetLastError();
+        }
+    }
+    return w.dev != nullptr ? &w : nullptr;
+}
+
+// 24-bit call tags, never 0 (the words' value when allocated).
+uint32_t next_tag() {
+    static std::atomic<uint32_t> counter{0};
+    uint32_t t;
+    do
+        t = (counter.fetch_add(1, std::memory_order_relaxed) + 1u) & 0xffffffu;
+    while (t == 0);
+    return t;
+}
+
+template <bool COMPACT>
+int jv_sync(const float *costs, int64_t B, int32_t N, int32_t M, int64_t *out,
+            void *workspace, size_t workspace_bytes, uint32_t *replays_out,
+            hipStream_t stream) {
+    if (replays_out != nullptr)
+        *replays_out = 0;
+    if (B < 0 || N < 0 || M < 0)
+        return kTmErrInvalidArgument;
+    if (B == 0 || N == 0 || M == 0)
+        return kTmOk;  // caller fills -1
+    HostWords *hw = host_words(stream);
+    if (hw == nullptr)
+        return TM_ERR_HIP;
+    volatile uint32_t *words = hw->host;
+    words[0] = 0;
+    words[1] = 0;
+    if (!fused_path(B, N, M)) {
+        const int rc = jv_launch<COMPACT>(costs, B, N, M, out, workspace, workspace_bytes,
+                                          hw->dev, stream);
+        // synchronise before returning, also after an error: the words are reused
+        const hipError_t e = hipStreamSynchronize(stream);
+        if (rc != kTmOk)
+            return rc;
+        if (e != hipSuccess)
+            return TM_ERR_HIP;
+        const uint32_t seen[2] = {words[0], words[1]};
+        return tm_jv_status_code(seen);
+    }
+    const uint32_t tag = next_tag();
+    int rc = jv_launch<COMPACT>(costs, B, N, M, out, workspace, workspace_bytes, hw->dev, stream,
+                                hw->dev + 2, tag);
+    if (rc != kTmOk) {
+        (void)hipStreamSynchronize(stream);
+        return rc;
+    }
+    // fold the tagged summaries as they arrive; if the stream goes idle
+    // before all of them are in, the launch failed
+    volatile uint32_t *tags = words + 2;
+    uint32_t acc = 0, nrep = 0;
+    int64_t seen = 0;
+    for (uint32_t spin = 1; seen < B; ++spin) {
+        const uint32_t t = tags[seen];
+        if ((t >> 8) == tag) {
+            acc |= t & 0xffu;
+            nrep += (t & kJvRecReplayed) ? 1u : 0u;
+            ++seen;
+            continue;
+        }
+        if ((spin & 4095u) == 0 && hipStreamQuery(stream) != hipErrorNotReady) {
+            const hipError_t e = hipStreamSynchronize(stream);
+            if ((tags[seen] >> 8) != tag)
+                return e != hipSuccess ? TM_ERR_HIP : TM_ERR_INTERNAL;
+        }
+    }
+    if (replays_out != nullptr)
+        *replays_out = nrep;
+    const uint32_t flags = acc & 0x1fu;
+    if ((acc & kJvRecDeferred) || (flags & (kJvFlagNan | kJvFlagNegInf))) {
+        // deferred problems and the -1 fill: the finishing launch
+        uint8_t *summary =
+            static_cast<uint8_t *>(workspace) + summary_offset(record_count(B, N, M));
+        hipLaunchKernelGGL((jv_solve_kernel<COMPACT, kJvFusedFinish>), dim3((unsigned)B),
+                           dim3(64), 0, stream, costs, B, N, M, stats_records(workspace), (int)B,
+                           summary, out, hw->dev, certify_enabled(), replay_counter(workspace),
+                           nullptr, 0u);
+        rc = hipGetLastError() == hipSuccess ? kTmOk : kTmErrLaunch;
+        const hipError_t e = hipStreamSynchronize(stream);
+        if (rc != kTmOk)
+            return rc;
+        if (e != hipSuccess)
+            return TM_ERR_HIP;
+        const uint32_t st[2] = {words[0], words[1]};
+        return tm_jv_status_code(st);
+    }
+    return (acc & kJvRecGuard) ? TM_ERR_INTERNAL : TM_OK;
+}
+} // namespace
+
+extern "C" int tm_jv_dense_batch_f32_sync(const float *costs, int64_t B, int32_t N, int32_t M,
+                                          int64_t *out, void *workspace, size_t workspace_bytes,
+                                          uint32_t *replays, hipStream_t stream) {
+    return jv_sync<false>(costs, B, N, M, out, workspace, workspace_bytes, replays, stream);
+}
+
+extern "C" int tm_jv_compact_batch_f32_sync(const float *costs, int64_t B, int32_t N,
+                                            int32_t M, int64_t *out, void *workspace,
+                                            size_t workspace_bytes, uint32_t *replays,
+                                            hipStream_t stream) {
+    return jv_sync<true>(costs, B, N, M, out, workspace, workspace_bytes, replays, stream);
 }
 
 // ---------------------------------------------------------------------------

@@ -64,43 +64,11 @@ void check_rc(int rc, const char *op_name) {
     }
 }
 
-// Two host-mapped pinned status words per device and host thread, allocated
-// on the thread's first call for that device and kept until the process ends
-// (a call synchronises before it returns, so the thread's next call may
-// reuse them).  Saves the pinned allocation and the device-pointer lookup of
-// every call.
-struct StatusSlot {
-    uint32_t *host = nullptr;
-    uint32_t *dev = nullptr;
-};
-
-const StatusSlot *status_slot(int device) {
-    constexpr int kMaxDevices = 64;
-    thread_local StatusSlot slots[kMaxDevices];
-    thread_local bool tried[kMaxDevices] = {};
-    if (device < 0 || device >= kMaxDevices)
-        return nullptr;
-    StatusSlot &s = slots[device];
-    if (!tried[device]) {
-        tried[device] = true;
-        void *h = nullptr;
-        void *d = nullptr;
-        if (hipHostMalloc(&h, 2 * sizeof(uint32_t), hipHostMallocMapped) == hipSuccess &&
-            hipHostGetDevicePointer(&d, h, 0) == hipSuccess) {
-            s.host = static_cast<uint32_t *>(h);
-            s.dev = static_cast<uint32_t *>(d);
-        } else {
-            (void)hipGetLastError();
-        }
-    }
-    return s.dev != nullptr ? &s : nullptr;
-}
-
 using JvSolver = int (*)(const float *, int64_t, int32_t, int32_t, int64_t *, void *, size_t,
                         uint32_t *, hipStream_t);
 
-// Shared body of the batched JV ops: checks, float32 view, workspace, one
-// solve launch, then the single status readback.
+// Shared body of the batched JV ops: checks, float32 view, workspace, then
+// the library's synchronous solve (launch, wait, status).
 at::Tensor jv_batch_hip(const at::Tensor &costs, JvSolver solver, int64_t max_k,
                         const char *op_name) {
     TORCH_CHECK(costs.is_cuda(), "costs must be a CUDA tensor");
@@ -130,45 +98,10 @@ at::Tensor jv_batch_hip(const at::Tensor &costs, JvSolver solver, int64_t max_k,
     const at::Tensor cf = costs.scalar_type() == at::kFloat ? costs : costs.to(at::kFloat);
     const size_t ws_bytes = tm_jv_workspace_bytes(B, (int32_t)N, (int32_t)M);
     auto ws = at::empty({(int64_t)ws_bytes}, costs.options().dtype(at::kByte));
-    // The status words go to pinned host memory the kernels write directly,
-    // so the readback is the stream synchronisation alone (no copy command);
-    // device memory and a copy when no pinned block can be mapped.
-    if (const StatusSlot *slot = status_slot(costs.get_device())) {
-        volatile uint32_t *words = slot->host;
-        words[0] = 0;
-        int rc = solver(cf.data_ptr<float>(), B, (int32_t)N, (int32_t)M,
-                        out.data_ptr<int64_t>(), ws.data_ptr(), ws_bytes, slot->dev, stream);
-        // Wait for TM_JV_FLAG_DONE (written last by launches that set it) or,
-        // for launches that do not, for the stream; synchronise before any
-        // error leaves, since the next call on this thread reuses the words.
-        hipError_t se = hipSuccess;
-        if (rc == TM_OK) {
-            for (uint32_t spin = 1;; ++spin) {
-                if (words[0] & TM_JV_FLAG_DONE)
-                    break;
-                if ((spin & 4095u) == 0 && hipStreamQuery(stream) != hipErrorNotReady) {
-                    se = hipStreamSynchronize(stream);
-                    break;
-                }
-            }
-        } else {
-            se = hipStreamSynchronize(stream);
-        }
-        check_rc(rc, op_name);
-        TORCH_CHECK(se == hipSuccess, op_name, ": stream synchronisation failed: ",
-                    hipGetErrorString(se));
-        uint32_t seen[2] = {words[0], words[1]};
-        rc = tm_jv_status_code(seen);
-        check_rc(rc, op_name);
-        return out;
-    }
-    auto status = at::empty({2}, costs.options().dtype(at::kInt));
-    int rc = solver(cf.data_ptr<float>(), B, (int32_t)N, (int32_t)M, out.data_ptr<int64_t>(),
-                    ws.data_ptr(), ws_bytes,
-                    reinterpret_cast<uint32_t *>(status.data_ptr<int32_t>()), stream);
-    check_rc(rc, op_name);
-    rc = tm_jv_check_status(reinterpret_cast<const uint32_t *>(status.data_ptr<int32_t>()),
-                            stream);
+    // launch, wait and status in one call (the library folds the batch's
+    // status on the host as the solve publishes it)
+    const int rc = solver(cf.data_ptr<float>(), B, (int32_t)N, (int32_t)M,
+                          out.data_ptr<int64_t>(), ws.data_ptr(), ws_bytes, nullptr, stream);
     check_rc(rc, op_name);
     return out;
 }
@@ -200,7 +133,7 @@ unpack_hip(const at::Tensor &costs, const at::Tensor &packed, const char *op_nam
 // Reference: assignment/cuda/dispatch.cu:137-177; results follow the CPU op
 // assignment/cpu/ops.cpp:176-289 (rectangular input accepted, like the CPU op).
 at::Tensor jonker_dense_batch_hip(const at::Tensor &costs) {
-    return jv_batch_hip(costs, &tm_jv_dense_batch_f32, tm_jv_max_k(), "jonker_dense_batch");
+    return jv_batch_hip(costs, &tm_jv_dense_batch_f32_sync, tm_jv_max_k(), "jonker_dense_batch");
 }
 
 // CUDA-key kernel of assignment::jonker_dense_batch_unpacked (CPU op at
@@ -214,7 +147,7 @@ jonker_dense_batch_unpacked_hip(const at::Tensor &costs) {
 // op assignment/cpu/ops.cpp:431-433 (solve_batch around the compact solver of
 // jonker_compact_core.h), which has no device counterpart in the reference.
 at::Tensor jonker_compact_batch_hip(const at::Tensor &costs) {
-    return jv_batch_hip(costs, &tm_jv_compact_batch_f32, tm_jv_compact_max_k(),
+    return jv_batch_hip(costs, &tm_jv_compact_batch_f32_sync, tm_jv_compact_max_k(),
                         "jonker_compact_batch");
 }
 
