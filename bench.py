@@ -54,10 +54,10 @@ JV_C2_RELAXATIONS = 28_681_299
 JV_BYTES_PER_RELAXATION = 12
 
 # The device kernel's certified path on the C2 seed-0 batch: its slowest
-# problem (544) takes 364 sequential steps (rows scanned + paths) in the
+# problem (456) takes 314 sequential steps (rows scanned + paths) in the
 # shortest-path searches, each needing one wave-wide argmin before the next
 # (oracle.jv.sap_batch_counted; tests/test_oracle_jv.py recomputes it).
-JV_C2_CRITICAL_STEPS = 364
+JV_C2_CRITICAL_STEPS = 314
 
 # HBM bytes per launch from rocprofv3 --pmc FETCH_SIZE (x2.00, the factor a
 # 256 MiB device copy calibrates) and WRITE_SIZE (x1.00), per dispatch; the

@@ -318,13 +318,78 @@ static void jvo_square(uint32_t n, const float *c, jvo_scratch *s, jvo_counts *c
 }
 
 /* Work model of the device kernel's certified path (not a reference
- * function): the same column reduction, then one shortest augmenting path per
- * free row with no augmenting row reduction.  Counted per problem, the
- * searches' scanned rows + paths are the sequential steps that path takes on
- * the device.  Its mapping equals the reference's whenever the optimum is
- * unique (the device keeps it only then). */
+ * function): the column reduction's claims as the reference's, the transfer
+ * taken for every unique row from the column minima at once (each row's
+ * minimum over its other columns of c - v, with v the minima before any
+ * transfer), then one shortest augmenting path per free row, from the
+ * highest free row down, with no augmenting row reduction.  Counted per
+ * problem, the searches' scanned rows + paths are the sequential steps that
+ * path takes on the device.  Its mapping equals the reference's whenever the
+ * optimum is unique (the device keeps it only then). */
+static int32_t jvo_column_reduction_parallel(uint32_t n, const float *c, jvo_scratch *s,
+                                             jvo_counts *cnt) {
+    int32_t *x = s->x, *y = s->y, *fr = s->free_rows;
+    float *v = s->v, *v0 = s->d;
+    char *unique = s->unique;
+    for (uint32_t k = 0; k < n; ++k) {
+        unique[k] = 1;
+        x[k] = -1;
+        v[k] = JVO_LARGE;
+        y[k] = 0;
+    }
+    for (uint32_t i = 0; i < n; ++i) {
+        const float *row = c + (size_t)i * n;
+        for (uint32_t j = 0; j < n; ++j)
+            if (row[j] < v[j]) {
+                v[j] = row[j];
+                y[j] = (int32_t)i;
+            }
+    }
+    for (int32_t j = (int32_t)n - 1; j >= 0; --j) {
+        const int32_t i = y[j];
+        if (x[i] < 0) {
+            x[i] = j;
+        } else {
+            unique[i] = 0;
+            y[j] = -1;
+        }
+    }
+    for (uint32_t j = 0; j < n; ++j)
+        v0[j] = v[j];
+    int32_t n_free = 0;
+    for (uint32_t i = 0; i < n; ++i) {
+        if (x[i] < 0) {
+            fr[n_free++] = (int32_t)i;
+            continue;
+        }
+        if (!unique[i])
+            continue;
+        const int32_t own = x[i];
+        const float *row = c + (size_t)i * n;
+        float mn = JVO_LARGE;
+        for (uint32_t j = 0; j < n; ++j) {
+            if ((int32_t)j == own)
+                continue;
+            const float r = row[j] - v0[j];
+            if (r < mn)
+                mn = r;
+        }
+        if (cnt)
+            cnt->relax += n - 1;
+        v[own] = v0[own] - mn;
+    }
+    if (cnt)
+        cnt->relax += (int64_t)n * n;
+    return n_free;
+}
+
 static void jvo_sap_square(uint32_t n, const float *c, jvo_scratch *s, jvo_counts *cnt) {
-    const int32_t n_free = jvo_column_reduction(n, c, s, cnt);
+    const int32_t n_free = jvo_column_reduction_parallel(n, c, s, cnt);
+    for (int32_t a = 0, b = n_free - 1; a < b; ++a, --b) {
+        const int32_t t = s->free_rows[a];
+        s->free_rows[a] = s->free_rows[b];
+        s->free_rows[b] = t;
+    }
     if (n_free > 0)
         jvo_augment(n, c, (uint32_t)n_free, s, cnt);
 }
