@@ -3,12 +3,13 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-sinkhorn]
                     [--no-extra] [--no-cpu-baseline] [--copy-calibration]
+                    [--no-host-facts]
 
 Prints ONE JSON line.  ``value`` is the BASELINE metric's lead figure:
 batched JV solves/s on C2 = float32 (1024, 64, 64) i.i.d. U[0,1), one step =
-one ``torch.ops.assignment.jonker_dense_batch`` call (statistics pass, solve,
-the validation readback the op performs), inputs resident in HBM before
-timing.  The Sinkhorn leg (C4 = (16, 2048, 2048), reg 0.05, 200 iterations)
+one ``torch.ops.assignment.jonker_dense_batch`` call (the solve launch, which
+also takes the batch statistics, and the wait for its validated result that
+the op performs), inputs resident in HBM before timing.  The Sinkhorn leg (C4 = (16, 2048, 2048), reg 0.05, 200 iterations)
 reports iterations/s and HBM GB/s from the slope between 200- and
 20-iteration runs; one step of this build reads K once (B*N*M*4 algorithmic
 bytes per iteration).  Beside it, the same kernel shape at B = 64 (1 GiB of
@@ -63,13 +64,16 @@ JV_C2_CRITICAL_STEPS = 314
 # 256 MiB device copy calibrates) and WRITE_SIZE (x1.00), per dispatch; the
 # runs and commands are recorded in the profiles/ summaries.
 MEASURED_TRAFFIC = {
-    # jv_stats_kernel + jv_solve_kernel on C2
-    "jv_c2": int(((8230.5 + 8351.5) * 2 + 8.1 + 512.0) * 1024),
+    # the fused solve launch on C2 (the op's only launch on this batch)
+    "jv_c2": int((8349.5 * 2 + 584.0) * 1024),
     # sk_fused_step + sk_col_merge_blk per C4 iteration: two batch groups of 8,
     # each one pass + one merge (K once, column sums twice)
-    "sinkhorn_c4": int(2 * ((66330.7 + 1173.5) * 2 + 2176.1 + 128.0) * 1024),
+    "sinkhorn_c4": int(2 * ((66330.9 + 1172.5) * 2 + 2176.0 + 128.0) * 1024),
+    # the same per iteration of the B = 64 control (two groups of 32; K read
+    # with non-temporal loads)
+    "sinkhorn_b64": int(2 * ((264874.5 + 1508.5) * 2 + 2560.0 + 512.0) * 1024),
     # the same pair per C5 iteration (one group)
-    "sinkhorn_c5": int(((525986.8 + 8354.5) * 2 + 17532.1 + 128.0) * 1024),
+    "sinkhorn_c5": int(((525955.8 + 8359.5) * 2 + 17412.8 + 128.0) * 1024),
 }
 
 
@@ -155,7 +159,13 @@ def bench_jv(steps: int, warmup: int, device) -> dict:
     wall = time.perf_counter() - t0
     ms_per_step = ms / steps
 
-    # kernel-level: the C-ABI entry launched back to back (no readback)
+    # kernel-level: the asynchronous C-ABI entry launched back to back, timed
+    # with one pair of events on the launch stream over the repeats (an event
+    # pair around a single launch adds 4-6 us on this platform): the fused
+    # solve plus the finishing launch the asynchronous entry always issues
+    # (the op itself, which waits on the host, runs the solve alone on this
+    # batch); the profiler's durations of jv_solve_kernel<false, 1> and
+    # <false, 2> add up to it
     lib = _native.lib()
     ws_bytes = lib.tm_jv_workspace_bytes(B, N, M)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=device)
@@ -216,7 +226,8 @@ def bench_jv(steps: int, warmup: int, device) -> dict:
             "argmin_cycles": round(chain["cycles_per_round"], 1),
             "clock_ghz": round(chain["clock_ghz"], 3),
             "note": "floor = slowest problem's search steps x one dependent wave-wide "
-                    "argmin; achieved = statistics pass + solve launch",
+                    "argmin; achieved = the asynchronous entry's launch (fused solve + "
+                    "finishing launch)",
         }
     # other seeds: problems that fail the certificate replay the reference
     # order, so batches differ in time
@@ -243,8 +254,9 @@ def bench_jv(steps: int, warmup: int, device) -> dict:
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 6),
             "traffic": MEASURED_TRAFFIC["jv_c2"],
-            "note": "statistics pass + LDS-resident solve per launch; HBM is not binding, "
-                    "the per-problem dependency chain is (latency_roofline)",
+            "note": "one read of the input per launch (statistics taken in the solve); "
+                    "HBM is not binding, the per-problem dependency chain is "
+                    "(latency_roofline); traffic = the fused solve's FETCH/WRITE",
         },
         "lds_roofline": lds_roofline,
         "latency_roofline": latency,
@@ -277,7 +289,8 @@ def bench_sinkhorn(device, B: int = 16, n_long: int = 200, n_short: int = 20,
     t_long = best(n_long)
     t_short = best(n_short)
     per_iter_ms = (t_long - t_short) / (n_long - n_short)
-    traffic = MEASURED_TRAFFIC.get("sinkhorn_c4") if B == 16 else None
+    traffic = {16: MEASURED_TRAFFIC.get("sinkhorn_c4"),
+               64: MEASURED_TRAFFIC.get("sinkhorn_b64")}.get(B)
     return {
         "config": {"workload": "log_sinkhorn C4" if B == 16 else "log_sinkhorn C4 shape",
                    "B": B, "N": N, "M": M, "reg": reg, "n_iter": n_long},
@@ -512,8 +525,12 @@ def main() -> int:
                    help="skip the C3 (K=768 JV) and C5 (unbalanced 16384^2) legs")
     p.add_argument("--copy-calibration", action="store_true",
                    help="only run a 256 MiB device copy (profiler counter calibration)")
+    p.add_argument("--no-host-facts", action="store_true",
+                   help="skip the lscpu / hipcc child processes (for runs under a profiler "
+                        "that initialises the GPU before the script starts)")
     args = p.parse_args()
-    host = None if args.copy_calibration else host_facts()  # before the GPU is touched
+    # before the GPU is touched
+    host = None if args.copy_calibration or args.no_host_facts else host_facts()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU only (each box has one MI355X); "
               "run with --gpus 1", file=sys.stderr)
