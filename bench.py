@@ -604,6 +604,7 @@ def main() -> int:
             line["unbalanced_c5"]["cpu_baseline"] = cpu_baseline_unbalanced_c5()
         if not args.no_sinkhorn:
             line["sinkhorn"]["cpu_baseline"] = cpu_baseline_sinkhorn()
+    host = host or {}
     host["gpu"] = torch.cuda.get_device_name(0)
     line["host"] = host
     line["inputs"] = inputs
