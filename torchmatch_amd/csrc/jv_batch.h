@@ -38,21 +38,17 @@ constexpr uint32_t kJvRecDeferred = 1u << 5;  // holds +inf: solved once the bat
 constexpr uint32_t kJvRecReplayed = 1u << 6;  // left the certified path for the exact replay
 constexpr uint32_t kJvRecGuard = 1u << 7;     // a solve hit its iteration guard
 
-// K in (64, jv_large_max_k()], cost read from global memory (jv_large.hip).
-// With `claims` (B zeroed words) and N <= M: the paired launch (certified
-// role and exact replay per problem; `replays` counts the replay's answers);
-// otherwise the exact replay alone, one workgroup per problem.
+// K in (64, jv_large_max_k()]: one workgroup per problem, cost read from
+// global memory (jv_large.hip).
 int launch_jv_large(const float *costs, int64_t B, int N, int M, const JvStats *partial,
-                    int n_partial, int64_t *out, uint32_t *status, uint32_t *claims,
-                    uint32_t *replays, hipStream_t stream);
+                    int n_partial, int64_t *out, uint32_t *status, hipStream_t stream);
 int jv_large_max_k();
 
 // Compact solver (assignment::jonker_compact_batch) for K in (64,
 // jv_compact_max_k()] (jv_large.hip).
 int launch_jv_compact_large(const float *costs, int64_t B, int N, int M,
                             const JvStats *partial, int n_partial, int64_t *out,
-                            uint32_t *status, uint32_t *claims, uint32_t *replays,
-                            hipStream_t stream);
+                            uint32_t *status, hipStream_t stream);
 int jv_compact_max_k();
 
 } // namespace tmamd

@@ -57,15 +57,11 @@ constexpr int kStatsBlock = 1024;  // 16 waves: four per SIMD while the pass str
 // ---------------------------------------------------------------------------
 __global__ void __launch_bounds__(kStatsBlock)
 jv_stats_kernel(const float *__restrict__ costs, int64_t n, JvStats *__restrict__ partial,
-                uint32_t *__restrict__ status, uint32_t *__restrict__ replays,
-                uint32_t *__restrict__ claims, int64_t n_claims) {
+                uint32_t *__restrict__ status, uint32_t *__restrict__ replays) {
     if (blockIdx.x == 0 && threadIdx.x == 0) {
         status[1] = 0;  // internal-error word, raised by jv_solve_kernel
         *replays = 0;   // problems the certified path handed to the exact replay
     }
-    for (int64_t k = (int64_t)blockIdx.x * kStatsBlock + threadIdx.x; k < n_claims;
-         k += (int64_t)gridDim.x * kStatsBlock)
-        claims[k] = 0;
     float mx = -finf(), mn = finf();
     uint32_t flags = 0;
     const int64_t stride = (int64_t)gridDim.x * kStatsBlock;
@@ -1597,12 +1593,8 @@ int64_t record_count(int64_t B, int32_t N, int32_t M) {
 
 extern "C" size_t tm_jv_workspace_bytes(int64_t B, int32_t N, int32_t M) {
     const int64_t records = record_count(B, N, M);
-    const int K = N > M ? N : M;
-    // fused path: one summary byte per problem; K > 64: one claim word
-    const size_t tail = fused_path(B, N, M) ? (size_t)((B + 15) / 16 * 16)
-                        : K > kTile        ? (size_t)((4 * B + 15) / 16 * 16)
-                                           : 0;
-    return summary_offset(records) + tail;
+    const size_t summary = fused_path(B, N, M) ? (size_t)((B + 15) / 16 * 16) : 0;
+    return summary_offset(records) + summary;
 }
 
 namespace {
@@ -1618,14 +1610,6 @@ uint32_t *replay_counter(void *workspace) { return static_cast<uint32_t *>(works
 JvStats *stats_records(void *workspace) {
     return reinterpret_cast<JvStats *>(static_cast<char *>(workspace) + kStatsOffset);
 }
-
-// The paired launch for 64 < K <= 1024 and N <= M (certified role and exact
-// replay per problem, jv_large.hip) is switched off: on the C3 batch
-// (64 x 512 x 768, 20 % +inf) it ended in a GPU memory fault whose cause has
-// not been found (a host emulation of the certified role stays in bounds
-// and matches the oracle on every problem of that batch).  Those batches run
-// the exact replay alone.
-constexpr bool kPairedLargeK = false;
 
 // The launches of tm_jv_dense_batch_f32 / tm_jv_compact_batch_f32.  K <= 64
 // with B <= kFusedMaxB: the fused solve launch, then the finishing launch (no
@@ -1665,22 +1649,15 @@ int jv_launch(const float *costs, int64_t B, int32_t N, int32_t M, int64_t *out,
     const int64_t n = B * (int64_t)N * M;
     int64_t blocks = (n / 4 + kStatsBlock - 1) / kStatsBlock;
     blocks = blocks < 1 ? 1 : (blocks > kJvMaxStatBlocks ? kJvMaxStatBlocks : blocks);
-    // K > 64 with N <= M: per-problem claim words of the paired launch,
-    // cleared by the statistics pass (the paired launch is switched off:
-    // kPairedLargeK)
-    uint32_t *claims = (kPairedLargeK && K > kTile && N <= M && certify)
-                           ? reinterpret_cast<uint32_t *>(static_cast<char *>(workspace) +
-                                                          summary_offset(record_count(B, N, M)))
-                           : nullptr;
     hipLaunchKernelGGL(jv_stats_kernel, dim3((unsigned)blocks), dim3(kStatsBlock), 0, stream,
-                       costs, n, stats, d_status, replays, claims, claims ? B : 0);
+                       costs, n, stats, d_status, replays);
     if (hipGetLastError() != hipSuccess)
         return kTmErrLaunch;
     if (K > kTile)
         return COMPACT ? launch_jv_compact_large(costs, B, N, M, stats, (int)blocks, out,
-                                                 d_status, claims, replays, stream)
+                                                 d_status, stream)
                        : launch_jv_large(costs, B, N, M, stats, (int)blocks, out, d_status,
-                                         claims, replays, stream);
+                                         stream);
     hipLaunchKernelGGL((jv_solve_kernel<COMPACT, kJvStandalone>), dim3((unsigned)B), dim3(64), 0,
                        stream, costs, B, N, M, stats, (int)blocks, nullptr, out, d_status,
                        certify, replays, nullptr, 0u);

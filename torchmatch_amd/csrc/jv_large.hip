@@ -25,7 +25,6 @@
 #include "jv_batch.h"
 #include "jv_common.h"
 #include "jv_compact.h"
-#include "jv_large_cert.h"
 #include "wave.h"
 
 namespace tmamd {
@@ -358,20 +357,6 @@ __device__ void scan_row(LargeLds &L, const CostView &C, int fi, int E, int K,
     }
 }
 
-// Outcomes of large_solve.
-enum LargeSolveResult { kSolveFailed = 0, kSolveDone = 1, kSolveAborted = 2 };
-
-// Per-problem claim word of the paired launch: 0 open, 1 the certified role
-// wrote the answer, 2 the replay did.
-constexpr uint32_t kClaimOpen = 0, kClaimCertified = 1, kClaimReplay = 2;
-
-// The replay of a problem stops once the certified role has answered it.
-__device__ __forceinline__ bool claimed_elsewhere(const uint32_t *claim) {
-    return claim != nullptr &&
-           __hip_atomic_load(claim, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-               kClaimCertified;
-}
-
 // COMPACT = false: jonker_dense_flat.h:124-274; COMPACT = true:
 // jonker_compact_core.h:51-252 (only called on its value range, where every
 // reduced cost stays far below LARGE): the same steps with no cap on the
@@ -379,8 +364,7 @@ __device__ __forceinline__ bool claimed_elsewhere(const uint32_t *claim) {
 // ending a path, the dual update (v + d) - min and FLT_MAX as the transfer's
 // starting minimum.
 template <bool COMPACT>
-__device__ __forceinline__ int large_solve(const int K, const int E, LargeLds &L,
-                                           const CostView &C, const uint32_t *abort_word) {
+__device__ bool large_solve(const int K, const int E, LargeLds &L, const CostView &C) {
     const int lane = lane_id();
 
     // ---- column reduction (ccrrt_dense, jonker_dense_flat.h:124-176) ----
@@ -518,9 +502,7 @@ __device__ __forceinline__ int large_solve(const int K, const int E, LargeLds &L
         while (cur < (uint32_t)n_free) {
             ++rr;
             if (rr > rr_limit)
-                return kSolveFailed;
-            if ((rr & 63u) == 0 && claimed_elsewhere(abort_word))
-                return kSolveAborted;
+                return false;
             const int fi = L.fr[cur];
             ++cur;
             const bool pad_row = fi >= C.N;
@@ -623,8 +605,6 @@ __device__ __forceinline__ int large_solve(const int K, const int E, LargeLds &L
     if (n_free > 0 && L.fr[0] < C.N)
         load_row_raw(C, L.fr[0], nx);
     for (int f = 0; f < n_free; ++f) {
-        if (claimed_elsewhere(abort_word))
-            return kSolveAborted;
         const int start = L.fr[f];
         float cr[kMaxChunks];
 #pragma unroll
@@ -646,7 +626,7 @@ __device__ __forceinline__ int large_solve(const int K, const int E, LargeLds &L
         float group_level = 0.f;  // d of the current minimum group
         while (final_j < 0) {
             if (lo >= K)
-                return kSolveFailed;
+                return false;
             if (lo == hi) {
                 // find_dense over positions [lo, K): classify each position
                 // against the running minimum of the positions before it
@@ -845,23 +825,19 @@ __device__ __forceinline__ int large_solve(const int K, const int E, LargeLds &L
         }
         lds_sync();
     }
-    return kSolveDone;
+    return true;
 }
 
-// The exact replay of problem b by one wave (lanes 0-63 of the workgroup).
-// With `claim` (the paired launch) it stops once the certified role has
-// answered the problem, and writes its own answer only if it claims the
-// problem first; `replays` counts those answers.
 template <bool COMPACT>
-__device__ __forceinline__ void replay_problem(LargeLds &L, const float *__restrict__ costs,
-                                               int64_t b, int N, int M,
-                                               const JvStats *__restrict__ partial, int n_partial,
-                                               int64_t *__restrict__ out,
-                                               uint32_t *__restrict__ status, uint32_t *claim,
-                                               uint32_t *replays) {
+__global__ void __launch_bounds__(64)
+jv_solve_large_kernel(const float *__restrict__ costs, int64_t B, int N, int M,
+                      const JvStats *__restrict__ partial, int n_partial,
+                      int64_t *__restrict__ out, uint32_t *__restrict__ status) {
+    __shared__ LargeLds L;
     const int lane = lane_id();
     const int K = N > M ? N : M;
     const int E = (K + 63) / 64;
+    const int64_t b = blockIdx.x;
     float mx, mn;
     uint32_t flags;
     fold_stats(partial, n_partial, mx, mn, flags);
@@ -879,10 +855,10 @@ __device__ __forceinline__ void replay_problem(LargeLds &L, const float *__restr
     C.N = N;
     C.M = M;
     C.sentinel = any_finite ? (mx + 1.0f) * (float)(K + 1) : 1.0f;
-    int res;
+    bool ok;
     if (!COMPACT || compact_wave_range(any_finite, mx, mn, (flags & kJvFlagPosInf) != 0,
                                        C.sentinel)) {
-        res = large_solve<COMPACT>(K, E, L, C, claim);
+        ok = large_solve<COMPACT>(K, E, L, C);
     } else {
         // compact outside the wave path's range: the lane-serial transcription
         if (lane == 0) {
@@ -893,20 +869,9 @@ __device__ __forceinline__ void replay_problem(LargeLds &L, const float *__restr
                                      L.d) ? 1 : 0;
         }
         lds_sync();
-        res = L.ev[0] != 0 ? kSolveDone : kSolveFailed;
+        ok = L.ev[0] != 0;
     }
-    if (res == kSolveAborted)
-        return;
-    if (claim != nullptr) {
-        uint32_t prev = 0;
-        if (lane == 0)
-            prev = atomicCAS(claim, kClaimOpen, kClaimReplay);
-        if (readlane_i((int)prev, 0) != (int)kClaimOpen)
-            return;  // the certified role answered first
-        if (lane == 0)
-            atomicAdd(replays, 1u);
-    }
-    if (res != kSolveDone) {
+    if (!ok) {
         if (lane == 0)
             raise_guard(status);
         for (int i = lane; i < N; i += 64)
@@ -919,129 +884,21 @@ __device__ __forceinline__ void replay_problem(LargeLds &L, const float *__restr
     }
 }
 
-template <bool COMPACT>
-__global__ void __launch_bounds__(64)
-jv_solve_large_kernel(const float *__restrict__ costs, int64_t B, int N, int M,
-                      const JvStats *__restrict__ partial, int n_partial,
-                      int64_t *__restrict__ out, uint32_t *__restrict__ status) {
-    __shared__ LargeLds L;
-    replay_problem<COMPACT>(L, costs, blockIdx.x, N, M, partial, n_partial, out, status,
-                            nullptr, nullptr);
-}
-
-// The certified role for problem b (all four waves).  Leaves the problem to
-// the replay (no claim) when the batch holds NaN / -inf, no finite value,
-// values outside the float paths' range, or when the certificate fails.
-template <int CW>
-__device__ __forceinline__ void certify_problem(cert::Lds &L, const float *__restrict__ costs,
-                                                int64_t b, int N, int M,
-                                                const JvStats *__restrict__ partial, int n_partial,
-                                                int64_t *__restrict__ out, uint32_t *claim) {
-    float mx, mn;
-    uint32_t flags;
-    fold_stats(partial, n_partial, mx, mn, flags);
-    if ((flags & (kJvFlagNan | kJvFlagNegInf)) || !(flags & kJvFlagAnyFinite))
-        return;
-    const float sentinel = (mx + 1.0f) * (float)(M + 1);
-    if (mx > kFastRange || mn < -kFastRange ||
-        ((flags & kJvFlagPosInf) && !(sentinel <= kFastRange)))
-        return;
-    const float *src = costs + b * (int64_t)N * M;
-    if (!cert::solve<CW>(L, src, N, M, sentinel))
-        return;
-    __shared__ uint32_t prev;
-    if (threadIdx.x == 0)
-        prev = atomicCAS(claim, kClaimOpen, kClaimCertified);
-    __syncthreads();
-    if (prev != kClaimOpen)
-        return;  // the replay answered first
-    int64_t *ob = out + b * N;
-    for (int i = threadIdx.x; i < N; i += cert::kThreads)
-        ob[i] = L.x[i];
-}
-
-// Not launched at present (kPairedLargeK in jv_batch.hip: it ended in a GPU
-// memory fault on the C3 batch, cause not found).
-// Paired launch for N <= M: workgroups [0, B) run the certified role on
-// problem b, workgroups [B, 2B) the exact replay of problem b - B on their
-// first wave (the other three end at once: a barrier waits only for the
-// waves still running).  The claim word decides whose answer is written; the
-// replay stops once the certified role has claimed its problem, so a batch
-// costs the certified solve unless a problem fails its certificate.
-template <bool COMPACT, int CW>
-__global__ void __launch_bounds__(cert::kThreads)
-jv_large_pair_kernel(const float *__restrict__ costs, int64_t B, int N, int M,
-                     const JvStats *__restrict__ partial, int n_partial,
-                     int64_t *__restrict__ out, uint32_t *__restrict__ status,
-                     uint32_t *__restrict__ claims, uint32_t *__restrict__ replays) {
-    __shared__ union {
-        LargeLds replay;
-        cert::Lds certified;
-    } U;
-    const int64_t g = blockIdx.x;
-    if (g < B) {
-        certify_problem<CW>(U.certified, costs, g, N, M, partial, n_partial, out, claims + g);
-        return;
-    }
-    if (__builtin_amdgcn_readfirstlane(threadIdx.x) >= 64)
-        return;
-    replay_problem<COMPACT>(U.replay, costs, g - B, N, M, partial, n_partial, out, status,
-                            claims + (g - B), replays);
-}
-
-} // namespace
-
-namespace {
-template <bool COMPACT, int CW>
-int launch_pair(const float *costs, int64_t B, int N, int M, const JvStats *partial,
-                int n_partial, int64_t *out, uint32_t *status, uint32_t *claims,
-                uint32_t *replays, hipStream_t stream) {
-    hipLaunchKernelGGL((jv_large_pair_kernel<COMPACT, CW>), dim3((unsigned)(2 * B)),
-                       dim3(cert::kThreads), 0, stream, costs, B, N, M, partial, n_partial, out,
-                       status, claims, replays);
-    return hipGetLastError() == hipSuccess ? kTmOk : kTmErrLaunch;
-}
-
-template <bool COMPACT>
-int launch_large(const float *costs, int64_t B, int N, int M, const JvStats *partial,
-                 int n_partial, int64_t *out, uint32_t *status, uint32_t *claims,
-                 uint32_t *replays, hipStream_t stream) {
-    if (claims != nullptr && N <= M && M <= cert::kMaxM && B <= 0x3fffffff) {
-        const int cw = (M + cert::kThreads - 1) / cert::kThreads;
-        switch (cw) {
-        case 1:
-            return launch_pair<COMPACT, 1>(costs, B, N, M, partial, n_partial, out, status,
-                                           claims, replays, stream);
-        case 2:
-            return launch_pair<COMPACT, 2>(costs, B, N, M, partial, n_partial, out, status,
-                                           claims, replays, stream);
-        case 3:
-            return launch_pair<COMPACT, 3>(costs, B, N, M, partial, n_partial, out, status,
-                                           claims, replays, stream);
-        default:
-            return launch_pair<COMPACT, 4>(costs, B, N, M, partial, n_partial, out, status,
-                                           claims, replays, stream);
-        }
-    }
-    hipLaunchKernelGGL(jv_solve_large_kernel<COMPACT>, dim3((unsigned)B), dim3(64), 0, stream,
-                       costs, B, N, M, partial, n_partial, out, status);
-    return hipGetLastError() == hipSuccess ? kTmOk : kTmErrLaunch;
-}
 } // namespace
 
 int launch_jv_large(const float *costs, int64_t B, int N, int M, const JvStats *partial,
-                    int n_partial, int64_t *out, uint32_t *status, uint32_t *claims,
-                    uint32_t *replays, hipStream_t stream) {
-    return launch_large<false>(costs, B, N, M, partial, n_partial, out, status, claims,
-                               replays, stream);
+                    int n_partial, int64_t *out, uint32_t *status, hipStream_t stream) {
+    hipLaunchKernelGGL(jv_solve_large_kernel<false>, dim3((unsigned)B), dim3(64), 0, stream,
+                       costs, B, N, M, partial, n_partial, out, status);
+    return hipGetLastError() == hipSuccess ? kTmOk : kTmErrLaunch;
 }
 
 int launch_jv_compact_large(const float *costs, int64_t B, int N, int M,
                             const JvStats *partial, int n_partial, int64_t *out,
-                            uint32_t *status, uint32_t *claims, uint32_t *replays,
-                            hipStream_t stream) {
-    return launch_large<true>(costs, B, N, M, partial, n_partial, out, status, claims, replays,
-                              stream);
+                            uint32_t *status, hipStream_t stream) {
+    hipLaunchKernelGGL(jv_solve_large_kernel<true>, dim3((unsigned)B), dim3(64), 0, stream,
+                       costs, B, N, M, partial, n_partial, out, status);
+    return hipGetLastError() == hipSuccess ? kTmOk : kTmErrLaunch;
 }
 
 int jv_large_max_k() { return kMaxLargeK; }
