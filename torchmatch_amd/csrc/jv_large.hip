@@ -200,22 +200,54 @@ __device__ __forceinline__ int append_events(LargeLds &L, int n_ev, uint64_t mas
     return n_ev + __builtin_popcountll(mask);
 }
 
+// A row's costs, chunk e of lane l at [e]; a vector value, so a read at a
+// wave-uniform chunk compiles to an indexed register move.
+typedef float f32x16 __attribute__((ext_vector_type(kMaxChunks)));
+
+// Lane l's value of chunk e (e, l uniform).
+__device__ __forceinline__ float chunk_value(const f32x16 &v, int e, int l) {
+    return readlane_f(v[e], l);
+}
+
+// Smallest column j = e * 64 + lane with key kk[e] == k, other than x1 and
+// x2 (uniform; kKeyNone if there is none).  One wave minimum over the
+// columns: the first column in index order, as the reference's scans take it.
+__device__ __forceinline__ int first_column(const int (&kk)[kMaxChunks], int k, int x1, int x2) {
+    const int lane = lane_id();
+    int best = kKeyNone;
+#pragma unroll
+    for (int e = kMaxChunks - 1; e >= 0; --e) {
+        const int j = e * 64 + lane;
+        if (kk[e] == k && j != x1 && j != x2)
+            best = j;
+    }
+    return wave_min_key_s(best);
+}
+
 // One row's two-minimum by a full scan (reference order: first column on
 // ties, the (LARGE, -1) start slot of the second minimum, column 0 as the
 // first seed), from registers `pf` when they hold row fi, else loaded.  When
 // `refill` is set and the result is within LARGE, the row cache of fi is
-// refilled from the same scan.
+// refilled from the same scan.  Nothing goes through LDS: the columns of
+// the two (three) smallest come from wave minima over the column indices,
+// their costs from the owning lanes.
 __device__ void scan_row(LargeLds &L, const CostView &C, int fi, int E, int K,
-                         const float (&pf)[kMaxChunks], int pf_row, float *cbuf, bool refill,
+                         const float (&pf)[kMaxChunks], int pf_row, bool refill,
                          int &j1, int &j2, float &u1, float &u2) {
     const int lane = lane_id();
-    float cr[kMaxChunks];
-    if (pf_row == fi) {
+    f32x16 cr;
+    {
+        float c[kMaxChunks];
+        if (pf_row == fi) {
+#pragma unroll
+            for (int e = 0; e < kMaxChunks; ++e)
+                c[e] = fix_cost(C, pf[e], e * 64 + lane);
+        } else {
+            load_row(C, fi, c);
+        }
 #pragma unroll
         for (int e = 0; e < kMaxChunks; ++e)
-            cr[e] = fix_cost(C, pf[e], e * 64 + lane);
-    } else {
-        load_row(C, fi, cr);
+            cr[e] = c[e];
     }
     // reduced costs, lane-local two-minimum of keys
     int kk[kMaxChunks];
@@ -226,8 +258,6 @@ __device__ void scan_row(LargeLds &L, const CostView &C, int fi, int E, int K,
         kk[e] = kKeyNone;
         if (e < E && j < K) {
             const float r = cr[e] - L.v[j];
-            L.rbuf[j] = r;
-            cbuf[j] = cr[e];
             const int k = fkey(r);
             kk[e] = k;
             if (k < a) {
@@ -247,13 +277,21 @@ __device__ void scan_row(LargeLds &L, const CostView &C, int fi, int E, int K,
         k1 = uniform_i(p1);
         k2 = min(uniform_i(p2), bmin);
     }
-    lds_sync();
-    const float r0 = L.rbuf[0];
+    // a reduced cost c - v, recomputed from the cost held by its lane
+    auto reduced = [&](int j) { return chunk_value(cr, j >> 6, j & 63) - L.v[j]; };
+    const float r0 = reduced(0);
     j1 = -1;
     j2 = -1;
     if (!(r0 <= kLarge)) {
         // the reference seeds (v1, j1) with column 0; beyond LARGE that seed
         // changes the outcome: run its scan verbatim
+#pragma unroll
+        for (int e = 0; e < kMaxChunks; ++e) {
+            const int j = e * 64 + lane;
+            if (e < E && j < K)
+                L.rbuf[j] = cr[e] - L.v[j];
+        }
+        lds_sync();
         float w1 = r0, w2 = kLarge;
         int i1 = 0, i2 = -1;
         if (lane == 0) {
@@ -280,34 +318,19 @@ __device__ void scan_row(LargeLds &L, const CostView &C, int fi, int E, int K,
     }
     // first column (in index order) at k1; second: the next one at k1 if
     // k2 == k1, else the first at k2
-    int found = 0;
-#pragma unroll
-    for (int e = 0; e < kMaxChunks; ++e) {
-        if (found < 2) {
-            uint64_t m1 = ballot(kk[e] == k1);
-            if (found == 0 && m1) {
-                j1 = e * 64 + first_lane(m1);
-                m1 &= m1 - 1;
-                found = 1;
-            }
-            if (k2 == k1 && found == 1 && m1) {
-                j2 = e * 64 + first_lane(m1);
-                found = 2;
-            }
-        }
-    }
-    if (k2 != k1 && k2 != kKeyNone) {
-#pragma unroll
-        for (int e = 0; e < kMaxChunks; ++e) {
-            const uint64_t m2 = ballot(kk[e] == k2);
-            if (j2 < 0 && m2)
-                j2 = e * 64 + first_lane(m2);
-        }
-    }
-    u1 = L.rbuf[j1];
+    // (a key taken from the row always has a column; the guards keep an
+    // index in range regardless)
+    j1 = first_column(kk, k1, -1, -1);
+    if (j1 == kKeyNone)
+        j1 = 0;
+    if (k2 != kKeyNone)
+        j2 = first_column(kk, k2, j1, -1);
+    if (j2 == kKeyNone)
+        j2 = -1;
+    u1 = reduced(j1);
     u2 = kLarge;
     if (j2 >= 0) {
-        const float w = L.rbuf[j2];
+        const float w = reduced(j2);
         if (w < kLarge)
             u2 = w;
         else
@@ -335,24 +358,22 @@ __device__ void scan_row(LargeLds &L, const CostView &C, int fi, int E, int K,
     const int k4 = min(uniform_i(p4), uniform_i(wave_min_key(b3)));
     if (k3 == kKeyNone)
         return;
-    int j3 = -1;
-#pragma unroll
-    for (int e = 0; e < kMaxChunks; ++e) {
-        const int j = e * 64 + lane;
-        const uint64_t m3 = ballot(j != j1 && j != j2 && kk[e] == k3);
-        if (j3 < 0 && m3)
-            j3 = e * 64 + first_lane(m3);
-    }
+    const int j3 = first_column(kk, k3, j1, j2);
+    if (j3 == kKeyNone)
+        return;
     const int lo12 = min(j1, j2), hi12 = max(j1, j2);
     const int s0 = min(lo12, j3), s2 = max(hi12, j3);
     const int s1 = j1 + j2 + j3 - s0 - s2;
+    const float g0 = chunk_value(cr, s0 >> 6, s0 & 63);
+    const float g1 = chunk_value(cr, s1 >> 6, s1 & 63);
+    const float g2 = chunk_value(cr, s2 >> 6, s2 & 63);
     if (lane == 0) {
         L.cq[0][fi] = s0;
         L.cq[1][fi] = s1;
         L.cq[2][fi] = s2;
-        L.cg[0][fi] = cbuf[s0];
-        L.cg[1][fi] = cbuf[s1];
-        L.cg[2][fi] = cbuf[s2];
+        L.cg[0][fi] = g0;
+        L.cg[1][fi] = g1;
+        L.cg[2][fi] = g2;
         L.ctau[fi] = k4 == kKeyNone ? finf() : key_to_float(k4);
     }
 }
@@ -486,7 +507,6 @@ __device__ bool large_solve(const int K, const int E, LargeLds &L, const CostVie
         COMPACT ? compact_arr_guard(K) : 4u * (uint32_t)K * (uint32_t)K + 64u;
     for (int i = lane; i < K; i += 64)
         L.ctau[i] = -finf();
-    float *cbuf = reinterpret_cast<float *>(L.ev);  // row costs of the last scan
     lds_sync();
     // Rows >= N of the padded tile are all 0, so their reduced costs are -v:
     // one two-minimum serves every such row until a dual changes.
@@ -538,7 +558,7 @@ __device__ bool large_solve(const int K, const int E, LargeLds &L, const CostVie
                 }
             }
             if (!known)
-                scan_row(L, C, fi, E, K, pf, pf_row, cbuf, !pad_row, j1, j2, u1, u2);
+                scan_row(L, C, fi, E, K, pf, pf_row, !pad_row, j1, j2, u1, u2);
             if (pad_row && !pad_valid) {
                 pad_j1 = j1;
                 pad_j2 = j2;
@@ -623,6 +643,7 @@ __device__ bool large_solve(const int K, const int E, LargeLds &L, const CostVie
         }
         lds_sync();
         int lo = 0, hi = 0, n_ready = 0, final_j = -1;
+
         float group_level = 0.f;  // d of the current minimum group
         while (final_j < 0) {
             if (lo >= K)
