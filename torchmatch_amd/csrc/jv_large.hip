@@ -67,11 +67,12 @@ struct CostView {
 // Every lane loads every chunk (addresses clamped into the row, extra values
 // ignored by the callers), so the loads carry no branches and all of them are
 // in flight before any is used: a row costs one memory latency.
-__device__ __forceinline__ void load_row_raw(const CostView &C, int i, float (&raw)[kMaxChunks]) {
+template <int NC>
+__device__ __forceinline__ void load_row_raw(const CostView &C, int i, float (&raw)[NC]) {
     const int lane = lane_id();
     const float *src = C.src + (int64_t)i * C.M;
 #pragma unroll
-    for (int e = 0; e < kMaxChunks; ++e)
+    for (int e = 0; e < NC; ++e)
         raw[e] = src[min(e * 64 + lane, C.M - 1)];
 }
 
@@ -81,17 +82,18 @@ __device__ __forceinline__ float fix_cost(const CostView &C, float raw, int j) {
 }
 
 // Row i of the padded tile into registers (values for j >= K are unused).
-__device__ __forceinline__ void load_row(const CostView &C, int i, float (&cr)[kMaxChunks]) {
+template <int NC>
+__device__ __forceinline__ void load_row(const CostView &C, int i, float (&cr)[NC]) {
     const int lane = lane_id();
     if (i < C.N) {
-        float raw[kMaxChunks];
-        load_row_raw(C, i, raw);
+        float raw[NC];
+        load_row_raw<NC>(C, i, raw);
 #pragma unroll
-        for (int e = 0; e < kMaxChunks; ++e)
+        for (int e = 0; e < NC; ++e)
             cr[e] = fix_cost(C, raw[e], e * 64 + lane);
     } else {
 #pragma unroll
-        for (int e = 0; e < kMaxChunks; ++e)
+        for (int e = 0; e < NC; ++e)
             cr[e] = 0.f;
     }
 }
@@ -212,11 +214,12 @@ __device__ __forceinline__ float chunk_value(const f32x16 &v, int e, int l) {
 // Smallest column j = e * 64 + lane with key kk[e] == k, other than x1 and
 // x2 (uniform; kKeyNone if there is none).  One wave minimum over the
 // columns: the first column in index order, as the reference's scans take it.
-__device__ __forceinline__ int first_column(const int (&kk)[kMaxChunks], int k, int x1, int x2) {
+template <int NC>
+__device__ __forceinline__ int first_column(const int (&kk)[NC], int k, int x1, int x2) {
     const int lane = lane_id();
     int best = kKeyNone;
 #pragma unroll
-    for (int e = kMaxChunks - 1; e >= 0; --e) {
+    for (int e = NC - 1; e >= 0; --e) {
         const int j = e * 64 + lane;
         if (kk[e] == k && j != x1 && j != x2)
             best = j;
@@ -231,29 +234,30 @@ __device__ __forceinline__ int first_column(const int (&kk)[kMaxChunks], int k, 
 // refilled from the same scan.  Nothing goes through LDS: the columns of
 // the two (three) smallest come from wave minima over the column indices,
 // their costs from the owning lanes.
+template <int NC>
 __device__ void scan_row(LargeLds &L, const CostView &C, int fi, int E, int K,
-                         const float (&pf)[kMaxChunks], int pf_row, bool refill,
+                         const float (&pf)[NC], int pf_row, bool refill,
                          int &j1, int &j2, float &u1, float &u2) {
     const int lane = lane_id();
     f32x16 cr;
     {
-        float c[kMaxChunks];
+        float c[NC];
         if (pf_row == fi) {
 #pragma unroll
-            for (int e = 0; e < kMaxChunks; ++e)
+            for (int e = 0; e < NC; ++e)
                 c[e] = fix_cost(C, pf[e], e * 64 + lane);
         } else {
-            load_row(C, fi, c);
+            load_row<NC>(C, fi, c);
         }
 #pragma unroll
-        for (int e = 0; e < kMaxChunks; ++e)
+        for (int e = 0; e < NC; ++e)
             cr[e] = c[e];
     }
     // reduced costs, lane-local two-minimum of keys
-    int kk[kMaxChunks];
+    int kk[NC];
     int a = kKeyNone, bk = kKeyNone;
 #pragma unroll
-    for (int e = 0; e < kMaxChunks; ++e) {
+    for (int e = 0; e < NC; ++e) {
         const int j = e * 64 + lane;
         kk[e] = kKeyNone;
         if (e < E && j < K) {
@@ -286,7 +290,7 @@ __device__ void scan_row(LargeLds &L, const CostView &C, int fi, int E, int K,
         // the reference seeds (v1, j1) with column 0; beyond LARGE that seed
         // changes the outcome: run its scan verbatim
 #pragma unroll
-        for (int e = 0; e < kMaxChunks; ++e) {
+        for (int e = 0; e < NC; ++e) {
             const int j = e * 64 + lane;
             if (e < E && j < K)
                 L.rbuf[j] = cr[e] - L.v[j];
@@ -320,11 +324,11 @@ __device__ void scan_row(LargeLds &L, const CostView &C, int fi, int E, int K,
     // k2 == k1, else the first at k2
     // (a key taken from the row always has a column; the guards keep an
     // index in range regardless)
-    j1 = first_column(kk, k1, -1, -1);
+    j1 = first_column<NC>(kk, k1, -1, -1);
     if (j1 == kKeyNone)
         j1 = 0;
     if (k2 != kKeyNone)
-        j2 = first_column(kk, k2, j1, -1);
+        j2 = first_column<NC>(kk, k2, j1, -1);
     if (j2 == kKeyNone)
         j2 = -1;
     u1 = reduced(j1);
@@ -342,7 +346,7 @@ __device__ void scan_row(LargeLds &L, const CostView &C, int fi, int E, int K,
     // smallest value
     int a3 = kKeyNone, b3 = kKeyNone;
 #pragma unroll
-    for (int e = 0; e < kMaxChunks; ++e) {
+    for (int e = 0; e < NC; ++e) {
         const int j = e * 64 + lane;
         const int k = (j != j1 && j != j2) ? kk[e] : kKeyNone;
         if (k < a3) {
@@ -358,7 +362,7 @@ __device__ void scan_row(LargeLds &L, const CostView &C, int fi, int E, int K,
     const int k4 = min(uniform_i(p4), uniform_i(wave_min_key(b3)));
     if (k3 == kKeyNone)
         return;
-    const int j3 = first_column(kk, k3, j1, j2);
+    const int j3 = first_column<NC>(kk, k3, j1, j2);
     if (j3 == kKeyNone)
         return;
     const int lo12 = min(j1, j2), hi12 = max(j1, j2);
@@ -384,16 +388,16 @@ __device__ void scan_row(LargeLds &L, const CostView &C, int fi, int E, int K,
 // augmenting row reduction, the first unassigned column of a minimum group
 // ending a path, the dual update (v + d) - min and FLT_MAX as the transfer's
 // starting minimum.
-template <bool COMPACT>
+template <bool COMPACT, int NC>
 __device__ bool large_solve(const int K, const int E, LargeLds &L, const CostView &C) {
     const int lane = lane_id();
 
     // ---- column reduction (ccrrt_dense, jonker_dense_flat.h:124-176) ----
     {
-        float vmin[kMaxChunks];
-        int ymin[kMaxChunks];
+        float vmin[NC];
+        int ymin[NC];
 #pragma unroll
-        for (int e = 0; e < kMaxChunks; ++e) {
+        for (int e = 0; e < NC; ++e) {
             vmin[e] = kLarge;
             ymin[e] = 0;
         }
@@ -401,14 +405,14 @@ __device__ bool large_solve(const int K, const int E, LargeLds &L, const CostVie
         // four rows' loads in flight per pass; rows still fold in order
         constexpr int R = 4;
         for (int i = 0; i < rows_real; i += R) {
-            float c[R][kMaxChunks];
+            float c[R][NC];
 #pragma unroll
             for (int q = 0; q < R; ++q)
-                load_row_raw(C, min(i + q, rows_real - 1), c[q]);
+                load_row_raw<NC>(C, min(i + q, rows_real - 1), c[q]);
 #pragma unroll
             for (int q = 0; q < R; ++q)
 #pragma unroll
-                for (int e = 0; e < kMaxChunks; ++e) {
+                for (int e = 0; e < NC; ++e) {
                     const int j = e * 64 + lane;
                     const float cv = fix_cost(C, c[q][e], j);
                     if (i + q < rows_real && e < E && j < K && cv < vmin[e]) {
@@ -419,7 +423,7 @@ __device__ bool large_solve(const int K, const int E, LargeLds &L, const CostVie
         }
         // padding rows (all 0): the first one wins where 0 is a strict new minimum
 #pragma unroll
-        for (int e = 0; e < kMaxChunks; ++e) {
+        for (int e = 0; e < NC; ++e) {
             const int j = e * 64 + lane;
             if (e < E && j < K) {
                 if (rows_real < K && 0.f < vmin[e]) {
@@ -469,11 +473,11 @@ __device__ bool large_solve(const int K, const int E, LargeLds &L, const CostVie
             t &= t - 1;
             const int own = L.x[i];
             // mn = LARGE, then `if (c < mn) mn = c` over j != own in order
-            float cr[kMaxChunks];
-            load_row(C, i, cr);
+            float cr[NC];
+            load_row<NC>(C, i, cr);
             int best = kKeyNone;
 #pragma unroll
-            for (int e2 = 0; e2 < kMaxChunks; ++e2) {
+            for (int e2 = 0; e2 < NC; ++e2) {
                 const int j = e2 * 64 + lane;
                 if (e2 < E && j < K) {
                     const float r = j != own ? cr[e2] - L.v[j] : finf();
@@ -514,7 +518,7 @@ __device__ bool large_solve(const int K, const int E, LargeLds &L, const CostVie
     float pad_u1 = 0.f, pad_u2 = 0.f;
     bool pad_valid = false;
     // the next row's raw costs, loaded while the current step finishes
-    float pf[kMaxChunks];
+    float pf[NC];
     int pf_row = -1;
     for (int round = 0; n_free > 0 && round < 2; ++round) {
         uint32_t cur = 0, rr = 0;
@@ -558,7 +562,7 @@ __device__ bool large_solve(const int K, const int E, LargeLds &L, const CostVie
                 }
             }
             if (!known)
-                scan_row(L, C, fi, E, K, pf, pf_row, !pad_row, j1, j2, u1, u2);
+                scan_row<NC>(L, C, fi, E, K, pf, pf_row, !pad_row, j1, j2, u1, u2);
             if (pad_row && !pad_valid) {
                 pad_j1 = j1;
                 pad_j2 = j2;
@@ -583,7 +587,7 @@ __device__ bool large_solve(const int K, const int E, LargeLds &L, const CostVie
                                     ? i0
                                     : (cur < (uint32_t)n_free ? L.fr[cur] : -1);
                 if (nxt >= 0 && nxt < C.N && nxt != pf_row) {
-                    load_row_raw(C, nxt, pf);
+                    load_row_raw<NC>(C, nxt, pf);
                     pf_row = nxt;
                 }
             }
@@ -621,19 +625,19 @@ __device__ bool large_solve(const int K, const int E, LargeLds &L, const CostVie
 
     // ---- augmentation (ca_dense / find_path_dense, jonker_dense_flat.h:75-122,237-258) ----
     // the next path's start row is loaded while this path is searched
-    float nx[kMaxChunks];
+    float nx[NC];
     if (n_free > 0 && L.fr[0] < C.N)
-        load_row_raw(C, L.fr[0], nx);
+        load_row_raw<NC>(C, L.fr[0], nx);
     for (int f = 0; f < n_free; ++f) {
         const int start = L.fr[f];
-        float cr[kMaxChunks];
+        float cr[NC];
 #pragma unroll
-        for (int e = 0; e < kMaxChunks; ++e)
+        for (int e = 0; e < NC; ++e)
             cr[e] = start < C.N ? fix_cost(C, nx[e], e * 64 + lane) : 0.f;
         if (f + 1 < n_free && L.fr[f + 1] < C.N)
-            load_row_raw(C, L.fr[f + 1], nx);
+            load_row_raw<NC>(C, L.fr[f + 1], nx);
 #pragma unroll
-        for (int e = 0; e < kMaxChunks; ++e) {
+        for (int e = 0; e < NC; ++e) {
             const int j = e * 64 + lane;
             if (e < E && j < K) {
                 L.cols[j] = j;
@@ -752,10 +756,10 @@ __device__ bool large_solve(const int K, const int E, LargeLds &L, const CostVie
                 const int base0 = shi;
                 // gather row iq at column jq and at the columns of positions
                 // [shi, K), all loads in flight together
-                int jg[kMaxChunks];
-                float cg[kMaxChunks];
+                int jg[NC];
+                float cg[NC];
 #pragma unroll
-                for (int e = 0; e < kMaxChunks; ++e) {
+                for (int e = 0; e < NC; ++e) {
                     const int p = base0 + e * 64 + lane;
                     jg[e] = p < K ? L.cols[p] : 0;
                 }
@@ -764,20 +768,20 @@ __device__ bool large_solve(const int K, const int E, LargeLds &L, const CostVie
                     const float *srow = C.src + (int64_t)iq * C.M;
                     cq = srow[min(jq, C.M - 1)];
 #pragma unroll
-                    for (int e = 0; e < kMaxChunks; ++e)
+                    for (int e = 0; e < NC; ++e)
                         cg[e] = srow[min(jg[e], C.M - 1)];
                     cq = fix_cost(C, cq, jq);
 #pragma unroll
-                    for (int e = 0; e < kMaxChunks; ++e)
+                    for (int e = 0; e < NC; ++e)
                         cg[e] = fix_cost(C, cg[e], jg[e]);
                 } else {
 #pragma unroll
-                    for (int e = 0; e < kMaxChunks; ++e)
+                    for (int e = 0; e < NC; ++e)
                         cg[e] = 0.f;
                 }
                 const float hq = cq - L.v[jq] - level;
 #pragma unroll
-                for (int e = 0; e < kMaxChunks; ++e) {
+                for (int e = 0; e < NC; ++e) {
                     const int base = base0 + e * 64;
                     if (base >= K)
                         break;
@@ -849,7 +853,7 @@ __device__ bool large_solve(const int K, const int E, LargeLds &L, const CostVie
     return true;
 }
 
-template <bool COMPACT>
+template <bool COMPACT, int NC>
 __global__ void __launch_bounds__(64)
 jv_solve_large_kernel(const float *__restrict__ costs, int64_t B, int N, int M,
                       const JvStats *__restrict__ partial, int n_partial,
@@ -879,7 +883,7 @@ jv_solve_large_kernel(const float *__restrict__ costs, int64_t B, int N, int M,
     bool ok;
     if (!COMPACT || compact_wave_range(any_finite, mx, mn, (flags & kJvFlagPosInf) != 0,
                                        C.sentinel)) {
-        ok = large_solve<COMPACT>(K, E, L, C);
+        ok = large_solve<COMPACT, NC>(K, E, L, C);
     } else {
         // compact outside the wave path's range: the lane-serial transcription
         if (lane == 0) {
@@ -907,19 +911,40 @@ jv_solve_large_kernel(const float *__restrict__ costs, int64_t B, int N, int M,
 
 } // namespace
 
+namespace {
+// One instantiation per chunk count (64-column chunks per lane: K <= 128,
+// 256, 512, 768, 1024), so the per-lane loops run over the chunks a row has.
+template <bool COMPACT>
+int launch_large(const float *costs, int64_t B, int N, int M, const JvStats *partial,
+                 int n_partial, int64_t *out, uint32_t *status, hipStream_t stream) {
+    const int K = N > M ? N : M;
+    const int E = (K + 63) / 64;
+    auto go = [&](auto kernel) {
+        hipLaunchKernelGGL(kernel, dim3((unsigned)B), dim3(64), 0, stream, costs, B, N, M,
+                           partial, n_partial, out, status);
+        return hipGetLastError() == hipSuccess ? kTmOk : kTmErrLaunch;
+    };
+    if (E <= 2)
+        return go(jv_solve_large_kernel<COMPACT, 2>);
+    if (E <= 4)
+        return go(jv_solve_large_kernel<COMPACT, 4>);
+    if (E <= 8)
+        return go(jv_solve_large_kernel<COMPACT, 8>);
+    if (E <= 12)
+        return go(jv_solve_large_kernel<COMPACT, 12>);
+    return go(jv_solve_large_kernel<COMPACT, kMaxChunks>);
+}
+} // namespace
+
 int launch_jv_large(const float *costs, int64_t B, int N, int M, const JvStats *partial,
                     int n_partial, int64_t *out, uint32_t *status, hipStream_t stream) {
-    hipLaunchKernelGGL(jv_solve_large_kernel<false>, dim3((unsigned)B), dim3(64), 0, stream,
-                       costs, B, N, M, partial, n_partial, out, status);
-    return hipGetLastError() == hipSuccess ? kTmOk : kTmErrLaunch;
+    return launch_large<false>(costs, B, N, M, partial, n_partial, out, status, stream);
 }
 
 int launch_jv_compact_large(const float *costs, int64_t B, int N, int M,
                             const JvStats *partial, int n_partial, int64_t *out,
                             uint32_t *status, hipStream_t stream) {
-    hipLaunchKernelGGL(jv_solve_large_kernel<true>, dim3((unsigned)B), dim3(64), 0, stream,
-                       costs, B, N, M, partial, n_partial, out, status);
-    return hipGetLastError() == hipSuccess ? kTmOk : kTmErrLaunch;
+    return launch_large<true>(costs, B, N, M, partial, n_partial, out, status, stream);
 }
 
 int jv_large_max_k() { return kMaxLargeK; }
