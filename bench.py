@@ -59,6 +59,11 @@ JV_BYTES_PER_RELAXATION = 12
 # shortest-path searches, each needing one wave-wide argmin before the next
 # (oracle.jv.sap_batch_counted; tests/test_oracle_jv.py recomputes it).
 JV_C2_CRITICAL_STEPS = 314
+# C3 seed 0: the reference order's sequential steps on its slowest problem
+# (problem 16: 2,496 augmenting row reduction steps + 254 paths + 0 scanned
+# rows; oracle.jv.jv_dense_batch_steps, recomputed by tests/test_oracle_jv.py).
+# The K = 768 kernel replays that order, one step after another.
+JV_C3_CRITICAL_STEPS = 2750
 
 # HBM bytes per launch from rocprofv3 --pmc FETCH_SIZE (x2.00, the factor a
 # 256 MiB device copy calibrates) and WRITE_SIZE (x1.00), per dispatch; the
@@ -334,14 +339,30 @@ def bench_jv_c3(device, reps: int = 3) -> dict:
     B, N, M = cost.shape
     nbytes = B * N * M * 4 + B * N * 8
     gbs = nbytes / (ms * 1e-3) / 1e9
-    return {"config": {"workload": "jonker_dense_batch C3", "B": B, "N": N, "M": M},
-            "solves_per_s": B / (ms * 1e-3), "ms_per_batch": ms,
-            "cost_sha256": workloads.sha256(cost_cpu),
-            "roofline": {"bound": "hbm", "binding": False, "achieved": round(gbs, 3),
-                         "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                         "frac": round(gbs / HBM_PEAK_GBS, 6), "traffic": None,
-                         "note": "one wave per problem walks a dependency chain over an "
-                                 "L2 / Infinity-Cache resident tile; HBM is not binding"}}
+    res = {"config": {"workload": "jonker_dense_batch C3", "B": B, "N": N, "M": M},
+           "solves_per_s": B / (ms * 1e-3), "ms_per_batch": ms,
+           "cost_sha256": workloads.sha256(cost_cpu),
+           "roofline": {"bound": "hbm", "binding": False, "achieved": round(gbs, 3),
+                        "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                        "frac": round(gbs / HBM_PEAK_GBS, 6), "traffic": None,
+                        "note": "one wave per problem walks a dependency chain over an "
+                                "L2 / Infinity-Cache resident tile; HBM is not binding"}}
+    # The binding resource, as for C2: the slowest problem's sequential steps
+    # (the reference order the kernel replays), each at least one dependent
+    # wave-wide argmin, against the batch time.
+    chain = argmin_chain(device)
+    if chain:
+        floor_ms = JV_C3_CRITICAL_STEPS * chain["cycles_per_round"] / (chain["clock_ghz"] * 1e6)
+        res["latency_roofline"] = {
+            "bound": "latency", "binding": True, "achieved": round(ms, 3),
+            "floor": round(floor_ms, 3), "unit": "ms per batch",
+            "frac": round(floor_ms / ms, 4),
+            "critical_problem_steps": JV_C3_CRITICAL_STEPS,
+            "argmin_cycles": round(chain["cycles_per_round"], 1),
+            "clock_ghz": round(chain["clock_ghz"], 3),
+            "note": "floor = slowest problem's row-reduction steps + paths + scanned rows "
+                    "x one dependent wave-wide argmin; achieved = the op per batch"}
+    return res
 
 
 def bench_jv_compact(device, reps: int = 20) -> dict:

@@ -59,6 +59,8 @@ def oracle_lib() -> ctypes.CDLL:
     ]
     lib.jvo_dense_batch_counted.restype = ctypes.c_int
     lib.jvo_sap_batch_counted.argtypes = lib.jvo_dense_batch_counted.argtypes
+    lib.jvo_dense_batch_steps.argtypes = lib.jvo_dense_batch_counted.argtypes
+    lib.jvo_dense_batch_steps.restype = ctypes.c_int
     lib.jvo_sap_batch_counted.restype = ctypes.c_int
     lib.jvo_compact_batch.argtypes = lib.jvo_dense_batch.argtypes
     lib.jvo_compact_batch.restype = ctypes.c_int
@@ -138,6 +140,22 @@ def jv_dense_batch_counted(costs) -> tuple[np.ndarray, np.ndarray]:
     )
     _raise(rc)
     return out, counts[:b]
+
+
+def jv_dense_batch_steps(costs) -> tuple[np.ndarray, np.ndarray]:
+    """Single-threaded oracle run that also returns the reference order's
+    sequential steps per problem, (B, 3) int64: augmenting row reduction steps,
+    augmenting paths, rows scanned in the paths' searches."""
+    arr = _prep(costs)
+    b, n, m = arr.shape
+    out = np.empty((b, n), dtype=np.int64)
+    steps = np.zeros((max(b, 1), 3), dtype=np.int64)
+    rc = oracle_lib().jvo_dense_batch_steps(
+        arr.ctypes.data_as(_F32P), b, n, m, out.ctypes.data_as(_I64P),
+        steps.ctypes.data_as(_I64P),
+    )
+    _raise(rc)
+    return out, steps[:b]
 
 
 def sap_batch_counted(costs) -> tuple[np.ndarray, np.ndarray]:

@@ -55,6 +55,7 @@ typedef struct {
     int64_t relax;  /* reduced-cost evaluations c[i][j] - v[j] (all phases) */
     int64_t paths;  /* augmenting paths searched in the augmentation phase */
     int64_t scans;  /* rows scanned inside augmenting-path searches */
+    int64_t rr_steps; /* steps of the augmenting row reduction (both rounds) */
 } jvo_counts;
 
 /* Per-solve scratch, sized K (mirrors the thread-local vectors of
@@ -258,8 +259,10 @@ static int32_t jvo_row_reduction(uint32_t n, const float *c, uint32_t n_free,
                 j1 = (int32_t)j;
             }
         }
-        if (cnt)
+        if (cnt) {
             cnt->relax += n;
+            cnt->rr_steps += 1;
+        }
         int32_t i0 = y[j1];
         const float lowered = v[j1] - (u2 - u1);
         const int lowers = lowered < v[j1];
@@ -721,6 +724,26 @@ int jvo_dense_batch_counted(const float *costs, int64_t B, int32_t N, int32_t M,
         counts3[3 * b + 0] = cnt[b].relax;
         counts3[3 * b + 1] = cnt[b].paths;
         counts3[3 * b + 2] = cnt[b].scans;
+    }
+    free(cnt);
+    return rc;
+}
+
+/* The reference order's sequential steps per problem, single-threaded (3 int64
+ * per problem: augmenting row reduction steps, paths, rows scanned in the
+ * paths' searches).  A solver that follows the reference's order takes these
+ * steps one after another; their total on the slowest problem bounds a
+ * launch from below. */
+int jvo_dense_batch_steps(const float *costs, int64_t B, int32_t N, int32_t M, int64_t *out,
+                          int64_t *steps3) {
+    jvo_counts *cnt = (jvo_counts *)calloc((size_t)(B > 0 ? B : 1), sizeof(jvo_counts));
+    if (!cnt)
+        return JVO_ERR_ALLOC;
+    const int rc = jvo_batch_impl(costs, B, N, M, out, 1, cnt, jvo_square);
+    for (int64_t b = 0; b < B; ++b) {
+        steps3[3 * b + 0] = cnt[b].rr_steps;
+        steps3[3 * b + 1] = cnt[b].paths;
+        steps3[3 * b + 2] = cnt[b].scans;
     }
     free(cnt);
     return rc;

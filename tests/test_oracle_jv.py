@@ -172,6 +172,30 @@ def test_bench_critical_steps():
     assert int(counts[:, 0].sum()) < bench.JV_C2_RELAXATIONS
 
 
+def test_bench_c3_critical_steps():
+    """bench.py floors the C3 batch at its slowest problem's sequential steps
+    in the reference's order (augmenting row reduction steps + paths + rows
+    scanned in the paths), which the K = 768 kernel replays one after another.
+    The step counter is checked on hand cases first."""
+    import bench
+
+    # column reduction settles a strictly diagonal problem: no further step
+    eye = (1.0 - np.eye(5, dtype=np.float32))[None]
+    _, st = jv.jv_dense_batch_steps(eye)
+    assert st.tolist() == [[0, 0, 0]]
+    # by hand: columns 1 and 2 take their minimum rows 0 and 1 (column 1
+    # outranks column 0 for row 0); row 2 stays free and one row-reduction
+    # step gives it column 0 (reduced costs 0, 1, 2: no displacement)
+    crowd = np.array([[[0, 5, 6], [0, 7, 5], [0, 6, 7]]], dtype=np.float32)
+    out, st = jv.jv_dense_batch_steps(crowd)
+    assert st.tolist() == [[1, 0, 0]]
+    assert out.tolist() == [[1, 2, 0]]
+    c = workloads.jv_rect_masked().numpy()
+    out, st = jv.jv_dense_batch_steps(c)
+    np.testing.assert_array_equal(out, jv.jv_dense_batch(c))
+    assert int(st.sum(axis=1).max()) == bench.JV_C3_CRITICAL_STEPS
+
+
 def test_unpack_restatement_known_cases():
     """Hand-worked unpacks (ops.cpp:387-414): row order of matches, increasing
     unmatched rows / columns, -1 padding."""
