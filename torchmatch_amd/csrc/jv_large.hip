@@ -636,6 +636,46 @@ __device__ bool large_solve(const int K, const int E, LargeLds &L, const CostVie
             cr[e] = start < C.N ? fix_cost(C, nx[e], e * 64 + lane) : 0.f;
         if (f + 1 < n_free && L.fr[f + 1] < C.N)
             load_row_raw<NC>(C, L.fr[f + 1], nx);
+        // The first find_dense, decided from the row in registers: cols[] is
+        // the identity, so its tied block is, in column order, every column
+        // whose d = c - v has the row's minimum key (the column of the last
+        // new running minimum is the first of them, the ties after it the
+        // rest).  When one of them is unassigned the path is that single
+        // column -- dense takes the last such column, compact the first --
+        // and neither cols / d / pred nor the event list is needed.  (At 16
+        // chunks this block takes the kernel from 148 to 247 VGPRs with
+        // spills, so K > 768 keeps the general search alone.)
+        if constexpr (NC < kMaxChunks) {
+            int dk[NC];
+            int mk = kKeyNone;
+#pragma unroll
+            for (int e = 0; e < NC; ++e) {
+                const int j = e * 64 + lane;
+                dk[e] = (e < E && j < K) ? fkey(cr[e] - L.v[j]) : kKeyNone;
+                mk = min(mk, dk[e]);
+            }
+            mk = wave_min_key_s(mk);
+            int found = -1;
+#pragma unroll
+            for (int e = 0; e < NC; ++e) {
+                const int j = e * 64 + lane;
+                const uint64_t open = ballot(dk[e] == mk && L.y[min(j, K - 1)] < 0);
+                if (COMPACT) {
+                    if (open && found < 0)
+                        found = e * 64 + first_lane(open);
+                } else if (open) {
+                    found = e * 64 + last_lane(open);
+                }
+            }
+            if (found >= 0) {
+                if (lane == 0) {
+                    L.y[found] = start;
+                    L.x[start] = found;
+                }
+                lds_sync();
+                continue;
+            }
+        }
 #pragma unroll
         for (int e = 0; e < NC; ++e) {
             const int j = e * 64 + lane;
@@ -677,7 +717,7 @@ __device__ bool large_solve(const int K, const int E, LargeLds &L, const CostVie
                     const uint64_t rec = ballot(later && dk < before);
                     const uint64_t tie = ballot(later && dk == before);
                     const uint64_t evm = rec | tie;
-                    if (rec) {
+                    if (NC == kMaxChunks && rec) {
                         const int lr = last_lane(rec);
                         const uint64_t upto = lr == 63 ? ~0ull : ((2ull << lr) - 1);
                         last_rec = n_ev + __builtin_popcountll(evm & upto) - 1;
@@ -686,13 +726,13 @@ __device__ bool large_solve(const int K, const int E, LargeLds &L, const CostVie
                     carry = min(carry, readlane_i(incl, 63));
                 }
                 lds_sync();
-                if (lo == 0) {
-                    // First search of the path: cols[] is still the identity,
-                    // so without replaying the swaps the tied block is, in
-                    // order, the column of the last new minimum (column 0 if
-                    // none) followed by the ties recorded after it.  If one of
-                    // them is unassigned the path ends here and cols[] is
-                    // never read again (the next path resets it).
+                if (NC == kMaxChunks && lo == 0) {
+                    // First search at 16 chunks (the register decision above
+                    // is compiled out there), from the event list: the tied
+                    // block is, in order, the column of the last new minimum
+                    // (column 0 if none) followed by the ties recorded after
+                    // it.  If one of them is unassigned the path ends here and
+                    // cols[] is never read again (the next path resets it).
                     const int c_lo = last_rec >= 0 ? (L.ev[last_rec] & 0x7fffffff) : 0;
                     int found = -1;
                     if (COMPACT) {
