@@ -389,7 +389,7 @@ __device__ void scan_row(LargeLds &L, const CostView &C, int fi, int E, int K,
 // ending a path, the dual update (v + d) - min and FLT_MAX as the transfer's
 // starting minimum.
 template <bool COMPACT, int NC>
-__device__ bool large_solve(const int K, const int E, LargeLds &L, const CostView &C) {
+__device__ __forceinline__ bool large_solve(const int K, const int E, LargeLds &L, const CostView &C) {
     const int lane = lane_id();
 
     // ---- column reduction (ccrrt_dense, jonker_dense_flat.h:124-176) ----
@@ -642,10 +642,8 @@ __device__ bool large_solve(const int K, const int E, LargeLds &L, const CostVie
         // new running minimum is the first of them, the ties after it the
         // rest).  When one of them is unassigned the path is that single
         // column -- dense takes the last such column, compact the first --
-        // and neither cols / d / pred nor the event list is needed.  (At 16
-        // chunks this block takes the kernel from 148 to 247 VGPRs with
-        // spills, so K > 768 keeps the general search alone.)
-        if constexpr (NC < kMaxChunks) {
+        // and neither cols / d / pred nor the event list is needed.
+        {
             int dk[NC];
             int mk = kKeyNone;
 #pragma unroll
@@ -704,7 +702,6 @@ __device__ bool large_solve(const int K, const int E, LargeLds &L, const CostVie
                 };
                 int carry = kKeyNone;
                 int n_ev = 0;
-                int last_rec = -1;  // index in ev of the last new minimum
                 int dk_next = chunk_key(lo);
 #pragma unroll 1
                 for (int base = lo; base < K; base += 64) {
@@ -717,51 +714,10 @@ __device__ bool large_solve(const int K, const int E, LargeLds &L, const CostVie
                     const uint64_t rec = ballot(later && dk < before);
                     const uint64_t tie = ballot(later && dk == before);
                     const uint64_t evm = rec | tie;
-                    if (NC == kMaxChunks && rec) {
-                        const int lr = last_lane(rec);
-                        const uint64_t upto = lr == 63 ? ~0ull : ((2ull << lr) - 1);
-                        last_rec = n_ev + __builtin_popcountll(evm & upto) - 1;
-                    }
                     n_ev = append_events(L, n_ev, evm, base, 0x80000000u, rec);
                     carry = min(carry, readlane_i(incl, 63));
                 }
                 lds_sync();
-                if (NC == kMaxChunks && lo == 0) {
-                    // First search at 16 chunks (the register decision above
-                    // is compiled out there), from the event list: the tied
-                    // block is, in order, the column of the last new minimum
-                    // (column 0 if none) followed by the ties recorded after
-                    // it.  If one of them is unassigned the path ends here and
-                    // cols[] is never read again (the next path resets it).
-                    const int c_lo = last_rec >= 0 ? (L.ev[last_rec] & 0x7fffffff) : 0;
-                    int found = -1;
-                    if (COMPACT) {
-                        // the first unassigned column of the block ends the path
-                        if (L.y[c_lo] < 0)
-                            found = c_lo;
-                        for (int k0 = last_rec + 1; k0 < n_ev && found < 0; k0 += 64) {
-                            const int k = k0 + lane;
-                            const bool ok = k < n_ev && L.y[L.ev[min(k, n_ev - 1)]] < 0;
-                            const uint64_t open = ballot(ok);
-                            if (open)
-                                found = L.ev[k0 + first_lane(open)];
-                        }
-                    } else {
-                        for (int top = n_ev; top > last_rec + 1 && found < 0; top -= 64) {
-                            const int k = top - 64 + lane;
-                            const bool ok = k > last_rec && k < top && L.y[L.ev[max(k, 0)]] < 0;
-                            const uint64_t open = ballot(ok);
-                            if (open)
-                                found = L.ev[top - 64 + last_lane(open)];
-                        }
-                        if (found < 0 && L.y[c_lo] < 0)
-                            found = c_lo;
-                    }
-                    if (found >= 0) {
-                        final_j = found;
-                        break;
-                    }
-                }
                 hi = replay_find_events(L, n_ev, lo);
                 group_level = L.d[L.cols[lo]];
                 // dense: the LAST unassigned column of the tied block wins
