@@ -88,6 +88,16 @@ int32_t tm_jv_max_k(void);
 /* Device workspace tm_jv_dense_batch_f32 needs for a (B, N, M) batch. */
 size_t tm_jv_workspace_bytes(int64_t B, int32_t N, int32_t M);
 
+/* Workspace with which K = max(N, M) > 64 batches also take the prefill: the
+ * column reduction and every row's cache of the augmenting row reduction
+ * computed by many-wave launches before the solve, which then spends its
+ * sequential steps on the reference order alone (C3, 64 x 512 x 768: about
+ * 2.6 MB).  Equal to tm_jv_workspace_bytes for K <= 64.  Any workspace of
+ * at least tm_jv_workspace_bytes is accepted; the result is the same, bit
+ * for bit, with or without the prefill.  No counterpart in the reference:
+ * its CPU op keeps thread-local scratch (ops.cpp:246-251). */
+size_t tm_jv_workspace_bytes_prefill(int64_t B, int32_t N, int32_t M);
+
 /* Solve B independent (N, M) float32 assignment problems.
  *   costs      device, (B, N, M) contiguous; +inf marks a forbidden pair
  *   out        device, (B, N) int64: row -> column, -1 for rows matched into

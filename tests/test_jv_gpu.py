@@ -107,6 +107,45 @@ def test_large_k_vs_oracle(kind, device):
         np.testing.assert_array_equal(got, want, err_msg=f"{kind} {(6, n, m)}")
 
 
+def _c_abi_solve(lib, entry, c: np.ndarray, ws_bytes: int, device) -> np.ndarray:
+    b, n, m = c.shape
+    dc = torch.from_numpy(c).to(device)
+    out = torch.full((b, n), -7, dtype=torch.int64, device=device)
+    ws = torch.full((ws_bytes,), 0xA5, dtype=torch.uint8, device=device)  # stale contents
+    status = torch.zeros(2, dtype=torch.int32, device=device)
+    stream = torch.cuda.current_stream(device).cuda_stream
+    rc = entry(dc.data_ptr(), b, n, m, out.data_ptr(), ws.data_ptr(), ctypes.c_size_t(ws_bytes),
+               status.data_ptr(), stream)
+    assert rc == _native.TM_OK
+    assert lib.tm_jv_check_status(status.data_ptr(), stream) == _native.TM_OK
+    return out.cpu().numpy()
+
+
+@pytest.mark.parametrize("kind", ["uniform", "tied", "masked", "tied_masked"])
+def test_large_k_prefill_and_plain_workspace(kind, device):
+    """K > 64 with the prefill workspace (column minima and row caches from
+    many-wave launches) and with the minimum workspace (both in the solve's
+    one wave): the same mapping as the oracle, dense and compact, at every
+    chunk count, rectangular both ways."""
+    lib = _native.lib()
+    rng = np.random.default_rng(zlib.crc32(("prefill" + kind).encode()))
+    for n, m in [(65, 70), (130, 100), (100, 250), (300, 512), (512, 768), (768, 700),
+                 (1024, 900)]:
+        c = _random_batch(rng, kind, 4, n, m)
+        print(f"prefill kind {kind} shape {(4, n, m)}", flush=True)
+        small = lib.tm_jv_workspace_bytes(4, n, m)
+        full = lib.tm_jv_workspace_bytes_prefill(4, n, m)
+        assert full > small
+        want = jv.jv_dense_batch(c)
+        for ws_bytes in (small, full):
+            got = _c_abi_solve(lib, lib.tm_jv_dense_batch_f32, c, ws_bytes, device)
+            np.testing.assert_array_equal(got, want, err_msg=f"{kind} {(n, m)} ws {ws_bytes}")
+        want_c = jv.jv_compact_batch(c)
+        for ws_bytes in (small, full):
+            got = _c_abi_solve(lib, lib.tm_jv_compact_batch_f32, c, ws_bytes, device)
+            np.testing.assert_array_equal(got, want_c, err_msg=f"compact {kind} {(n, m)}")
+
+
 def test_c2_full_size_mapping_and_total_cost(device):
     cost = workloads.jv_uniform(1024, 64, 64, seed=0)
     want = jv.jv_dense_batch(cost.numpy())

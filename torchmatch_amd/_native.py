@@ -34,6 +34,10 @@ _VP = ctypes.c_void_p
 SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "tm_jv_max_k": (ctypes.c_int32, []),
     "tm_jv_workspace_bytes": (ctypes.c_size_t, [ctypes.c_int64, ctypes.c_int32, ctypes.c_int32]),
+    "tm_jv_workspace_bytes_prefill": (
+        ctypes.c_size_t,
+        [ctypes.c_int64, ctypes.c_int32, ctypes.c_int32],
+    ),
     "tm_jv_dense_batch_f32": (
         ctypes.c_int,
         [_VP, ctypes.c_int64, ctypes.c_int32, ctypes.c_int32, _VP, _VP, ctypes.c_size_t, _VP, _VP],

@@ -39,15 +39,19 @@ constexpr uint32_t kJvRecReplayed = 1u << 6;  // left the certified path for the
 constexpr uint32_t kJvRecGuard = 1u << 7;     // a solve hit its iteration guard
 
 // K in (64, jv_large_max_k()]: one workgroup per problem, cost read from
-// global memory (jv_large.hip).
+// global memory (jv_large.hip).  prep_ws: nullptr, or jv_large_prep_bytes of
+// device memory for the prefill (column minima and row caches built by
+// many-wave launches before the solve; the same result either way).
 int launch_jv_large(const float *costs, int64_t B, int N, int M, const JvStats *partial,
-                    int n_partial, int64_t *out, uint32_t *status, hipStream_t stream);
+                    int n_partial, void *prep_ws, int64_t *out, uint32_t *status,
+                    hipStream_t stream);
 int jv_large_max_k();
+size_t jv_large_prep_bytes(int64_t B, int N, int M);
 
 // Compact solver (assignment::jonker_compact_batch) for K in (64,
 // jv_compact_max_k()] (jv_large.hip).
 int launch_jv_compact_large(const float *costs, int64_t B, int N, int M,
-                            const JvStats *partial, int n_partial, int64_t *out,
+                            const JvStats *partial, int n_partial, void *prep_ws, int64_t *out,
                             uint32_t *status, hipStream_t stream);
 int jv_compact_max_k();
 

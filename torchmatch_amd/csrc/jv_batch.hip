@@ -1598,6 +1598,22 @@ extern "C" size_t tm_jv_workspace_bytes(int64_t B, int32_t N, int32_t M) {
 }
 
 namespace {
+// Offset of the large-K prefill in the workspace (after the statistics
+// records), or 0 when the shape has none.
+size_t prefill_offset(int64_t B, int32_t N, int32_t M) {
+    const int K = N > M ? N : M;
+    if (B <= 0 || N <= 0 || M <= 0 || K <= kTile || K > jv_large_max_k())
+        return 0;
+    return (tm_jv_workspace_bytes(B, N, M) + 255) / 256 * 256;
+}
+} // namespace
+
+extern "C" size_t tm_jv_workspace_bytes_prefill(int64_t B, int32_t N, int32_t M) {
+    const size_t off = prefill_offset(B, N, M);
+    return off == 0 ? tm_jv_workspace_bytes(B, N, M) : off + jv_large_prep_bytes(B, N, M);
+}
+
+namespace {
 // TORCHMATCH_AMD_JV_CERTIFY=0 switches the certified path off (every problem
 // then takes the exact replay of the reference's order).
 int certify_enabled() {
@@ -1653,11 +1669,17 @@ int jv_launch(const float *costs, int64_t B, int32_t N, int32_t M, int64_t *out,
                        costs, n, stats, d_status, replays);
     if (hipGetLastError() != hipSuccess)
         return kTmErrLaunch;
-    if (K > kTile)
-        return COMPACT ? launch_jv_compact_large(costs, B, N, M, stats, (int)blocks, out,
+    if (K > kTile) {
+        // the prefill when the workspace holds it (the same result without)
+        const size_t off = prefill_offset(B, N, M);
+        void *prep = (off != 0 && workspace_bytes >= tm_jv_workspace_bytes_prefill(B, N, M))
+                         ? static_cast<char *>(workspace) + off
+                         : nullptr;
+        return COMPACT ? launch_jv_compact_large(costs, B, N, M, stats, (int)blocks, prep, out,
                                                  d_status, stream)
-                       : launch_jv_large(costs, B, N, M, stats, (int)blocks, out, d_status,
-                                         stream);
+                       : launch_jv_large(costs, B, N, M, stats, (int)blocks, prep, out,
+                                         d_status, stream);
+    }
     hipLaunchKernelGGL((jv_solve_kernel<COMPACT, kJvStandalone>), dim3((unsigned)B), dim3(64), 0,
                        stream, costs, B, N, M, stats, (int)blocks, nullptr, out, d_status,
                        certify, replays, nullptr, 0u);

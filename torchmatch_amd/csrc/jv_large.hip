@@ -11,13 +11,14 @@
 // the cost is read from global memory (L2 / Infinity Cache) through a view
 // that pads virtually (rows >= N and columns >= M read 0) and maps +inf to
 // the batch sentinel -- the padded tile is never materialised.  Per-column
-// state (v, y, d, pred), per-row state (x), the free-row list and the cols[]
-// permutation live in LDS (about 36 KiB).  Lane l handles columns / positions
-// l, l + 64, l + 128, ... of every K-wide pass; passes that must respect the
-// reference's sequential order (first index on ties, the swaps of find_dense
-// and scan_dense) are resolved with per-chunk ballots in increasing index
-// order, and the swap sequence itself is replayed by lane 0 on cols[] -- swaps
-// are rare events, the K-wide relaxations around them are parallel.
+// state (v, y, d, pred), per-row state (x, the row cache), the free-row list
+// and the cols[] permutation live in LDS (about 108 KiB).  Lane l handles
+// columns / positions l, l + 64, l + 128, ... of every K-wide pass; passes
+// that must respect the reference's sequential order (first index on ties,
+// the swaps of find_dense and scan_dense) are resolved with per-chunk
+// ballots in increasing index order, and the swap sequence itself is
+// replayed by lane 0 on cols[] -- swaps are rare events, the K-wide
+// relaxations around them are parallel.
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdint.h>
@@ -32,6 +33,7 @@ namespace {
 
 constexpr int kMaxLargeK = 1024;
 constexpr int kMaxChunks = kMaxLargeK / 64;
+constexpr int kCacheSlots = 8;  // row-cache depth; one slot per lane of lanes 0..7
 
 struct LargeLds {
     float v[kMaxLargeK];
@@ -44,15 +46,18 @@ struct LargeLds {
     int32_t cols[kMaxLargeK];
     int32_t ev[kMaxLargeK];  // claims in the column reduction, swap events later
     int32_t emap[kMaxLargeK];  // position -> index in the current tie run, else -1
-    // Row cache of the augmenting row reduction: for row i, the three columns
-    // that were its smallest reduced costs when it was last scanned (ascending
-    // column order), their costs, and tau = the fourth smallest reduced cost
-    // of that scan (-inf: never scanned).  Duals only fall in that phase, so
-    // every other reduced cost of the row is still >= tau; when the second
-    // smallest cached value (with the current duals) is < tau, the two cached
-    // minima are the row's two minima, first column on ties.
-    int32_t cq[3][kMaxLargeK];
-    float cg[3][kMaxLargeK];
+    // Row cache of the augmenting row reduction: for row i, up to
+    // kCacheSlots columns that were its smallest reduced costs when it was
+    // filled (ascending column order, -1 = empty slot), their costs, and tau
+    // = the next smallest reduced cost of that fill (-inf: never filled).
+    // Duals only fall from the column reduction on, so every other reduced
+    // cost of the row is still >= tau; when the second smallest cached value
+    // (with the current duals) is < tau, the two cached minima are the row's
+    // two minima, first column on ties.  Filled with 8 columns for every row
+    // before the solve when the caller's workspace holds the prefill
+    // (jv_large_rowcache_kernel), and with 3 by the row scans.
+    alignas(16) int32_t cq[kMaxLargeK][kCacheSlots];  // 16-byte copies (copy_to_lds)
+    alignas(16) float cg[kMaxLargeK][kCacheSlots];
     float ctau[kMaxLargeK];
 };
 
@@ -209,6 +214,51 @@ typedef float f32x16 __attribute__((ext_vector_type(kMaxChunks)));
 // Lane l's value of chunk e (e, l uniform).
 __device__ __forceinline__ float chunk_value(const f32x16 &v, int e, int l) {
     return readlane_f(v[e], l);
+}
+
+// Smallest key of lanes 0..7, in each of those lanes: quad butterflies, then
+// the 8-lane mirror (the groups of eight never mix).
+__device__ __forceinline__ int min8_key(int key) {
+    int a = key;
+    a = min(a, dpp_full<kDppQuadXor1>(a));
+    a = min(a, dpp_full<kDppQuadXor2>(a));
+    return min(a, dpp_full<kDppRowHalfMirror>(a));
+}
+
+// One problem's share of the prefill (all null: none).  v / y: the column
+// reduction's minima and their rows (K each); cq / cg: kCacheSlots cache
+// columns and costs per real row (N x kCacheSlots), ctau: their tau (N).
+struct LargePrep {
+    const float *v;
+    const int32_t *y;
+    const int32_t *cq;
+    const float *cg;
+    const float *ctau;
+};
+
+// n dwords from global memory into LDS, eight 16-byte loads per lane in
+// flight (n % 4 == 0, both sides 16-byte aligned).
+__device__ __forceinline__ void copy_to_lds(void *dst, const void *src, int n) {
+    const int lane = lane_id();
+    const int n4 = n / 4;
+    if (n4 <= 0)
+        return;
+    int4 *d = static_cast<int4 *>(dst);
+    const int4 *q = static_cast<const int4 *>(src);
+    for (int base = 0; base < n4; base += 8 * 64) {
+        int4 t[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int k = base + u * 64 + lane;
+            t[u] = q[min(k, n4 - 1)];
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int k = base + u * 64 + lane;
+            if (k < n4)
+                d[k] = t[u];
+        }
+    }
 }
 
 // Smallest column j = e * 64 + lane with key kk[e] == k, other than x1 and
@@ -371,14 +421,191 @@ __device__ void scan_row(LargeLds &L, const CostView &C, int fi, int E, int K,
     const float g0 = chunk_value(cr, s0 >> 6, s0 & 63);
     const float g1 = chunk_value(cr, s1 >> 6, s1 & 63);
     const float g2 = chunk_value(cr, s2 >> 6, s2 & 63);
-    if (lane == 0) {
-        L.cq[0][fi] = s0;
-        L.cq[1][fi] = s1;
-        L.cq[2][fi] = s2;
-        L.cg[0][fi] = g0;
-        L.cg[1][fi] = g1;
-        L.cg[2][fi] = g2;
+    // slots 0..2 by column, the rest empty
+    if (lane < kCacheSlots) {
+        L.cq[fi][lane] = lane == 0 ? s0 : (lane == 1 ? s1 : (lane == 2 ? s2 : -1));
+        L.cg[fi][lane] = lane == 0 ? g0 : (lane == 1 ? g1 : g2);
+    }
+    if (lane == 0)
         L.ctau[fi] = k4 == kKeyNone ? finf() : key_to_float(k4);
+}
+
+// ---- prefill: the column reduction's minima and every row's cache -----------
+//
+// Both are many-wave passes over the batch, launched after the statistics
+// pass and before the solve when the caller's workspace holds them.  The
+// solve then starts its augmenting row reduction with every real row cached
+// at depth kCacheSlots: with the duals of the column reduction, which only
+// fall afterwards (the reduction transfer and the row reduction lower them),
+// so each cache stays valid.  C3's slowest problem: 745 of 2,496 steps scan
+// their row without it, 80 with it.
+
+constexpr int kColminCols = 128;   // columns per block
+constexpr int kColminGroups = 8;   // row groups per block: rows g, g + 8, ...
+constexpr int kColminRows = 8;     // rows in flight per thread
+
+// The sentinel of the batch from the statistics partials (one wave); false
+// when the batch holds NaN / -inf (the solve then writes -1 and nothing of
+// the prefill is read).
+__device__ __forceinline__ bool prep_sentinel(const JvStats *partial, int n_partial, int K,
+                                              float &sentinel) {
+    float mx, mn;
+    uint32_t flags;
+    fold_stats(partial, n_partial, mx, mn, flags);
+    sentinel = (flags & kJvFlagAnyFinite) ? (mx + 1.0f) * (float)(K + 1) : 1.0f;
+    return !(flags & (kJvFlagNan | kJvFlagNegInf));
+}
+
+// v[b][j] = the smallest cost of column j of the padded tile, starting from
+// LARGE with row 0 and taking a row only on a strictly smaller cost in row
+// order (jonker_dense_flat.h:124-140), y[b][j] = that row: each row group
+// folds its rows in order, the groups merge by (cost, row), then the padding
+// rows (all 0) win where 0 is strictly smaller.  Grid (B, ceil(K / 128)).
+__global__ void __launch_bounds__(kColminCols * kColminGroups)
+jv_large_colmin_kernel(const float *__restrict__ costs, int N, int M,
+                       const JvStats *__restrict__ partial, int n_partial,
+                       float *__restrict__ v_out, int32_t *__restrict__ y_out) {
+    const int K = N > M ? N : M;
+    const int64_t b = blockIdx.x;
+    const int col = (int)(threadIdx.x % kColminCols);
+    const int g = (int)(threadIdx.x / kColminCols);
+    const int j = (int)blockIdx.y * kColminCols + col;
+    float sentinel;
+    if (!prep_sentinel(partial, n_partial, K, sentinel))
+        return;  // uniform over the block
+    float vmin = kLarge;
+    int ymin = 0;
+    if (j < K) {
+        if (j >= M) {
+            // a padding column reads 0 in every real row: the group's first row
+            if (g < N && 0.f < vmin) {
+                vmin = 0.f;
+                ymin = g;
+            }
+        } else {
+            const float *src = costs + b * (int64_t)N * M + j;
+            for (int i = g; i < N; i += kColminGroups * kColminRows) {
+                float c[kColminRows];
+#pragma unroll
+                for (int u = 0; u < kColminRows; ++u) {
+                    const int r = min(i + u * kColminGroups, N - 1);
+                    c[u] = src[(int64_t)r * M];
+                }
+#pragma unroll
+                for (int u = 0; u < kColminRows; ++u) {
+                    const int r = i + u * kColminGroups;
+                    const float cv = isfinite(c[u]) ? c[u] : sentinel;
+                    if (r < N && cv < vmin) {
+                        vmin = cv;
+                        ymin = r;
+                    }
+                }
+            }
+        }
+    }
+    __shared__ float sv[kColminGroups][kColminCols];
+    __shared__ int sy[kColminGroups][kColminCols];
+    sv[g][col] = vmin;
+    sy[g][col] = ymin;
+    __syncthreads();
+    if (g != 0 || j >= K)
+        return;
+#pragma unroll
+    for (int q = 1; q < kColminGroups; ++q) {
+        const float w = sv[q][col];
+        const int r = sy[q][col];
+        if (w < vmin || (w == vmin && r < ymin)) {
+            vmin = w;
+            ymin = r;
+        }
+    }
+    if (N < K && 0.f < vmin) {
+        vmin = 0.f;
+        ymin = N;
+    }
+    v_out[b * K + j] = vmin;
+    y_out[b * K + j] = ymin;
+}
+
+// Row i < N of problem b: the kCacheSlots smallest reduced costs c - v
+// (v from jv_large_colmin_kernel), in order of (value, column) as the
+// reference's scans rank them, stored by ascending column with their costs,
+// and tau = the next smallest value.  One wave per row, four per block.
+template <int NC>
+__global__ void __launch_bounds__(256)
+jv_large_rowcache_kernel(const float *__restrict__ costs, int64_t B, int N, int M,
+                         const JvStats *__restrict__ partial, int n_partial,
+                         const float *__restrict__ v_in, int32_t *__restrict__ cq_out,
+                         float *__restrict__ cg_out, float *__restrict__ tau_out) {
+    const int K = N > M ? N : M;
+    const int E = (K + 63) / 64;
+    const int lane = lane_id();
+    CostView C;
+    C.N = N;
+    C.M = M;
+    if (!prep_sentinel(partial, n_partial, K, C.sentinel))
+        return;
+    const int64_t rows = B * (int64_t)N;
+    for (int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); row < rows;
+         row += (int64_t)gridDim.x * 4) {
+        const int64_t b = row / N;
+        const int i = (int)(row - b * N);
+        C.src = costs + b * (int64_t)N * M;
+        const float *vb = v_in + b * K;
+        float raw[NC], vv[NC];
+        load_row_raw<NC>(C, i, raw);
+#pragma unroll
+        for (int e = 0; e < NC; ++e)
+            vv[e] = vb[min(e * 64 + lane, K - 1)];
+        f32x16 cr;
+        int kk[NC];
+#pragma unroll
+        for (int e = 0; e < NC; ++e) {
+            const int j = e * 64 + lane;
+            const float c = fix_cost(C, raw[e], j);
+            cr[e] = c;
+            kk[e] = (e < E && j < K) ? fkey(c - vv[e]) : kKeyNone;
+        }
+        int my_col = -1;
+        float my_cost = 0.f;
+        int tau_key = kKeyNone;
+        for (int t = 0; t <= kCacheSlots; ++t) {
+            int lm = kKeyNone;
+#pragma unroll
+            for (int e = 0; e < NC; ++e)
+                lm = min(lm, kk[e]);
+            const int k = wave_min_key_s(lm);
+            if (t == kCacheSlots || k == kKeyNone) {
+                tau_key = k;
+                break;
+            }
+            const int j = first_column<NC>(kk, k, -1, -1);
+            if (j == kKeyNone)
+                break;  // not reached: k is a key of the row
+            const float c = chunk_value(cr, j >> 6, j & 63);
+            if (lane == t) {
+                my_col = j;
+                my_cost = c;
+            }
+#pragma unroll
+            for (int e = 0; e < NC; ++e)
+                if (e * 64 + lane == j)
+                    kk[e] = kKeyNone;
+        }
+        // slot = rank of the column among the chosen ones
+        int rank = 0;
+#pragma unroll
+        for (int q = 0; q < kCacheSlots; ++q) {
+            const int cq = readlane_i(my_col, q);
+            rank += (cq >= 0 && cq < my_col) ? 1 : 0;
+        }
+        if (lane < kCacheSlots) {
+            const int slot = my_col >= 0 ? rank : lane;
+            cq_out[row * kCacheSlots + slot] = my_col;
+            cg_out[row * kCacheSlots + slot] = my_cost;
+        }
+        if (lane == 0)
+            tau_out[row] = tau_key == kKeyNone ? finf() : key_to_float(tau_key);
     }
 }
 
@@ -389,11 +616,33 @@ __device__ void scan_row(LargeLds &L, const CostView &C, int fi, int E, int K,
 // ending a path, the dual update (v + d) - min and FLT_MAX as the transfer's
 // starting minimum.
 template <bool COMPACT, int NC>
-__device__ __forceinline__ bool large_solve(const int K, const int E, LargeLds &L, const CostView &C) {
+__device__ __forceinline__ bool large_solve(const int K, const int E, LargeLds &L, const CostView &C,
+                                            const LargePrep &P) {
     const int lane = lane_id();
 
     // ---- column reduction (ccrrt_dense, jonker_dense_flat.h:124-176) ----
-    {
+    if (P.v != nullptr) {
+        // the minima and their rows from the prefill (jv_large_colmin_kernel)
+        float pv[NC];
+        int py[NC];
+#pragma unroll
+        for (int e = 0; e < NC; ++e) {
+            const int j = min(e * 64 + lane, K - 1);
+            pv[e] = P.v[j];
+            py[e] = P.y[j];
+        }
+#pragma unroll
+        for (int e = 0; e < NC; ++e) {
+            const int j = e * 64 + lane;
+            if (e < E && j < K) {
+                L.v[j] = pv[e];
+                L.y[j] = py[e];
+                L.x[j] = -1;   // K rows == K columns
+                L.ev[j] = 0;   // claim counts
+                L.emap[j] = -1;
+            }
+        }
+    } else {
         float vmin[NC];
         int ymin[NC];
 #pragma unroll
@@ -509,8 +758,16 @@ __device__ __forceinline__ bool large_solve(const int K, const int E, LargeLds &
     // ---- augmenting row reduction (carr_dense, jonker_dense_flat.h:178-235) ----
     const uint32_t rr_limit =
         COMPACT ? compact_arr_guard(K) : 4u * (uint32_t)K * (uint32_t)K + 64u;
-    for (int i = lane; i < K; i += 64)
-        L.ctau[i] = -finf();
+    if (P.v != nullptr) {
+        // every real row's cache from the prefill (jv_large_rowcache_kernel)
+        copy_to_lds(&L.cq[0][0], P.cq, C.N * kCacheSlots);
+        copy_to_lds(&L.cg[0][0], P.cg, C.N * kCacheSlots);
+        for (int i = lane; i < K; i += 64)
+            L.ctau[i] = i < C.N ? P.ctau[i] : -finf();
+    } else {
+        for (int i = lane; i < K; i += 64)
+            L.ctau[i] = -finf();
+    }
     lds_sync();
     // Rows >= N of the padded tile are all 0, so their reduced costs are -v:
     // one two-minimum serves every such row until a dual changes.
@@ -542,22 +799,29 @@ __device__ __forceinline__ bool large_solve(const int K, const int E, LargeLds &
             } else if (!pad_row) {
                 const float tau = L.ctau[fi];
                 if (tau > -finf()) {
-                    const int q0 = L.cq[0][fi], q1 = L.cq[1][fi], q2 = L.cq[2][fi];
-                    const float r0 = L.cg[0][fi] - L.v[q0];
-                    const float r1 = L.cg[1][fi] - L.v[q1];
-                    const float r2 = L.cg[2][fi] - L.v[q2];
-                    const float t1 = fminf(fminf(r0, r1), r2);
-                    const float t2 = __builtin_amdgcn_fmed3f(r0, r1, r2);
-                    if (t2 < tau && t2 < kLarge) {
-                        // u2 < LARGE: the reference's (LARGE, -1) start slot
-                        // cannot win
-                        known = true;
-                        const bool e0 = r0 == t1, e1 = r1 == t1;
-                        j1 = e0 ? q0 : (e1 ? q1 : q2);
-                        j2 = e0 ? (r2 < r1 ? q2 : q1)
-                                : (e1 ? (r2 < r0 ? q2 : q0) : (r1 < r0 ? q1 : q0));
-                        u1 = t1;
-                        u2 = t2;
+                    // lane s < kCacheSlots holds slot s (columns ascending
+                    // with the slot): the first lane at a key is the first
+                    // column at that key
+                    const int q = L.cq[fi][lane & (kCacheSlots - 1)];
+                    const float g = L.cg[fi][lane & (kCacheSlots - 1)];
+                    const float r = g - L.v[max(q, 0)];
+                    const int key = (lane < kCacheSlots && q >= 0) ? fkey(r) : kKeyNone;
+                    const int k1 = readlane_i(min8_key(key), 0);
+                    const int l1 = first_lane(ballot(key == k1));
+                    const int key2 = lane == l1 ? kKeyNone : key;
+                    const int k2 = readlane_i(min8_key(key2), 0);
+                    if (k1 != kKeyNone && k2 != kKeyNone) {
+                        const int l2 = first_lane(ballot(key2 == k2));
+                        const float t2 = readlane_f(r, l2);
+                        if (t2 < tau && t2 < kLarge) {
+                            // u2 < LARGE: the reference's (LARGE, -1) start
+                            // slot cannot win
+                            known = true;
+                            j1 = readlane_i(q, l1);
+                            j2 = readlane_i(q, l2);
+                            u1 = readlane_f(r, l1);
+                            u2 = t2;
+                        }
                     }
                 }
             }
@@ -852,7 +1116,7 @@ __device__ __forceinline__ bool large_solve(const int K, const int E, LargeLds &
 template <bool COMPACT, int NC>
 __global__ void __launch_bounds__(64)
 jv_solve_large_kernel(const float *__restrict__ costs, int64_t B, int N, int M,
-                      const JvStats *__restrict__ partial, int n_partial,
+                      const JvStats *__restrict__ partial, int n_partial, LargePrep prep,
                       int64_t *__restrict__ out, uint32_t *__restrict__ status) {
     __shared__ LargeLds L;
     const int lane = lane_id();
@@ -879,7 +1143,15 @@ jv_solve_large_kernel(const float *__restrict__ costs, int64_t B, int N, int M,
     bool ok;
     if (!COMPACT || compact_wave_range(any_finite, mx, mn, (flags & kJvFlagPosInf) != 0,
                                        C.sentinel)) {
-        ok = large_solve<COMPACT, NC>(K, E, L, C);
+        LargePrep P{nullptr, nullptr, nullptr, nullptr, nullptr};
+        if (prep.v != nullptr) {
+            P.v = prep.v + b * K;
+            P.y = prep.y + b * K;
+            P.cq = prep.cq + b * N * kCacheSlots;
+            P.cg = prep.cg + b * N * kCacheSlots;
+            P.ctau = prep.ctau + b * N;
+        }
+        ok = large_solve<COMPACT, NC>(K, E, L, C, P);
     } else {
         // compact outside the wave path's range: the lane-serial transcription
         if (lane == 0) {
@@ -908,16 +1180,72 @@ jv_solve_large_kernel(const float *__restrict__ costs, int64_t B, int N, int M,
 } // namespace
 
 namespace {
+size_t align256(size_t n) { return (n + 255) / 256 * 256; }
+
+// The prefill's arrays in a workspace of jv_large_prep_bytes(B, N, M).
+struct PrepBuffers {
+    float *v;
+    int32_t *y;
+    int32_t *cq;
+    float *cg;
+    float *ctau;
+};
+
+PrepBuffers prep_buffers(void *ws, int64_t B, int N, int M) {
+    const int64_t K = N > M ? N : M;
+    char *p = static_cast<char *>(ws);
+    PrepBuffers r;
+    r.v = reinterpret_cast<float *>(p);
+    p += align256((size_t)(B * K) * 4);
+    r.y = reinterpret_cast<int32_t *>(p);
+    p += align256((size_t)(B * K) * 4);
+    r.cq = reinterpret_cast<int32_t *>(p);
+    p += align256((size_t)(B * N) * kCacheSlots * 4);
+    r.cg = reinterpret_cast<float *>(p);
+    p += align256((size_t)(B * N) * kCacheSlots * 4);
+    r.ctau = reinterpret_cast<float *>(p);
+    return r;
+}
+
 // One instantiation per chunk count (64-column chunks per lane: K <= 128,
 // 256, 512, 768, 1024), so the per-lane loops run over the chunks a row has.
+// With a prefill workspace the column minima and the row caches are built
+// by two many-wave launches first.
 template <bool COMPACT>
 int launch_large(const float *costs, int64_t B, int N, int M, const JvStats *partial,
-                 int n_partial, int64_t *out, uint32_t *status, hipStream_t stream) {
+                 int n_partial, void *prep_ws, int64_t *out, uint32_t *status,
+                 hipStream_t stream) {
     const int K = N > M ? N : M;
     const int E = (K + 63) / 64;
+    LargePrep prep{nullptr, nullptr, nullptr, nullptr, nullptr};
+    if (prep_ws != nullptr) {
+        const PrepBuffers pb = prep_buffers(prep_ws, B, N, M);
+        hipLaunchKernelGGL(jv_large_colmin_kernel,
+                           dim3((unsigned)B, (unsigned)((K + kColminCols - 1) / kColminCols)),
+                           dim3(kColminCols * kColminGroups), 0, stream, costs, N, M, partial,
+                           n_partial, pb.v, pb.y);
+        if (hipGetLastError() != hipSuccess)
+            return kTmErrLaunch;
+        const int64_t rows = B * (int64_t)N;
+        const int64_t want = (rows + 3) / 4;
+        const unsigned grid = (unsigned)(want < 65536 ? want : 65536);
+        auto fill = [&](auto kernel) {
+            hipLaunchKernelGGL(kernel, dim3(grid), dim3(256), 0, stream, costs, B, N, M, partial,
+                               n_partial, pb.v, pb.cq, pb.cg, pb.ctau);
+            return hipGetLastError() == hipSuccess;
+        };
+        const bool ok = E <= 2    ? fill(jv_large_rowcache_kernel<2>)
+                        : E <= 4  ? fill(jv_large_rowcache_kernel<4>)
+                        : E <= 8  ? fill(jv_large_rowcache_kernel<8>)
+                        : E <= 12 ? fill(jv_large_rowcache_kernel<12>)
+                                  : fill(jv_large_rowcache_kernel<kMaxChunks>);
+        if (!ok)
+            return kTmErrLaunch;
+        prep = LargePrep{pb.v, pb.y, pb.cq, pb.cg, pb.ctau};
+    }
     auto go = [&](auto kernel) {
         hipLaunchKernelGGL(kernel, dim3((unsigned)B), dim3(64), 0, stream, costs, B, N, M,
-                           partial, n_partial, out, status);
+                           partial, n_partial, prep, out, status);
         return hipGetLastError() == hipSuccess ? kTmOk : kTmErrLaunch;
     };
     if (E <= 2)
@@ -932,15 +1260,22 @@ int launch_large(const float *costs, int64_t B, int N, int M, const JvStats *par
 }
 } // namespace
 
+size_t jv_large_prep_bytes(int64_t B, int N, int M) {
+    const int64_t K = N > M ? N : M;
+    return 2 * align256((size_t)(B * K) * 4) + 2 * align256((size_t)(B * N) * kCacheSlots * 4) +
+           align256((size_t)(B * N) * 4);
+}
+
 int launch_jv_large(const float *costs, int64_t B, int N, int M, const JvStats *partial,
-                    int n_partial, int64_t *out, uint32_t *status, hipStream_t stream) {
-    return launch_large<false>(costs, B, N, M, partial, n_partial, out, status, stream);
+                    int n_partial, void *prep_ws, int64_t *out, uint32_t *status,
+                    hipStream_t stream) {
+    return launch_large<false>(costs, B, N, M, partial, n_partial, prep_ws, out, status, stream);
 }
 
 int launch_jv_compact_large(const float *costs, int64_t B, int N, int M,
-                            const JvStats *partial, int n_partial, int64_t *out,
+                            const JvStats *partial, int n_partial, void *prep_ws, int64_t *out,
                             uint32_t *status, hipStream_t stream) {
-    return launch_large<true>(costs, B, N, M, partial, n_partial, out, status, stream);
+    return launch_large<true>(costs, B, N, M, partial, n_partial, prep_ws, out, status, stream);
 }
 
 int jv_large_max_k() { return kMaxLargeK; }

@@ -96,7 +96,8 @@ at::Tensor jv_batch_hip(const at::Tensor &costs, JvSolver solver, int64_t max_k,
     // float64 input is solved in float32, as the reference device op does
     // (dispatch.cu:156).
     const at::Tensor cf = costs.scalar_type() == at::kFloat ? costs : costs.to(at::kFloat);
-    const size_t ws_bytes = tm_jv_workspace_bytes(B, (int32_t)N, (int32_t)M);
+    // K > 64: with room for the prefill (column reduction and row caches)
+    const size_t ws_bytes = tm_jv_workspace_bytes_prefill(B, (int32_t)N, (int32_t)M);
     auto ws = at::empty({(int64_t)ws_bytes}, costs.options().dtype(at::kByte));
     // launch, wait and status in one call (the library folds the batch's
     // status on the host as the solve publishes it)
