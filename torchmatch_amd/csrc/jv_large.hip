@@ -103,7 +103,16 @@ __device__ __forceinline__ void load_row(const CostView &C, int i, float (&cr)[N
     }
 }
 
-__device__ __forceinline__ void lds_sync() { __syncthreads(); }
+// The solve's workgroup is one wave (64 threads): its LDS operations execute
+// in issue order, so a sync between lanes only has to keep the compiler from
+// moving LDS accesses across it.  Wavefront-scope fences around the wave
+// barrier do that and emit no wait for outstanding LDS operations (a
+// workgroup fence, as in __syncthreads, waits for all of them).
+__device__ __forceinline__ void lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
 
 // A run of tie events: for i = 0 .. n-1 in order, swap cols[pos_i] with
 // cols[h0 + i] (pos_i = ev[k0 + i], strictly increasing, pos_i >= h0 + i).
@@ -237,7 +246,9 @@ struct LargePrep {
 };
 
 // n dwords from global memory into LDS, eight 16-byte loads per lane in
-// flight (n % 4 == 0, both sides 16-byte aligned).
+// flight (n % 4 == 0, both sides 16-byte aligned).  Loads and stores carry
+// no condition (lanes past the end copy the last 16 bytes again), so the
+// compiler cannot sink each load into a guarded store and wait for it alone.
 __device__ __forceinline__ void copy_to_lds(void *dst, const void *src, int n) {
     const int lane = lane_id();
     const int n4 = n / 4;
@@ -248,16 +259,11 @@ __device__ __forceinline__ void copy_to_lds(void *dst, const void *src, int n) {
     for (int base = 0; base < n4; base += 8 * 64) {
         int4 t[8];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
-            const int k = base + u * 64 + lane;
-            t[u] = q[min(k, n4 - 1)];
-        }
+        for (int u = 0; u < 8; ++u)
+            t[u] = q[min(base + u * 64 + lane, n4 - 1)];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
-            const int k = base + u * 64 + lane;
-            if (k < n4)
-                d[k] = t[u];
-        }
+        for (int u = 0; u < 8; ++u)
+            d[min(base + u * 64 + lane, n4 - 1)] = t[u];
     }
 }
 
@@ -279,26 +285,18 @@ __device__ __forceinline__ int first_column(const int (&kk)[NC], int k, int x1, 
 
 // One row's two-minimum by a full scan (reference order: first column on
 // ties, the (LARGE, -1) start slot of the second minimum, column 0 as the
-// first seed), from registers `pf` when they hold row fi, else loaded.  When
-// `refill` is set and the result is within LARGE, the row cache of fi is
-// refilled from the same scan.  Nothing goes through LDS: the columns of
-// the two (three) smallest come from wave minima over the column indices,
-// their costs from the owning lanes.
+// first seed).  When `refill` is set and the result is within LARGE, the row
+// cache of fi is refilled from the same scan.  Nothing goes through LDS: the
+// columns of the two (three) smallest come from wave minima over the column
+// indices, their costs from the owning lanes.
 template <int NC>
 __device__ void scan_row(LargeLds &L, const CostView &C, int fi, int E, int K,
-                         const float (&pf)[NC], int pf_row, bool refill,
-                         int &j1, int &j2, float &u1, float &u2) {
+                         bool refill, int &j1, int &j2, float &u1, float &u2) {
     const int lane = lane_id();
     f32x16 cr;
     {
         float c[NC];
-        if (pf_row == fi) {
-#pragma unroll
-            for (int e = 0; e < NC; ++e)
-                c[e] = fix_cost(C, pf[e], e * 64 + lane);
-        } else {
-            load_row<NC>(C, fi, c);
-        }
+        load_row<NC>(C, fi, c);
 #pragma unroll
         for (int e = 0; e < NC; ++e)
             cr[e] = c[e];
@@ -633,14 +631,12 @@ __device__ __forceinline__ bool large_solve(const int K, const int E, LargeLds &
         }
 #pragma unroll
         for (int e = 0; e < NC; ++e) {
-            const int j = e * 64 + lane;
-            if (e < E && j < K) {
-                L.v[j] = pv[e];
-                L.y[j] = py[e];
-                L.x[j] = -1;   // K rows == K columns
-                L.ev[j] = 0;   // claim counts
-                L.emap[j] = -1;
-            }
+            const int j = min(e * 64 + lane, K - 1);  // past K: column K-1 again
+            L.v[j] = pv[e];
+            L.y[j] = py[e];
+            L.x[j] = -1;   // K rows == K columns
+            L.ev[j] = 0;   // claim counts
+            L.emap[j] = -1;
         }
     } else {
         float vmin[NC];
@@ -762,8 +758,15 @@ __device__ __forceinline__ bool large_solve(const int K, const int E, LargeLds &
         // every real row's cache from the prefill (jv_large_rowcache_kernel)
         copy_to_lds(&L.cq[0][0], P.cq, C.N * kCacheSlots);
         copy_to_lds(&L.cg[0][0], P.cg, C.N * kCacheSlots);
-        for (int i = lane; i < K; i += 64)
-            L.ctau[i] = i < C.N ? P.ctau[i] : -finf();
+        float t[NC];
+#pragma unroll
+        for (int e = 0; e < NC; ++e)
+            t[e] = P.ctau[min(e * 64 + lane, C.N - 1)];
+#pragma unroll
+        for (int e = 0; e < NC; ++e) {
+            const int i = min(e * 64 + lane, K - 1);
+            L.ctau[i] = i < C.N ? t[e] : -finf();
+        }
     } else {
         for (int i = lane; i < K; i += 64)
             L.ctau[i] = -finf();
@@ -774,9 +777,9 @@ __device__ __forceinline__ bool large_solve(const int K, const int E, LargeLds &
     int pad_j1 = -1, pad_j2 = -1;
     float pad_u1 = 0.f, pad_u2 = 0.f;
     bool pad_valid = false;
-    // the next row's raw costs, loaded while the current step finishes
-    float pf[NC];
-    int pf_row = -1;
+    // No prefetch of the next step's row: with the prefilled caches few steps
+    // scan a row, and a row load in flight across the step's end made the
+    // compiler wait for it at every step (C3 2.64 against 2.27 ms).
     for (int round = 0; n_free > 0 && round < 2; ++round) {
         uint32_t cur = 0, rr = 0;
         int still = 0;
@@ -826,7 +829,7 @@ __device__ __forceinline__ bool large_solve(const int K, const int E, LargeLds &
                 }
             }
             if (!known)
-                scan_row<NC>(L, C, fi, E, K, pf, pf_row, !pad_row, j1, j2, u1, u2);
+                scan_row<NC>(L, C, fi, E, K, !pad_row, j1, j2, u1, u2);
             if (pad_row && !pad_valid) {
                 pad_j1 = j1;
                 pad_j2 = j2;
@@ -843,17 +846,6 @@ __device__ __forceinline__ bool large_solve(const int K, const int E, LargeLds &
             if (cap && !lowers && i0 >= 0 && j2 >= 0) {
                 jsel = j2;
                 i0 = L.y[j2];
-            }
-            // the row the next step takes: the displaced owner when it goes
-            // back to the front, else the next queued row; load it now
-            {
-                const int nxt = (cap && lowers && i0 >= 0)
-                                    ? i0
-                                    : (cur < (uint32_t)n_free ? L.fr[cur] : -1);
-                if (nxt >= 0 && nxt < C.N && nxt != pf_row) {
-                    load_row_raw<NC>(C, nxt, pf);
-                    pf_row = nxt;
-                }
             }
             lds_sync();
             if (cap) {
