@@ -331,7 +331,7 @@ __device__ void scan_row(LargeLds &L, const CostView &C, int fi, int E, int K,
     }
     // a reduced cost c - v, recomputed from the cost held by its lane
     auto reduced = [&](int j) { return chunk_value(cr, j >> 6, j & 63) - L.v[j]; };
-    const float r0 = reduced(0);
+    const float r0 = uniform_f(reduced(0));
     j1 = -1;
     j2 = -1;
     if (!(r0 <= kLarge)) {
@@ -379,10 +379,10 @@ __device__ void scan_row(LargeLds &L, const CostView &C, int fi, int E, int K,
         j2 = first_column<NC>(kk, k2, j1, -1);
     if (j2 == kKeyNone)
         j2 = -1;
-    u1 = reduced(j1);
+    u1 = uniform_f(reduced(j1));
     u2 = kLarge;
     if (j2 >= 0) {
-        const float w = reduced(j2);
+        const float w = uniform_f(reduced(j2));
         if (w < kLarge)
             u2 = w;
         else
@@ -787,7 +787,9 @@ __device__ __forceinline__ bool large_solve(const int K, const int E, LargeLds &
             ++rr;
             if (rr > rr_limit)
                 return false;
-            const int fi = L.fr[cur];
+            // LDS words every lane reads alike are made uniform explicitly, so
+            // that the step's branches are scalar (no exec-mask bookkeeping)
+            const int fi = uniform_i(L.fr[cur]);
             ++cur;
             const bool pad_row = fi >= C.N;
             int j1 = -1, j2 = -1;
@@ -800,7 +802,7 @@ __device__ __forceinline__ bool large_solve(const int K, const int E, LargeLds &
                 u2 = pad_u2;
                 known = true;
             } else if (!pad_row) {
-                const float tau = L.ctau[fi];
+                const float tau = uniform_f(L.ctau[fi]);
                 if (tau > -finf()) {
                     // lane s < kCacheSlots holds slot s (columns ascending
                     // with the slot): the first lane at a key is the first
@@ -838,14 +840,14 @@ __device__ __forceinline__ bool large_solve(const int K, const int E, LargeLds &
                 pad_valid = true;
             }
             int jsel = j1;
-            int i0 = L.y[j1];
-            const float vj1 = L.v[j1];
+            int i0 = uniform_i(L.y[j1]);
+            const float vj1 = uniform_f(L.v[j1]);
             const float lowered = vj1 - (u2 - u1);
             const bool lowers = lowered < vj1;
             const bool cap = COMPACT || rr < cur * (uint32_t)K;
             if (cap && !lowers && i0 >= 0 && j2 >= 0) {
                 jsel = j2;
-                i0 = L.y[j2];
+                i0 = uniform_i(L.y[j2]);
             }
             lds_sync();
             if (cap) {
@@ -885,7 +887,7 @@ __device__ __forceinline__ bool large_solve(const int K, const int E, LargeLds &
     if (n_free > 0 && L.fr[0] < C.N)
         load_row_raw<NC>(C, L.fr[0], nx);
     for (int f = 0; f < n_free; ++f) {
-        const int start = L.fr[f];
+        const int start = uniform_i(L.fr[f]);
         float cr[NC];
 #pragma unroll
         for (int e = 0; e < NC; ++e)
