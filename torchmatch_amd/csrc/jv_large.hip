@@ -301,15 +301,21 @@ __device__ void scan_row(LargeLds &L, const CostView &C, int fi, int E, int K,
         for (int e = 0; e < NC; ++e)
             cr[e] = c[e];
     }
-    // reduced costs, lane-local two-minimum of keys
+    // reduced costs, lane-local two-minimum of keys (the duals are read
+    // outside the guard, all in flight together: a read inside it would be
+    // waited for chunk by chunk)
     int kk[NC];
+    float vv[NC];
+#pragma unroll
+    for (int e = 0; e < NC; ++e)
+        vv[e] = L.v[min(e * 64 + lane, K - 1)];
     int a = kKeyNone, bk = kKeyNone;
 #pragma unroll
     for (int e = 0; e < NC; ++e) {
         const int j = e * 64 + lane;
         kk[e] = kKeyNone;
         if (e < E && j < K) {
-            const float r = cr[e] - L.v[j];
+            const float r = cr[e] - vv[e];
             const int k = fkey(r);
             kk[e] = k;
             if (k < a) {
@@ -721,11 +727,15 @@ __device__ __forceinline__ bool large_solve(const int K, const int E, LargeLds &
             float cr[NC];
             load_row<NC>(C, i, cr);
             int best = kKeyNone;
+            float vv[NC];
+#pragma unroll
+            for (int e2 = 0; e2 < NC; ++e2)
+                vv[e2] = L.v[min(e2 * 64 + lane, K - 1)];
 #pragma unroll
             for (int e2 = 0; e2 < NC; ++e2) {
                 const int j = e2 * 64 + lane;
                 if (e2 < E && j < K) {
-                    const float r = j != own ? cr[e2] - L.v[j] : finf();
+                    const float r = j != own ? cr[e2] - vv[e2] : finf();
                     L.rbuf[j] = r;
                     if (j != own)
                         best = min(best, fkey(r));
@@ -902,20 +912,26 @@ __device__ __forceinline__ bool large_solve(const int K, const int E, LargeLds &
         // column -- dense takes the last such column, compact the first --
         // and neither cols / d / pred nor the event list is needed.
         {
-            int dk[NC];
+            // duals and owners read outside any guard, all in flight together
+            int dk[NC], yv[NC];
+            float vv[NC];
+#pragma unroll
+            for (int e = 0; e < NC; ++e) {
+                vv[e] = L.v[min(e * 64 + lane, K - 1)];
+                yv[e] = L.y[min(e * 64 + lane, K - 1)];
+            }
             int mk = kKeyNone;
 #pragma unroll
             for (int e = 0; e < NC; ++e) {
                 const int j = e * 64 + lane;
-                dk[e] = (e < E && j < K) ? fkey(cr[e] - L.v[j]) : kKeyNone;
+                dk[e] = (e < E && j < K) ? fkey(cr[e] - vv[e]) : kKeyNone;
                 mk = min(mk, dk[e]);
             }
             mk = wave_min_key_s(mk);
             int found = -1;
 #pragma unroll
             for (int e = 0; e < NC; ++e) {
-                const int j = e * 64 + lane;
-                const uint64_t open = ballot(dk[e] == mk && L.y[min(j, K - 1)] < 0);
+                const uint64_t open = ballot((dk[e] == mk) & (yv[e] < 0));
                 if (COMPACT) {
                     if (open && found < 0)
                         found = e * 64 + first_lane(open);
@@ -932,12 +948,16 @@ __device__ __forceinline__ bool large_solve(const int K, const int E, LargeLds &
                 continue;
             }
         }
+        float vv[NC];  // read outside the guard, all in flight together
+#pragma unroll
+        for (int e = 0; e < NC; ++e)
+            vv[e] = L.v[min(e * 64 + lane, K - 1)];
 #pragma unroll
         for (int e = 0; e < NC; ++e) {
             const int j = e * 64 + lane;
             if (e < E && j < K) {
                 L.cols[j] = j;
-                L.d[j] = cr[e] - L.v[j];
+                L.d[j] = cr[e] - vv[e];
                 L.pred[j] = start;
             }
         }
@@ -1015,7 +1035,8 @@ __device__ __forceinline__ bool large_solve(const int K, const int E, LargeLds &
 #pragma unroll
                 for (int e = 0; e < NC; ++e) {
                     const int p = base0 + e * 64 + lane;
-                    jg[e] = p < K ? L.cols[p] : 0;
+                    const int cp = L.cols[min(p, K - 1)];  // outside the guard
+                    jg[e] = p < K ? cp : 0;
                 }
                 float cq = 0.f;
                 if (iq < C.N) {
@@ -1040,17 +1061,15 @@ __device__ __forceinline__ bool large_solve(const int K, const int E, LargeLds &
                     if (base >= K)
                         break;
                     const int p = base + lane;
-                    int jp = 0;
-                    float r = 0.f, dp = 0.f;
-                    bool better = false;
-                    if (p < K) {
-                        jp = jg[e];
-                        r = cg[e] - L.v[jp] - hq;
-                        dp = L.d[jp];
-                        better = r < dp;
-                    }
+                    // jg[e] is a column for every lane (0 past K)
+                    const int jp = p < K ? jg[e] : 0;
+                    const float vj = L.v[jp], dj = L.d[jp];
+                    const int yj = L.y[jp];
+                    const float r = p < K ? cg[e] - vj - hq : 0.f;
+                    const float dp = p < K ? dj : 0.f;
+                    const bool better = p < K && r < dp;
                     const bool tie = better && r == level;
-                    const uint64_t ret = ballot(tie && L.y[jp] < 0);
+                    const uint64_t ret = ballot(tie & (yj < 0));
                     if (ret) {
                         const int kk = first_lane(ret);
                         // compact stops before relaxing column kk itself
