@@ -37,6 +37,10 @@ def test_workspace_queries():
     lib = _native.lib()
     assert lib.tm_jv_max_k() >= 64
     assert lib.tm_jv_workspace_bytes(1024, 64, 64) >= 256
+    # the prefill size: equal for K <= 64, larger for K > 64 (C3: ~2.6 MB)
+    assert lib.tm_jv_workspace_bytes_prefill(1024, 64, 64) == lib.tm_jv_workspace_bytes(1024, 64, 64)
+    c3 = lib.tm_jv_workspace_bytes_prefill(64, 512, 768)
+    assert lib.tm_jv_workspace_bytes(64, 512, 768) < c3 < 3 << 20
     small = lib.tm_sinkhorn_workspace_bytes(2, 8, 8)
     big = lib.tm_sinkhorn_workspace_bytes(16, 2048, 2048)
     assert big > 16 * 2048 * 2048 * 4 > small
@@ -79,6 +83,22 @@ def test_schemas_match_reference():
         "Tensor b, Tensor? mask=None, float? scaling=None, Tensor? cost_aa=None, "
         "Tensor? cost_bb=None) -> Tensor"
     )
+
+
+def test_ops_modules_are_the_registered_ops():
+    """The reference's import paths for the op handles
+    (assignment/ops.py:17-28, transport/matrix/ops.py:8-10) resolve to the
+    ops this package registers, under the reference's names."""
+    from torchmatch_amd.assignment import ops as aops
+    from torchmatch_amd.transport.matrix import ops as tops
+
+    assert sorted(aops.__all__) == ["jonker_compact_batch", "jonker_compact_batch_unpacked",
+                                    "jonker_dense_batch", "jonker_dense_batch_unpacked"]
+    for name in aops.__all__:
+        assert getattr(aops, name) is getattr(torch.ops.assignment, name)
+    assert sorted(tops.__all__) == ["log_sinkhorn", "sinkhorn_divergence", "unbalanced_sinkhorn"]
+    for name in tops.__all__:
+        assert getattr(tops, name) is getattr(torch.ops.transport, name)
 
 
 def test_no_host_fallback():
