@@ -234,6 +234,17 @@ __device__ __forceinline__ int min8_key(int key) {
     return min(a, dpp_full<kDppRowHalfMirror>(a));
 }
 
+// Smallest and second smallest key (as a multiset) of lanes 0..7, in each
+// of those lanes: three pair-merge butterfly stages.
+__device__ __forceinline__ void min2_8_key(int key, int &k1, int &k2) {
+    int a = key, b = kKeyNone;
+    pair_merge(a, b, dpp_full<kDppQuadXor1>(a), dpp_full<kDppQuadXor1>(b));
+    pair_merge(a, b, dpp_full<kDppQuadXor2>(a), dpp_full<kDppQuadXor2>(b));
+    pair_merge(a, b, dpp_full<kDppRowHalfMirror>(a), dpp_full<kDppRowHalfMirror>(b));
+    k1 = a;
+    k2 = b;
+}
+
 // One problem's share of the prefill (all null: none).  v / y: the column
 // reduction's minima and their rows (K each); cq / cg: kCacheSlots cache
 // columns and costs per real row (N x kCacheSlots), ctau: their tau (N).
@@ -430,8 +441,7 @@ __device__ void scan_row(LargeLds &L, const CostView &C, int fi, int E, int K,
         L.cq[fi][lane] = lane == 0 ? s0 : (lane == 1 ? s1 : (lane == 2 ? s2 : -1));
         L.cg[fi][lane] = lane == 0 ? g0 : (lane == 1 ? g1 : g2);
     }
-    if (lane == 0)
-        L.ctau[fi] = k4 == kKeyNone ? finf() : key_to_float(k4);
+    L.ctau[fi] = k4 == kKeyNone ? finf() : key_to_float(k4);  // every lane, the same word
 }
 
 // ---- prefill: the column reduction's minima and every row's cache -----------
@@ -583,18 +593,31 @@ jv_large_rowcache_kernel(const float *__restrict__ costs, int64_t B, int N, int 
                 tau_key = k;
                 break;
             }
-            const int j = first_column<NC>(kk, k, -1, -1);
-            if (j == kKeyNone)
+            // the first column at k: the first chunk holding k, its first
+            // lane (chunk index uniform, so the chunks after it branch past
+            // their compare)
+            int ef = -1, lf = 0;
+#pragma unroll
+            for (int e = 0; e < NC; ++e) {
+                if (ef < 0) {
+                    const uint64_t m = ballot(kk[e] == k);
+                    if (m) {
+                        ef = e;
+                        lf = first_lane(m);
+                    }
+                }
+            }
+            if (ef < 0)
                 break;  // not reached: k is a key of the row
-            const float c = chunk_value(cr, j >> 6, j & 63);
+            const float c = chunk_value(cr, ef, lf);
             if (lane == t) {
-                my_col = j;
+                my_col = ef * 64 + lf;
                 my_cost = c;
             }
 #pragma unroll
             for (int e = 0; e < NC; ++e)
-                if (e * 64 + lane == j)
-                    kk[e] = kKeyNone;
+                if (e == ef)
+                    kk[e] = lane == lf ? kKeyNone : kk[e];
         }
         // slot = rank of the column among the chosen ones
         int rank = 0;
@@ -821,12 +844,13 @@ __device__ __forceinline__ bool large_solve(const int K, const int E, LargeLds &
                     const float g = L.cg[fi][lane & (kCacheSlots - 1)];
                     const float r = g - L.v[max(q, 0)];
                     const int key = (lane < kCacheSlots && q >= 0) ? fkey(r) : kKeyNone;
-                    const int k1 = readlane_i(min8_key(key), 0);
-                    const int l1 = first_lane(ballot(key == k1));
-                    const int key2 = lane == l1 ? kKeyNone : key;
-                    const int k2 = readlane_i(min8_key(key2), 0);
+                    int p1, p2;
+                    min2_8_key(key, p1, p2);
+                    const int k1 = readlane_i(p1, 0), k2 = readlane_i(p2, 0);
+                    const uint64_t m1 = ballot(key == k1);
+                    const int l1 = first_lane(m1);
                     if (k1 != kKeyNone && k2 != kKeyNone) {
-                        const int l2 = first_lane(ballot(key2 == k2));
+                        const int l2 = first_lane(ballot(key == k2) & ~(1ull << l1));
                         const float t2 = readlane_f(r, l2);
                         if (t2 < tau && t2 < kLarge) {
                             // u2 < LARGE: the reference's (LARGE, -1) start
@@ -860,32 +884,27 @@ __device__ __forceinline__ bool large_solve(const int K, const int E, LargeLds &
                 i0 = uniform_i(L.y[j2]);
             }
             lds_sync();
+            // every lane writes the same word (no exec-mask round trip)
             if (cap) {
                 if (lowers) {
-                    if (lane == 0)
-                        L.v[j1] = lowered;
+                    L.v[j1] = lowered;
                     pad_valid = false;
                 }
                 if (i0 >= 0) {
                     if (lowers) {
                         --cur;
-                        if (lane == 0)
-                            L.fr[cur] = i0;
+                        L.fr[cur] = i0;
                     } else {
-                        if (lane == 0)
-                            L.fr[still] = i0;
+                        L.fr[still] = i0;
                         ++still;
                     }
                 }
             } else if (i0 >= 0) {
-                if (lane == 0)
-                    L.fr[still] = i0;
+                L.fr[still] = i0;
                 ++still;
             }
-            if (lane == 0) {
-                L.x[fi] = jsel;
-                L.y[jsel] = fi;
-            }
+            L.x[fi] = jsel;
+            L.y[jsel] = fi;
             lds_sync();
         }
         n_free = still;
@@ -940,10 +959,8 @@ __device__ __forceinline__ bool large_solve(const int K, const int E, LargeLds &
                 }
             }
             if (found >= 0) {
-                if (lane == 0) {
-                    L.y[found] = start;
-                    L.x[start] = found;
-                }
+                L.y[found] = start;  // every lane writes the same word
+                L.x[start] = found;
                 lds_sync();
                 continue;
             }
