@@ -14,6 +14,12 @@
 //    `iters` dependent (minimum, argmin lane) rounds and records core-clock
 //    cycles (s_memtime) and wall time (s_memrealtime, 100 MHz), which also
 //    gives the shader clock.
+// 3. Streaming HBM read: what one kernel that reads a buffer once reaches on
+//    this chip, the practical ceiling of the Sinkhorn pass.  Each workgroup
+//    reads its own contiguous range with eight 16-byte non-temporal loads per
+//    lane in flight (the fastest layout of a sweep over grid-stride and
+//    contiguous ranges, ordinary and non-temporal loads) and folds them so
+//    the loads cannot be dropped.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -67,6 +73,32 @@ argmin_chain_probe(const float *__restrict__ in, unsigned long long *__restrict_
     }
 }
 
+typedef float vf4 __attribute__((ext_vector_type(4)));
+constexpr int kReadUnroll = 8;
+
+__global__ void __launch_bounds__(kProbeThreads)
+hbm_read_probe(const vf4 *__restrict__ src, size_t n4, size_t per_block,
+               float *__restrict__ sink) {
+    const size_t begin = (size_t)blockIdx.x * per_block;
+    const size_t end = begin + per_block < n4 ? begin + per_block : n4;
+    vf4 acc = {0.f, 0.f, 0.f, 0.f};
+    for (size_t i = begin + threadIdx.x; i < end; i += kReadUnroll * kProbeThreads) {
+        vf4 v[kReadUnroll];
+#pragma unroll
+        for (int u = 0; u < kReadUnroll; ++u) {
+            const size_t k = i + (size_t)u * kProbeThreads;
+            v[u] = __builtin_nontemporal_load(src + (k < end ? k : end - 1));
+        }
+#pragma unroll
+        for (int u = 0; u < kReadUnroll; ++u)
+            if (i + (size_t)u * kProbeThreads < end)
+                acc += v[u];
+    }
+    const float s = acc.x + acc.y + acc.z + acc.w;
+    if (s == -1234.5f)  // keeps the loads; sink has a word per workgroup
+        sink[blockIdx.x] = s;
+}
+
 } // namespace
 
 // One wave runs `iters` dependent argmin rounds over 64 floats `in` (device,
@@ -94,4 +126,21 @@ extern "C" int64_t tm_probe_lds_read(uint32_t *sink, int blocks, int iters,
     if (hipGetLastError() != hipSuccess)
         return 0;
     return (int64_t)blocks * kProbeThreads * (int64_t)iters * 16;
+}
+
+// Reads `bytes` (a multiple of 16, > 0) of device memory at `src` once, split
+// into `blocks` contiguous ranges of 256-lane workgroups, on `stream`;
+// returns the bytes read (0 on a bad argument or a launch error).  `sink`
+// needs `blocks` floats of device memory.
+extern "C" int64_t tm_probe_hbm_read(const void *src, size_t bytes, float *sink, int blocks,
+                                     hipStream_t stream) {
+    if (src == nullptr || sink == nullptr || blocks <= 0 || bytes < 16 || bytes % 16 != 0)
+        return 0;
+    const size_t n4 = bytes / 16;
+    const size_t per_block = (n4 + (size_t)blocks - 1) / (size_t)blocks;
+    hipLaunchKernelGGL(hbm_read_probe, dim3((unsigned)blocks), dim3(kProbeThreads), 0, stream,
+                       static_cast<const vf4 *>(src), n4, per_block, sink);
+    if (hipGetLastError() != hipSuccess)
+        return 0;
+    return (int64_t)bytes;
 }
