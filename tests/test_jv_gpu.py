@@ -146,6 +146,41 @@ def test_large_k_prefill_and_plain_workspace(kind, device):
             np.testing.assert_array_equal(got, want_c, err_msg=f"compact {kind} {(n, m)}")
 
 
+def test_large_k_error_contracts_both_workspaces(device):
+    """K > 64 with NaN or -inf: the prefill launches see the flags and write
+    nothing, the solve fills -1 and the status decodes to TM_ERR_NAN /
+    TM_ERR_NEG_INF (ops.cpp:67-93), with either workspace; an all-+inf
+    problem (sentinel cost everywhere) beside finite ones still matches the
+    oracle."""
+    lib = _native.lib()
+    stream = torch.cuda.current_stream(device).cuda_stream
+    rng = np.random.default_rng(17)
+    for bad, code in ((np.nan, _native.TM_ERR_NAN), (-np.inf, _native.TM_ERR_NEG_INF)):
+        c = rng.random((3, 100, 130), dtype=np.float32)
+        c[1, 50, 77] = bad
+        print(f"large-K error contract {bad} (3, 100, 130)", flush=True)
+        for ws_bytes in (lib.tm_jv_workspace_bytes(3, 100, 130),
+                         lib.tm_jv_workspace_bytes_prefill(3, 100, 130)):
+            dc = torch.from_numpy(c).to(device)
+            out = torch.full((3, 100), -7, dtype=torch.int64, device=device)
+            ws = torch.zeros(ws_bytes, dtype=torch.uint8, device=device)
+            status = torch.zeros(2, dtype=torch.int32, device=device)
+            rc = lib.tm_jv_dense_batch_f32(dc.data_ptr(), 3, 100, 130, out.data_ptr(),
+                                           ws.data_ptr(), ctypes.c_size_t(ws_bytes),
+                                           status.data_ptr(), stream)
+            assert rc == _native.TM_OK
+            assert lib.tm_jv_check_status(status.data_ptr(), stream) == code
+            assert (out.cpu().numpy() == -1).all()
+    c = rng.random((3, 90, 120), dtype=np.float32)
+    c[2] = np.inf
+    print("large-K all-+inf problem (3, 90, 120)", flush=True)
+    want = jv.jv_dense_batch(c)
+    for ws_bytes in (lib.tm_jv_workspace_bytes(3, 90, 120),
+                     lib.tm_jv_workspace_bytes_prefill(3, 90, 120)):
+        got = _c_abi_solve(lib, lib.tm_jv_dense_batch_f32, c, ws_bytes, device)
+        np.testing.assert_array_equal(got, want)
+
+
 def test_c2_full_size_mapping_and_total_cost(device):
     cost = workloads.jv_uniform(1024, 64, 64, seed=0)
     want = jv.jv_dense_batch(cost.numpy())
