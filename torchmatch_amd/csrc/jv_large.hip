@@ -558,8 +558,8 @@ jv_large_rowcache_kernel(const float *__restrict__ costs, int64_t B, int N, int 
     CostView C;
     C.N = N;
     C.M = M;
-    if (!prep_sentinel(partial, n_partial, K, C.sentinel))
-        return;
+    C.sentinel = 1.f;
+    bool have_sentinel = false;
     const int64_t rows = B * (int64_t)N;
     for (int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); row < rows;
          row += (int64_t)gridDim.x * 4) {
@@ -572,6 +572,13 @@ jv_large_rowcache_kernel(const float *__restrict__ costs, int64_t B, int N, int 
 #pragma unroll
         for (int e = 0; e < NC; ++e)
             vv[e] = vb[min(e * 64 + lane, K - 1)];
+        // the statistics are folded while the row is in flight (the raw
+        // costs need the sentinel only from here on)
+        if (!have_sentinel) {
+            if (!prep_sentinel(partial, n_partial, K, C.sentinel))
+                return;
+            have_sentinel = true;
+        }
         f32x16 cr;
         int kk[NC];
 #pragma unroll
