@@ -174,7 +174,8 @@ def argmin_chain(device, iters: int = 20000) -> dict | None:
 
 
 def bench_jv(steps: int, warmup: int, device) -> dict:
-    from torchmatch_amd import _native, workloads
+    from torchmatch_amd import _native
+    import workloads
 
     B, N, M = 1024, 64, 64
     cost_cpu = workloads.jv_uniform(B, N, M, seed=0)
@@ -297,7 +298,7 @@ def bench_jv(steps: int, warmup: int, device) -> dict:
 
 def bench_sinkhorn(device, B: int = 16, n_long: int = 200, n_short: int = 20,
                    reps: int = 3) -> dict:
-    from torchmatch_amd import workloads
+    import workloads
 
     N = M = 2048
     reg = 0.05
@@ -353,7 +354,7 @@ def _sinkhorn_roofline(B, N, M, per_iter_ms, traffic) -> dict:
 
 def bench_jv_c3(device, reps: int = 3) -> dict:
     """C3: (64, 512, 768) squared distances + jitter, 20% +inf (K = 768 kernel)."""
-    from torchmatch_amd import workloads
+    import workloads
 
     cost_cpu = workloads.jv_rect_masked()
     cost = cost_cpu.to(device)
@@ -392,7 +393,7 @@ def bench_jv_c3(device, reps: int = 3) -> dict:
 
 def bench_jv_compact(device, reps: int = 20) -> dict:
     """jonker_compact_batch on the C2 input (1024, 64, 64), op time per batch."""
-    from torchmatch_amd import workloads
+    import workloads
 
     cost = workloads.jv_uniform(1024, 64, 64, seed=0).to(device)
     op = torch.ops.assignment.jonker_compact_batch
@@ -406,7 +407,7 @@ def bench_jv_compact(device, reps: int = 20) -> dict:
 
 
 def _c5_inputs():
-    from torchmatch_amd import workloads
+    import workloads
 
     N = 16384
     cost = workloads.sinkhorn_points(1, N, N, 8, seed=0)
@@ -417,7 +418,7 @@ def _c5_inputs():
 
 def bench_unbalanced_c5(device, n_long: int = 100, n_short: int = 20) -> dict:
     """C5: unbalanced Sinkhorn on (1, 16384, 16384), reg 0.02, rho 1 (slope)."""
-    from torchmatch_amd import workloads
+    import workloads
 
     cost_cpu, a_cpu, b_cpu = _c5_inputs()
     shas = {"cost": workloads.sha256(cost_cpu), "a": workloads.sha256(a_cpu),
@@ -473,7 +474,7 @@ def _time_median(fn, budget_s: float, min_runs: int = 5) -> tuple[float, int]:
 def cpu_baseline_jv(budget_s: float = 10.0, compact: bool = False, threads: int | None = None,
                     cost=None, label: str = "C2 (1024,64,64) seed 0") -> dict:
     from oracle import jv
-    from torchmatch_amd import workloads
+    import workloads
 
     if cost is None:
         cost = workloads.jv_uniform(1024, 64, 64, seed=0).numpy()
@@ -494,7 +495,7 @@ def cpu_baseline_jv(budget_s: float = 10.0, compact: bool = False, threads: int 
 
 def cpu_baseline_sinkhorn(n_iter: int = 3) -> dict:
     from oracle import sinkhorn as sk
-    from torchmatch_amd import workloads
+    import workloads
 
     B, N, M = 16, 2048, 2048
     cost = workloads.sinkhorn_points(B, N, M, 8, seed=0)
@@ -647,7 +648,7 @@ def main() -> int:
         line["cpu_baseline"] = cpu_baseline_jv()
         line["cpu_baseline_single_thread"] = cpu_baseline_jv(3.0, threads=1)
         if not args.no_extra:
-            from torchmatch_amd import workloads
+            import workloads
 
             line["jv_compact_c2"]["cpu_baseline"] = cpu_baseline_jv(5.0, compact=True)
             line["jv_c3"]["cpu_baseline"] = cpu_baseline_jv(

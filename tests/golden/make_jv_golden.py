@@ -25,7 +25,7 @@ ROOT = Path(__file__).resolve().parents[2]
 sys.path.insert(0, str(ROOT))
 
 from oracle import jv  # noqa: E402
-from torchmatch_amd import workloads  # noqa: E402
+import workloads  # noqa: E402
 
 OUT = Path(__file__).resolve().parent
 

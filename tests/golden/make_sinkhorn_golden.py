@@ -39,7 +39,7 @@ ROOT = Path(__file__).resolve().parents[2]
 sys.path.insert(0, str(ROOT))
 
 from oracle import sinkhorn as sk  # noqa: E402
-from torchmatch_amd import workloads  # noqa: E402
+import workloads  # noqa: E402
 
 OUT = Path(__file__).resolve().parent
 INDEX = OUT / "sk_golden.json"

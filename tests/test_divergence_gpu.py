@@ -20,7 +20,7 @@ import torch
 
 import torchmatch_amd  # noqa: F401
 from oracle import sinkhorn as sk
-from torchmatch_amd import workloads
+import workloads
 from torchmatch_amd.transport.matrix import Backend, solve
 
 pytestmark = pytest.mark.gpu

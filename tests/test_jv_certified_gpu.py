@@ -24,7 +24,8 @@ import torch
 
 import torchmatch_amd  # noqa: F401
 from oracle import jv
-from torchmatch_amd import _native, workloads
+from torchmatch_amd import _native
+import workloads
 
 pytestmark = pytest.mark.gpu
 

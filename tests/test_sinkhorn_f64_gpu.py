@@ -16,7 +16,7 @@ import torch
 import sk_parity
 import torchmatch_amd  # noqa: F401
 from oracle import sinkhorn as sk
-from torchmatch_amd import workloads
+import workloads
 from torchmatch_amd.transport.matrix import solve
 
 pytestmark = pytest.mark.gpu

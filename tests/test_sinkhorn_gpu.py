@@ -21,7 +21,7 @@ import torch
 import torchmatch_amd  # noqa: F401
 from oracle import sinkhorn as sk
 import sk_parity
-from torchmatch_amd import workloads
+import workloads
 from torchmatch_amd.transport.matrix import Backend, marginal_error, solve
 
 pytestmark = pytest.mark.gpu

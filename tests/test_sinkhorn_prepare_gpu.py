@@ -21,7 +21,8 @@ import pytest
 import torch
 
 import torchmatch_amd  # noqa: F401
-from torchmatch_amd import _native, workloads
+from torchmatch_amd import _native
+import workloads
 from torchmatch_amd.transport.matrix import Backend, solve
 from torchmatch_amd.transport.matrix._schedule import build_eps_schedule
 from torchmatch_amd.transport.matrix._sinkhorn import _device_solve, log_sinkhorn_plan

@@ -19,7 +19,8 @@ import pytest
 import torch
 
 import torchmatch_amd  # noqa: F401
-from torchmatch_amd import _native, workloads
+from torchmatch_amd import _native
+import workloads
 
 pytestmark = pytest.mark.gpu
 
