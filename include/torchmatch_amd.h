@@ -126,6 +126,12 @@ int tm_jv_dense_batch_f32(const float *costs, int64_t B, int32_t N, int32_t M, i
  * summary to pinned host memory the library holds per host thread and
  * device, and the host folds those as they arrive, so a batch with no +inf,
  * NaN or -inf returns without a second launch or a stream synchronisation.
+ * That memory (8,200 bytes per block) is the one allocation these entry
+ * points make: a block is taken from a per-device pool at a thread's first
+ * call on a device (allocated only when the pool is empty) and returned to
+ * the pool when the thread exits, so the process holds one block per device
+ * for each host thread that has called and is alive at once, and keeps the
+ * blocks until it ends.
  * `replays` (host, may be NULL) receives the number of problems that left
  * the certified path for the exact replay on that path (0 otherwise).  Calls
  * on one host thread must not overlap (each returns before the next starts).

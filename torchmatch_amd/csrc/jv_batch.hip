@@ -37,6 +37,7 @@
 #include <math.h>
 #include <atomic>
 #include <mutex>
+#include <vector>
 #include <stdint.h>
 #include <stdlib.h>
 #include <string.h>
@@ -1719,36 +1720,76 @@ extern "C" int tm_jv_compact_batch_f32(const float *costs, int64_t B, int32_t N,
 // statistics-pass path, and the host synchronises the stream.
 // ---------------------------------------------------------------------------
 namespace {
-// Pinned words per host thread and device: the two status words, then one
-// tag word per problem (kFusedMaxB of them), zero-filled when allocated.
+// Pinned words: the two status words, then one tag word per problem
+// (kFusedMaxB of them).  Blocks are allocated once per device and reused: a
+// host thread takes one from its device's pool at its first call and hands it
+// back when it exits, so the pinned memory held is one block per device per
+// host thread alive at once (sizeof(uint32_t) * (2 + kFusedMaxB) = 8,200 bytes
+// each), and a thread-per-request caller reuses blocks instead of allocating.
+// The pool itself is never destroyed (a thread may exit during process
+// teardown) and nothing is freed; the blocks go with the process.
 struct HostWords {
     uint32_t *host = nullptr;
     uint32_t *dev = nullptr;
 };
 
+constexpr int kMaxDevices = 64;
+
+struct HostWordsPool {
+    std::mutex mu;
+    std::vector<HostWords> free_blocks[kMaxDevices];
+};
+
+HostWordsPool &host_words_pool() {
+    static HostWordsPool *pool = new HostWordsPool;  // leaked on purpose, see above
+    return *pool;
+}
+
+// The calling thread's blocks, returned to the pool when the thread exits.
+struct ThreadWords {
+    HostWords slot[kMaxDevices];
+    ~ThreadWords() {
+        HostWordsPool &pool = host_words_pool();
+        std::lock_guard<std::mutex> lock(pool.mu);
+        for (int d = 0; d < kMaxDevices; ++d)
+            if (slot[d].host != nullptr)
+                pool.free_blocks[d].push_back(slot[d]);
+    }
+};
+
 HostWords *host_words(hipStream_t stream) {
-    constexpr int kMaxDevices = 64;
-    thread_local HostWords slots[kMaxDevices];
-    thread_local bool tried[kMaxDevices] = {};
+    thread_local ThreadWords mine;
     hipDevice_t dev = 0;
     if (hipStreamGetDevice(stream, &dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
         return nullptr;
-    HostWords &w = slots[dev];
-    if (!tried[dev]) {
-        tried[dev] = true;
-        const size_t bytes = sizeof(uint32_t) * (2 + (size_t)kFusedMaxB);
-        void *h = nullptr;
-        void *d = nullptr;
-        if (hipHostMalloc(&h, bytes, hipHostMallocMapped) == hipSuccess &&
-            hipHostGetDevicePointer(&d, h, 0) == hipSuccess) {
-            memset(h, 0, bytes);
-            w.host = static_cast<uint32_t *>(h);
-            w.dev = static_cast<uint32_t *>(d);
-        } else {
-            (void)hipGetLastError();
+    HostWords &w = mine.slot[dev];
+    if (w.host != nullptr)
+        return &w;
+    HostWordsPool &pool = host_words_pool();
+    {
+        std::lock_guard<std::mutex> lock(pool.mu);
+        if (!pool.free_blocks[dev].empty()) {
+            w = pool.free_blocks[dev].back();
+            pool.free_blocks[dev].pop_back();
+            return &w;
         }
     }
-    return w.dev != nullptr ? &w : nullptr;
+    const size_t bytes = sizeof(uint32_t) * (2 + (size_t)kFusedMaxB);
+    void *h = nullptr;
+    void *d = nullptr;
+    if (hipHostMalloc(&h, bytes, hipHostMallocMapped) != hipSuccess) {
+        (void)hipGetLastError();
+        return nullptr;
+    }
+    if (hipHostGetDevicePointer(&d, h, 0) != hipSuccess) {
+        (void)hipGetLastError();
+        (void)hipHostFree(h);
+        return nullptr;
+    }
+    memset(h, 0, bytes);
+    w.host = static_cast<uint32_t *>(h);
+    w.dev = static_cast<uint32_t *>(d);
+    return &w;
 }
 
 // 24-bit call tags, never 0 (the words' value when allocated).
@@ -1789,6 +1830,12 @@ int jv_sync(const float *costs, int64_t B, int32_t N, int32_t M, int64_t *out,
         const uint32_t seen[2] = {words[0], words[1]};
         return tm_jv_status_code(seen);
     }
+    // the tag words of this batch start at 0: a word left by an earlier call
+    // (whose writes all landed before it returned) can then never carry the
+    // new tag, even after the 24-bit tags wrap
+    volatile uint32_t *tags = words + 2;
+    for (int64_t p = 0; p < B; ++p)
+        tags[p] = 0;
     const uint32_t tag = next_tag();
     int rc = jv_launch<COMPACT>(costs, B, N, M, out, workspace, workspace_bytes, hw->dev, stream,
                                 hw->dev + 2, tag);
@@ -1798,7 +1845,6 @@ int jv_sync(const float *costs, int64_t B, int32_t N, int32_t M, int64_t *out,
     }
     // fold the tagged summaries as they arrive; if the stream goes idle
     // before all of them are in, the launch failed
-    volatile uint32_t *tags = words + 2;
     uint32_t acc = 0, nrep = 0;
     int64_t seen = 0;
     for (uint32_t spin = 1; seen < B; ++spin) {
