@@ -166,45 +166,51 @@ sk64_row(const double *__restrict__ K, const double *__restrict__ log_v,
 }
 
 // Column half-step: lse_i(K + log_u) per column (64-column strips, four row
-// groups), then log_v (keep-previous rule).
+// groups), then log_v (keep-previous rule).  Blocks stride over the
+// (batch, strip) pairs on gridDim.x, so the batch size has no grid limit.
 __global__ void __launch_bounds__(kThreads)
 sk64_col(const double *__restrict__ K, const double *__restrict__ log_u,
          const double *__restrict__ log_nu, const uint8_t *__restrict__ inf_col,
-         double *__restrict__ log_v, int64_t N, int64_t M, double damp, int unbalanced) {
+         double *__restrict__ log_v, int64_t B, int64_t N, int64_t M, double damp,
+         int unbalanced) {
     __shared__ double part[kGroups][kStrip];
-    const int64_t b = blockIdx.y;
     const int lc = threadIdx.x % kStrip, g = threadIdx.x / kStrip;
-    const int64_t j = (int64_t)blockIdx.x * kStrip + lc;
-    const bool live = j < M;
-    const double *Kb = K + b * N * M;
-    const double *lu = log_u + b * N;
-    double m = -INFINITY;
-    if (live)
-        for (int64_t i = g; i < N; i += kGroups)
-            m = fmax(m, Kb[i * M + j] + lu[i]);
-    part[g][lc] = m;
-    __syncthreads();
-    double mm = part[0][lc];
-    for (int k = 1; k < kGroups; ++k)
-        mm = fmax(mm, part[k][lc]);
-    const double sh = shift_of(mm);
-    __syncthreads();
-    double s = 0.0;
-    if (live)
-        for (int64_t i = g; i < N; i += kGroups)
-            s += exp((Kb[i * M + j] + lu[i]) - sh);
-    part[g][lc] = s;
-    __syncthreads();
-    if (g == 0 && live) {
-        double ss = part[0][lc];
+    const int64_t strips = (M + kStrip - 1) / kStrip;
+    for (int64_t task = blockIdx.x; task < B * strips; task += gridDim.x) {
+        const int64_t b = task / strips;
+        const int64_t j = (task - b * strips) * kStrip + lc;
+        const bool live = j < M;
+        const double *Kb = K + b * N * M;
+        const double *lu = log_u + b * N;
+        double m = -INFINITY;
+        if (live)
+            for (int64_t i = g; i < N; i += kGroups)
+                m = fmax(m, Kb[i * M + j] + lu[i]);
+        part[g][lc] = m;
+        __syncthreads();
+        double mm = part[0][lc];
         for (int k = 1; k < kGroups; ++k)
-            ss += part[k][lc];
-        const double lse = log(ss) + sh;
-        const int64_t t = b * M + j;
-        if (!inf_col[t] && isfinite(lse)) {
-            const double diff = log_nu[t] - lse;
-            log_v[t] = unbalanced ? damp * diff : diff;
+            mm = fmax(mm, part[k][lc]);
+        const double sh = shift_of(mm);
+        __syncthreads();
+        double s = 0.0;
+        if (live)
+            for (int64_t i = g; i < N; i += kGroups)
+                s += exp((Kb[i * M + j] + lu[i]) - sh);
+        part[g][lc] = s;
+        __syncthreads();
+        if (g == 0 && live) {
+            double ss = part[0][lc];
+            for (int k = 1; k < kGroups; ++k)
+                ss += part[k][lc];
+            const double lse = log(ss) + sh;
+            const int64_t t = b * M + j;
+            if (!inf_col[t] && isfinite(lse)) {
+                const double diff = log_nu[t] - lse;
+                log_v[t] = unbalanced ? damp * diff : diff;
+            }
         }
+        __syncthreads();  // part[] is written again by the next task
     }
 }
 
@@ -265,9 +271,6 @@ extern "C" int tm_sinkhorn_f64(const double *cost, const double *a, const double
         return TM_OK;  // no pair: the potentials keep their start value
     if (cost == nullptr || a == nullptr || b == nullptr)
         return TM_ERR_INVALID_ARGUMENT;
-    if (B * M > (int64_t)0x7fffffff || (M + kStrip - 1) / kStrip > (int64_t)0x7fffffff ||
-        B > 65535)
-        return TM_ERR_UNSUPPORTED_SHAPE;
     const Layout64 L = layout64(B, N, M);
     if (workspace == nullptr || workspace_bytes < L.total)
         return TM_ERR_WORKSPACE;
@@ -289,7 +292,7 @@ extern "C" int tm_sinkhorn_f64(const double *cost, const double *a, const double
                 inf_col, B, N, M);
     const bool unbalanced = rho > 0.0;
     const dim3 row_grid(grid_for(B * N, 1, 1 << 16));
-    const dim3 col_grid((unsigned)((M + kStrip - 1) / kStrip), (unsigned)B);
+    const dim3 col_grid(grid_for(B * ((M + kStrip - 1) / kStrip), 1, 1 << 16));
     double cur = -1.0;
     for (int32_t s = 0; s < n_iter; ++s) {
         const double e = eps_sched[s];
@@ -301,7 +304,7 @@ extern "C" int tm_sinkhorn_f64(const double *cost, const double *a, const double
         TM64_LAUNCH(sk64_row, row_grid, dim3(kThreads), stream, K, log_v, log_mu, inf_row,
                     log_u, B, N, M, damp, unbalanced ? 1 : 0);
         TM64_LAUNCH(sk64_col, col_grid, dim3(kThreads), stream, K, log_u, log_nu, inf_col,
-                    log_v, N, M, damp, unbalanced ? 1 : 0);
+                    log_v, B, N, M, damp, unbalanced ? 1 : 0);
     }
     if (log_plan != nullptr)
         TM64_LAUNCH(sk64_plan, map_grid, dim3(256), stream, K, log_u, log_v, log_plan, B, N, M);
