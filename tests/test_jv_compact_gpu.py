@@ -16,7 +16,6 @@ NaN / -inf contract and the unpacked tuple.
 from __future__ import annotations
 
 import json
-import zlib
 from pathlib import Path
 
 import numpy as np
@@ -25,7 +24,9 @@ import torch
 
 import torchmatch_amd  # noqa: F401
 from oracle import jv
-from torchmatch_amd import _native, workloads
+from torchmatch_amd import _native
+import jv_inputs
+import workloads
 
 pytestmark = pytest.mark.gpu
 
@@ -61,68 +62,28 @@ def test_golden_fixture(name, meta, device):
     assert mism.size == 0, f"{mism.size} problems differ, first {mism[:8].tolist()}"
 
 
-def _random_batch(rng, kind: str, b: int, n: int, m: int) -> np.ndarray:
-    if kind == "uniform":
-        c = rng.random((b, n, m), dtype=np.float32)
-    elif kind == "tied":
-        c = rng.integers(0, 3, (b, n, m)).astype(np.float32)
-    elif kind == "masked":
-        c = rng.random((b, n, m), dtype=np.float32)
-        c[rng.random((b, n, m)) < 0.5] = np.inf
-    elif kind == "tied_masked":
-        c = rng.integers(0, 2, (b, n, m)).astype(np.float32)
-        c[rng.random((b, n, m)) < 0.3] = np.inf
-    elif kind == "negative":
-        c = (rng.random((b, n, m), dtype=np.float32) - 0.7) * 100.0
-    elif kind == "huge":  # beyond 1e15: lane-serial path
-        c = rng.random((b, n, m), dtype=np.float32) * np.float32(3e16)
-    elif kind == "big":  # 1e12 .. 1e15: serial for compact, wave path for dense
-        c = rng.random((b, n, m), dtype=np.float32) * np.float32(5e13)
-        c[rng.random((b, n, m)) < 0.1] = np.inf
-    elif kind == "signed_zero":
-        c = rng.integers(-1, 2, (b, n, m)).astype(np.float32) * np.float32(0.0)
-        c[rng.random((b, n, m)) < 0.5] = np.float32(1.0)
-    else:
-        raise ValueError(kind)
-    return c
-
-
-KINDS = ["uniform", "tied", "masked", "tied_masked", "negative", "huge", "big", "signed_zero"]
-
-
-@pytest.mark.parametrize("kind", KINDS)
+@pytest.mark.parametrize("kind", jv_inputs.KINDS_COMPACT)
 def test_random_batches_match_oracle(kind, device):
-    rng = np.random.default_rng(zlib.crc32(b"compact-gpu-" + kind.encode()))
-    kmax = min(_max_k(), 64)
-    shapes = [(64, kmax, kmax), (64, 40, kmax), (64, kmax, 23), (128, 17, 17), (128, 5, 5),
-              (64, 1, 1), (64, 2, 2), (64, 3, 7)]
-    for b, n, m in shapes:
-        c = _random_batch(rng, kind, b, n, m)
-        print(f"compact {kind} {(b, n, m)}", flush=True)
+    for n, m, c in jv_inputs.compact_small_batches(kind, min(_max_k(), 64)):
+        print(f"compact {kind} {c.shape}", flush=True)
         want = jv.jv_compact_batch(c)
         got = run_op(c, device)
         mism = np.argwhere((got != want).any(axis=1)).ravel()
-        assert mism.size == 0, f"{kind} {(b, n, m)}: {mism.size} problems differ"
+        assert mism.size == 0, f"{kind} {c.shape}: {mism.size} problems differ"
 
 
-@pytest.mark.parametrize("kind", ["uniform", "tied", "masked", "tied_masked", "negative", "huge",
-                                  "big"])
+@pytest.mark.parametrize("kind", jv_inputs.KINDS_COMPACT_LARGE)
 def test_large_k_match_oracle(kind, device):
     """64 < K <= 1024: the large-K compact kernel (and its lane-serial path for
     huge magnitudes)."""
     if _max_k() <= 64:
         pytest.skip("no large-K compact kernel in this build")
-    rng = np.random.default_rng(zlib.crc32(b"compact-large-" + kind.encode()))
-    shapes = [(16, 65, 65), (8, 100, 130), (8, 130, 100), (6, 300, 300), (3, 700, 768)]
-    if kind not in ("huge", "big"):
-        shapes.append((2, 1024, 1000))
-    for b, n, m in shapes:
-        c = _random_batch(rng, kind, b, n, m)
-        print(f"compact large {kind} {(b, n, m)}", flush=True)
+    for n, m, c in jv_inputs.compact_large_batches(kind):
+        print(f"compact large {kind} {c.shape}", flush=True)
         want = jv.jv_compact_batch(c)
         got = run_op(c, device)
         mism = np.argwhere((got != want).any(axis=1)).ravel()
-        assert mism.size == 0, f"{kind} {(b, n, m)}: {mism.size} problems differ"
+        assert mism.size == 0, f"{kind} {c.shape}: {mism.size} problems differ"
 
 
 def test_every_k_up_to_limit(device):

@@ -11,7 +11,6 @@ problems, and the reference tests' known answers and error contracts
 from __future__ import annotations
 
 import ctypes
-import zlib
 import json
 import subprocess
 import sys
@@ -24,7 +23,9 @@ import torch
 
 import torchmatch_amd
 from oracle import jv
-from torchmatch_amd import _native, workloads
+from torchmatch_amd import _native
+import jv_inputs
+import workloads
 from torchmatch_amd.assignment import assignment_cost
 
 pytestmark = pytest.mark.gpu
@@ -58,53 +59,24 @@ def test_golden_fixture(name, meta, device):
     assert mism.size == 0, f"{mism.size} problems differ, first {mism[:8].tolist()}"
 
 
-def _random_batch(rng, kind: str, b: int, n: int, m: int) -> np.ndarray:
-    if kind == "uniform":
-        c = rng.random((b, n, m), dtype=np.float32)
-    elif kind == "tied":
-        c = rng.integers(0, 3, (b, n, m)).astype(np.float32)
-    elif kind == "masked":
-        c = rng.random((b, n, m), dtype=np.float32)
-        c[rng.random((b, n, m)) < 0.5] = np.inf
-    elif kind == "tied_masked":
-        c = rng.integers(0, 2, (b, n, m)).astype(np.float32)
-        c[rng.random((b, n, m)) < 0.3] = np.inf
-    elif kind == "negative":
-        c = (rng.random((b, n, m), dtype=np.float32) - 0.7) * 100.0
-    elif kind == "huge":  # beyond 1e15: lane-serial path
-        c = rng.random((b, n, m), dtype=np.float32) * np.float32(3e16)
-    else:
-        raise ValueError(kind)
-    return c
-
-
-@pytest.mark.parametrize("kind", ["uniform", "tied", "masked", "tied_masked", "negative", "huge"])
+@pytest.mark.parametrize("kind", jv_inputs.KINDS_SMALL)
 def test_random_batches_vs_oracle(kind, device):
-    rng = np.random.default_rng(zlib.crc32(kind.encode()))
-    shapes = [(64, 64), (1, 1), (1, 5), (5, 1), (2, 2), (17, 17), (31, 64), (64, 31),
-              (63, 63), (40, 7), (7, 40), (33, 48)]
-    for n, m in shapes:
-        b = 64 if kind != "huge" else 8
-        c = _random_batch(rng, kind, b, n, m)
+    for n, m, c in jv_inputs.small_batches(kind):
         want = jv.jv_dense_batch(c)
-        print(f"kind {kind} shape {(b, n, m)}", flush=True)
+        print(f"kind {kind} shape {c.shape}", flush=True)
         got = run_op(torch.from_numpy(c), device)
-        np.testing.assert_array_equal(got, want, err_msg=f"{kind} {(b, n, m)}")
+        np.testing.assert_array_equal(got, want, err_msg=f"{kind} {c.shape}")
 
 
-@pytest.mark.parametrize("kind", ["uniform", "tied", "masked", "tied_masked", "negative"])
+@pytest.mark.parametrize("kind", jv_inputs.KINDS_LARGE)
 def test_large_k_vs_oracle(kind, device):
-    """K > 64: the global-memory kernel (cost outside LDS)."""
-    rng = np.random.default_rng(zlib.crc32(("large" + kind).encode()))
-    # every chunk-count instantiation (2, 4, 8, 12, 16 chunks of 64 columns),
-    # rectangular both ways
-    for n, m in [(65, 65), (100, 80), (80, 100), (128, 128), (200, 130), (300, 300),
-                 (700, 768), (768, 600), (1000, 1024)]:
-        c = _random_batch(rng, kind, 6, n, m)
+    """K > 64: the global-memory kernel (cost outside LDS), at every
+    chunk-count instantiation, rectangular both ways."""
+    for n, m, c in jv_inputs.large_batches(kind):
         want = jv.jv_dense_batch(c)
-        print(f"large kind {kind} shape {(6, n, m)}", flush=True)
+        print(f"large kind {kind} shape {c.shape}", flush=True)
         got = run_op(torch.from_numpy(c), device)
-        np.testing.assert_array_equal(got, want, err_msg=f"{kind} {(6, n, m)}")
+        np.testing.assert_array_equal(got, want, err_msg=f"{kind} {c.shape}")
 
 
 def _c_abi_solve(lib, entry, c: np.ndarray, ws_bytes: int, device) -> np.ndarray:
@@ -121,17 +93,14 @@ def _c_abi_solve(lib, entry, c: np.ndarray, ws_bytes: int, device) -> np.ndarray
     return out.cpu().numpy()
 
 
-@pytest.mark.parametrize("kind", ["uniform", "tied", "masked", "tied_masked"])
+@pytest.mark.parametrize("kind", jv_inputs.KINDS_PREFILL)
 def test_large_k_prefill_and_plain_workspace(kind, device):
     """K > 64 with the prefill workspace (column minima and row caches from
     many-wave launches) and with the minimum workspace (both in the solve's
     one wave): the same mapping as the oracle, dense and compact, at every
     chunk count, rectangular both ways."""
     lib = _native.lib()
-    rng = np.random.default_rng(zlib.crc32(("prefill" + kind).encode()))
-    for n, m in [(65, 70), (130, 100), (100, 250), (300, 512), (512, 768), (768, 700),
-                 (1024, 900)]:
-        c = _random_batch(rng, kind, 4, n, m)
+    for n, m, c in jv_inputs.prefill_batches(kind):
         print(f"prefill kind {kind} shape {(4, n, m)}", flush=True)
         small = lib.tm_jv_workspace_bytes(4, n, m)
         full = lib.tm_jv_workspace_bytes_prefill(4, n, m)

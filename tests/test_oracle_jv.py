@@ -24,7 +24,8 @@ import pytest
 import torch
 
 from oracle import jv
-from torchmatch_amd import workloads
+import jv_inputs
+import workloads
 
 GOLDEN = Path(__file__).resolve().parent / "golden"
 
@@ -77,6 +78,38 @@ def test_oracle_matches_reference_build(kind):
         np.testing.assert_array_equal(jv.jv_dense_batch(c), jv.ref_jv_dense_batch(c))
 
 
+@pytest.mark.skipif(not jv.ref_available(), reason="reference build (oracle/_ref) absent")
+@pytest.mark.parametrize("kind", jv_inputs.KINDS_SMALL)
+def test_oracle_matches_reference_build_on_small_k_gpu_inputs(kind):
+    """The exact K <= 64 batches the GPU tests compare the kernel with the
+    oracle on (tests/test_jv_gpu.py): oracle == reference build."""
+    for n, m, c in jv_inputs.small_batches(kind):
+        np.testing.assert_array_equal(jv.jv_dense_batch(c), jv.ref_jv_dense_batch(c),
+                                      err_msg=f"{kind} {c.shape}")
+
+
+@pytest.mark.skipif(not jv.ref_available(), reason="reference build (oracle/_ref) absent")
+@pytest.mark.parametrize("kind", jv_inputs.KINDS_LARGE)
+def test_oracle_matches_reference_build_on_large_k_gpu_inputs(kind):
+    """K = 65 ... 1024, rectangular both ways, negative costs: the exact
+    batches of the GPU large-K tests, oracle == reference build."""
+    for n, m, c in jv_inputs.large_batches(kind):
+        np.testing.assert_array_equal(jv.jv_dense_batch(c), jv.ref_jv_dense_batch(c),
+                                      err_msg=f"{kind} {c.shape}")
+
+
+@pytest.mark.skipif(not jv.ref_available(), reason="reference build (oracle/_ref) absent")
+@pytest.mark.parametrize("kind", jv_inputs.KINDS_PREFILL)
+def test_oracle_matches_reference_build_on_prefill_gpu_inputs(kind):
+    """The batches of the GPU prefill / plain-workspace test, dense and
+    compact solvers."""
+    for n, m, c in jv_inputs.prefill_batches(kind):
+        np.testing.assert_array_equal(jv.jv_dense_batch(c), jv.ref_jv_dense_batch(c),
+                                      err_msg=f"dense {kind} {c.shape}")
+        np.testing.assert_array_equal(jv.jv_compact_batch(c), jv.ref_jv_compact_batch(c),
+                                      err_msg=f"compact {kind} {c.shape}")
+
+
 def _golden_cases():
     index = json.loads((GOLDEN / "jv_golden.json").read_text())
     return sorted(index.items())
@@ -84,8 +117,6 @@ def _golden_cases():
 
 @pytest.mark.parametrize(("name", "meta"), _golden_cases(), ids=[n for n, _ in _golden_cases()])
 def test_oracle_matches_golden(name, meta):
-    if meta["shape"][1] * meta["shape"][2] > 100_000:
-        pytest.skip("large case: covered on the GPU against the fixture directly")
     cost = getattr(workloads, meta["generator"])(**meta["kwargs"])
     assert workloads.sha256(cost) == meta["sha256"], "input generator drifted"
     want = np.load(GOLDEN / meta["file"])["mapping"].astype(np.int64)

@@ -25,7 +25,8 @@ import numpy as np
 import pytest
 
 from oracle import jv
-from torchmatch_amd import workloads
+import jv_inputs
+import workloads
 
 GOLDEN = Path(__file__).resolve().parent / "golden"
 
@@ -77,6 +78,21 @@ def test_oracle_matches_reference_build(kind):
     np.testing.assert_array_equal(jv.jv_compact_batch(c), jv.ref_jv_compact_batch(c))
 
 
+@pytest.mark.skipif(not jv.ref_available(), reason="reference build (oracle/_ref) absent")
+@pytest.mark.parametrize("kind", jv_inputs.KINDS_COMPACT)
+def test_oracle_matches_reference_build_on_gpu_inputs(kind):
+    """The exact batches the compact GPU tests compare the kernels with this
+    oracle on (tests/test_jv_compact_gpu.py), K <= 64 and 64 < K <= 1024:
+    oracle == reference build."""
+    for n, m, c in jv_inputs.compact_small_batches(kind):
+        np.testing.assert_array_equal(jv.jv_compact_batch(c), jv.ref_jv_compact_batch(c),
+                                      err_msg=f"{kind} {c.shape}")
+    if kind in jv_inputs.KINDS_COMPACT_LARGE:
+        for n, m, c in jv_inputs.compact_large_batches(kind):
+            np.testing.assert_array_equal(jv.jv_compact_batch(c), jv.ref_jv_compact_batch(c),
+                                          err_msg=f"large {kind} {c.shape}")
+
+
 def _golden_cases():
     index = json.loads((GOLDEN / "jv_golden.json").read_text())
     return sorted(index.items())
@@ -84,8 +100,6 @@ def _golden_cases():
 
 @pytest.mark.parametrize(("name", "meta"), _golden_cases(), ids=[n for n, _ in _golden_cases()])
 def test_oracle_matches_golden(name, meta):
-    if meta["shape"][1] * meta["shape"][2] > 100_000:
-        pytest.skip("large case: covered on the GPU against the fixture directly")
     cost = getattr(workloads, meta["generator"])(**meta["kwargs"])
     assert workloads.sha256(cost) == meta["sha256"], "input generator drifted"
     want = np.load(GOLDEN / meta["file"])["compact"].astype(np.int64)
