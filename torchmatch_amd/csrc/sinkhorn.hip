@@ -160,6 +160,12 @@ struct SinkhornLayout {
     int fz_interleave;           // chunks take every n_chunk-th row (else a range)
     size_t off_k, off_logmu, off_lognu, off_infrow, off_infcol, off_colpart, off_lse2col,
         off_lse2row, off_stats, total;
+    // float64 state of the fused step: the potentials, the marginals' logs,
+    // and the potentials scaled by kLog2e in float32 (what the element
+    // loops add), B*N / B*M each
+    size_t off_lu64, off_lv64, off_mu64, off_nu64, off_lu2, off_lv2;
+    // per-column weights 2^(lv2 rounding residual), float32, B*M
+    size_t off_lvw;
 };
 
 __host__ __device__ inline size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
@@ -181,7 +187,7 @@ struct FusedShape {
     int W, RW, NV, blocks_per_cu;
 };
 constexpr FusedShape kFusedShapes[] = {
-    {0, 0, 0, 0}, {1, 4, 4, 7}, {1, 4, 8, 2}, {2, 1, 8, 4}, {4, 1, 8, 2}, {8, 1, 8, 1},
+    {0, 0, 0, 0}, {1, 4, 4, 5}, {1, 4, 8, 2}, {2, 1, 8, 4}, {4, 1, 8, 2}, {8, 1, 8, 1},
     {16, 1, 4, 1}, {1, 4, 1, 8}, {1, 4, 2, 8},
 };
 constexpr int kFusedMinRowsPerWave = 8;
@@ -271,6 +277,27 @@ SinkhornLayout make_layout(int64_t B, int64_t N, int64_t M) {
     L.off_lse2row = off;
     if (L.fused)
         off = align_up(off + sizeof(float) * (size_t)(B * N), 256);
+    L.off_lu64 = off;
+    if (L.fused)
+        off = align_up(off + sizeof(double) * (size_t)(B * N), 256);
+    L.off_lv64 = off;
+    if (L.fused)
+        off = align_up(off + sizeof(double) * (size_t)(B * M), 256);
+    L.off_mu64 = off;
+    if (L.fused)
+        off = align_up(off + sizeof(double) * (size_t)(B * N), 256);
+    L.off_nu64 = off;
+    if (L.fused)
+        off = align_up(off + sizeof(double) * (size_t)(B * M), 256);
+    L.off_lu2 = off;
+    if (L.fused)
+        off = align_up(off + sizeof(float) * (size_t)(B * N), 256);
+    L.off_lv2 = off;
+    if (L.fused)
+        off = align_up(off + sizeof(float) * (size_t)(B * M), 256);
+    L.off_lvw = off;
+    if (L.fused)
+        off = align_up(off + sizeof(float) * (size_t)(B * M), 256);
     L.off_stats = off;
     off += 256;
     L.total = off;
@@ -296,10 +323,18 @@ __device__ __forceinline__ uint32_t order_key(float f) {
 // C' = C, or with a keep mask C' = keep ? C : +inf (torch's
 // `cost.masked_fill(~mask, inf)`), so masked pairs hold -inf.  Float4 steps
 // when `vec` (C and K 16-byte aligned, keep 4-byte aligned), else scalar.
+// One element of K from C': -C'/e (float32 IEEE division, the reference's
+// expression) when s2 == 0, else C' * s2 rounded once to float32 with
+// s2 = -log2(e)/e in float64: the fused step's base-2 log kernel, in which
+// 2^(K + p) is exactly e^(-C'/e + p/log2(e)) up to the one rounding of K.
+__device__ __forceinline__ float k_of(float c, float e, double s2) {
+    return s2 != 0.0 ? (float)((double)c * s2) : -c / e;
+}
+
 template <bool MASK>
 __global__ void __launch_bounds__(kMapBlock)
 sk_log_kernel(const float *__restrict__ C, const uint8_t *__restrict__ keep,
-              float *__restrict__ K, int64_t n, float eps, int vec) {
+              float *__restrict__ K, int64_t n, float eps, double s2, int vec) {
     const int64_t stride = (int64_t)gridDim.x * kMapBlock;
     const int64_t n4 = vec ? n / 4 : 0;
     const float4 *c4 = reinterpret_cast<const float4 *>(C);
@@ -315,31 +350,43 @@ sk_log_kernel(const float *__restrict__ C, const uint8_t *__restrict__ keep,
             c.w = (kp & 0xff000000u) ? c.w : f_inf();
         }
         float4 r;
-        r.x = -c.x / eps;
-        r.y = -c.y / eps;
-        r.z = -c.z / eps;
-        r.w = -c.w / eps;
+        r.x = k_of(c.x, eps, s2);
+        r.y = k_of(c.y, eps, s2);
+        r.z = k_of(c.z, eps, s2);
+        r.w = k_of(c.w, eps, s2);
         k4[k] = r;
     }
     for (int64_t k = n4 * 4 + (int64_t)blockIdx.x * kMapBlock + threadIdx.x; k < n; k += stride)
-        K[k] = -((MASK && keep[k] == 0) ? f_inf() : C[k]) / eps;
+        K[k] = k_of((MASK && keep[k] == 0) ? f_inf() : C[k], eps, s2);
 }
 
 // log of a marginal (torch `a.log()`), n elements; sets `neg_flag` in
 // stats[0] when an element is negative (the reference's `(a < 0).any()`).
+// y64 (may be null): the same log in float64 of the float32 value, for the
+// fused step's float64 potentials.
 __global__ void __launch_bounds__(kMapBlock)
-sk_log_marginal(const float *__restrict__ x, float *__restrict__ y, int64_t n,
-                uint32_t *__restrict__ stats, uint32_t neg_flag) {
+sk_log_marginal(const float *__restrict__ x, float *__restrict__ y, double *__restrict__ y64,
+                int64_t n, uint32_t *__restrict__ stats, uint32_t neg_flag) {
     const int64_t k = (int64_t)blockIdx.x * kMapBlock + threadIdx.x;
     const float v = k < n ? x[k] : 0.f;
-    if (k < n)
+    if (k < n) {
         y[k] = logf(v);
+        if (y64 != nullptr)
+            y64[k] = log((double)v);
+    }
     if (ballot(v < 0.f) != 0 && lane_id() == 0)
         atomicOr(&stats[0], neg_flag);
 }
 
 __global__ void __launch_bounds__(kMapBlock)
 sk_fill(float *__restrict__ y, int64_t n, float value) {
+    const int64_t k = (int64_t)blockIdx.x * kMapBlock + threadIdx.x;
+    if (k < n)
+        y[k] = value;
+}
+
+__global__ void __launch_bounds__(kMapBlock)
+sk_fill64(double *__restrict__ y, int64_t n, double value) {
     const int64_t k = (int64_t)blockIdx.x * kMapBlock + threadIdx.x;
     if (k < n)
         y[k] = value;
@@ -378,7 +425,7 @@ template <bool VEC, bool MASK>
 __global__ void __launch_bounds__(kPrepWaves * 64)
 sk_prepare(const float *__restrict__ C, const uint8_t *__restrict__ keep,
            float *__restrict__ K, uint8_t *__restrict__ inf_row, uint8_t *__restrict__ inf_col,
-           uint32_t *__restrict__ stats, int64_t N, int64_t M, int groups, float e) {
+           uint32_t *__restrict__ stats, int64_t N, int64_t M, int groups, float e, double s2) {
     constexpr int CW = VEC ? 4 : 1;
     __shared__ uint32_t col_any[kPrepWaves][64];
     __shared__ float blk_max[kPrepWaves];
@@ -436,7 +483,7 @@ sk_prepare(const float *__restrict__ C, const uint8_t *__restrict__ keep,
                 }
                 if (__builtin_isfinite(y))
                     vmax = fmaxf(vmax, y);
-                kv[q] = -y / e;
+                kv[q] = k_of(y, e, s2);
             }
             if (write_k && col_ok) {
                 const int64_t off = (b * N + r) * M + c0;
@@ -863,24 +910,79 @@ __device__ __forceinline__ Lse fold_partial(float m, float s) {
     return Lse{s != 0.f ? m : -f_inf(), m == f_inf() ? f_inf() : s};
 }
 
+// Natural units per base-2 unit and back, float64: the fused step's K holds
+// -C'*log2(e)/e (k_of with s2 = -kLog2eD/e) and its potentials enter the
+// element loops scaled by kLog2eD, so 2^(K + p2) = e^(-C'/e + p) up to the
+// float32 roundings of K and p2, with no constant's rounding in the exponent.
+constexpr double kLog2eD = 1.4426950408889634074;
+constexpr double kLn2D = 0.69314718055994530942;
+
+// log2 of a float32 s > 0 in float64: s = m * 2^e with m in [sqrt(1/2),
+// sqrt(2)), e exact and the native log on m only.  The native log is
+// accurate near 1 but its error grows with |log2 s| (up to one float32 ulp
+// of the result, biased low), and a bias common to every row or column is
+// what the balanced potentials' neutral mode accumulates step after step.
+// +inf, 0 and NaN go to the native log directly.
+__device__ __forceinline__ double log2_split(float s) {
+    if (!(s > 0.f) || !__builtin_isfinite(s))
+        return (double)__builtin_amdgcn_logf(s);
+    int e = __builtin_amdgcn_frexp_expf(s);
+    float m = __builtin_amdgcn_frexp_mantf(s);  // [0.5, 1)
+    if (m < 0.70710678f) {
+        m *= 2.f;
+        e -= 1;
+    }
+    return (double)e + (double)__builtin_amdgcn_logf(m);
+}
+
+// log2 of a float64 sum s > 0: log2_split of its float32 rounding plus the
+// first-order term of the rounding (relative <= 2^-24, so the second-order
+// term is below 2^-49).
+__device__ __forceinline__ double log2_of_sum(double s) {
+    const float h = (float)s;
+    const float r = (float)(s - (double)h);  // exact: |r| <= ulp(h) / 2
+    return log2_split(h) + (double)(r * __builtin_amdgcn_rcpf(h) * kLog2e);
+}
+
+// A potential p (float64) enters the float32 element loops as p2 = fl(p *
+// log2 e) and the weight w = 2^(p * log2 e - p2) = 1 + (p*log2 e - p2) ln 2
+// (to 1e-13), so a term 2^(K + p2) * w carries the potential's float64 value:
+// the rounding of p2 is not a fixed error of every step's sums.
+__device__ __forceinline__ float potential_weight(double p, float p2) {
+    return (float)(1.0 + (p * kLog2eD - (double)p2) * kLn2D);
+}
+
+// The potential update in float64: the reference's isfinite keep-previous
+// rule on the natural LSE l2 * ln 2, damping in float64 (the reference's
+// rule and order, _log_sinkhorn.py:194-215, _unbalanced_sinkhorn.py:72-100).
+__device__ __forceinline__ double update_potential64(double l2, double log_marg, double old,
+                                                     double damp, bool unbalanced) {
+    if (!isfinite(l2))
+        return old;
+    const double diff = log_marg - l2 * kLn2D;
+    return unbalanced ? damp * diff : diff;
+}
+
 // All NV float4 of a row in flight at once: scalar row base + 32-bit lane
 // byte offsets (the saddr form of the load).  Lanes past the row end read its
 // last float4 again (offsets clamped); their log_v in LDS is -inf, which
 // keeps them out of the row LSE, and their column sums are never stored.
-// The row's flag, log marginal, current log_u and previous base-2 LSE (its
-// shift) are loaded with it: a load
-// issued later would make the wait for it a wait for every row in flight.
+// The row's float64 log marginal and potential and its previous base-2 LSE
+// (its shift) are loaded with it: a load issued later would make the wait
+// for it a wait for every row in flight.  A row of C' that is all +inf needs
+// no flag: K is -inf on it, its terms are 0 and its sum 0 or NaN, which
+// fails the window test; the exact LSE is then -inf and the potential keeps
+// its value (the reference's keep-previous rule), and its column terms are 0.
 // NT: non-temporal loads, for a K larger than the last-level (Infinity)
 // cache, which each step streams once and would only evict what the next
 // step reads (C5, 1 GiB: 187.9 against 193.7 us per step; C4's 256 MiB, which
 // the cache partly keeps between steps, is faster with ordinary loads).
 template <int NV, bool NT>
-__device__ __forceinline__ void fz_load(vf4 (&dst)[NV], float &mu, float &u, float &rs, int &skip,
+__device__ __forceinline__ void fz_load(vf4 (&dst)[NV], double &mu, double &u, float &rs,
                                         const vf4 *__restrict__ row4, const uint32_t (&qb)[NV],
-                                        int64_t r, const float *__restrict__ log_mu,
-                                        const float *__restrict__ log_u,
-                                        const float *__restrict__ lse2_row,
-                                        const uint8_t *__restrict__ inf_row) {
+                                        int64_t r, const double *__restrict__ mu64,
+                                        const double *__restrict__ lu64,
+                                        const float *__restrict__ lse2_row) {
     const char *base = reinterpret_cast<const char *>(row4);
     if constexpr (NT) {
 #pragma unroll
@@ -891,9 +993,8 @@ __device__ __forceinline__ void fz_load(vf4 (&dst)[NV], float &mu, float &u, flo
         for (int k = 0; k < NV; ++k)
             dst[k] = *reinterpret_cast<const vf4 *>(base + qb[k]);
     }
-    skip = inf_row[r];
-    mu = log_mu[r];
-    u = log_u[r];
+    mu = mu64[r];
+    u = lu64[r];
     rs = lse2_row[r];
 }
 
@@ -902,14 +1003,14 @@ __device__ __forceinline__ void fz_load(vf4 (&dst)[NV], float &mu, float &u, flo
 // in LDS slot `par`.  Returns the slot parity for the next use.
 template <int W, int NV>
 __device__ __forceinline__ int fz_row_exact(const vf4 (&kk)[NV], const vf4 *lv_s,
-                                            float2 (*rowpart)[W], int par, int w, int lane,
-                                            Lse &tot) {
+                                            const vf4 (&wv)[NV], float2 (*rowpart)[W], int par,
+                                            int w, int lane, Lse &tot) {
     float m = -f_inf();
 #pragma unroll
     for (int k = 0; k < NV; ++k) {
-        const vf4 lv = lv_s[(k * W + w) * 64 + lane];
-        m = fmax_nn(fmax_nn(m, fmaf(kk[k].x, kLog2e, lv.x)), fmaf(kk[k].y, kLog2e, lv.y));
-        m = fmax_nn(fmax_nn(m, fmaf(kk[k].z, kLog2e, lv.z)), fmaf(kk[k].w, kLog2e, lv.w));
+        const vf4 y = kk[k] + lv_s[(k * W + w) * 64 + lane];
+        m = fmax_nn(fmax_nn(m, y.x), y.y);
+        m = fmax_nn(fmax_nn(m, y.z), y.w);
     }
     m = wave_max_all(m);
     const float sh = lse_shift(m);
@@ -919,13 +1020,13 @@ __device__ __forceinline__ int fz_row_exact(const vf4 (&kk)[NV], const vf4 *lv_s
     float s = 0.f;
 #pragma unroll
     for (int k = 0; k < NV; ++k) {
-        const vf4 lv = lv_s[(k * W + w) * 64 + lane];
-        s += __builtin_amdgcn_exp2f(fmaf(kk[k].x, kLog2e, lv.x) - sh);
-        s += __builtin_amdgcn_exp2f(fmaf(kk[k].y, kLog2e, lv.y) - sh);
-        s += __builtin_amdgcn_exp2f(fmaf(kk[k].z, kLog2e, lv.z) - sh);
-        s += __builtin_amdgcn_exp2f(fmaf(kk[k].w, kLog2e, lv.w) - sh);
+        const vf4 y = kk[k] + lv_s[(k * W + w) * 64 + lane];
+        s = fmaf(__builtin_amdgcn_exp2f(y.x - sh), wv[k].x, s);
+        s = fmaf(__builtin_amdgcn_exp2f(y.y - sh), wv[k].y, s);
+        s = fmaf(__builtin_amdgcn_exp2f(y.z - sh), wv[k].z, s);
+        s = fmaf(__builtin_amdgcn_exp2f(y.w - sh), wv[k].w, s);
     }
-    s = wave_sum_all(s);
+    s = (float)wave_sum_all_d((double)s);
     tot = Lse{m, s};
     if constexpr (W > 1) {
         if (lane == 0)
@@ -940,75 +1041,95 @@ __device__ __forceinline__ int fz_row_exact(const vf4 (&kk)[NV], const vf4 *lv_s
     return par;
 }
 
+// Outputs of the fused step's row update (row r): the float64 potential, its
+// float32 copy (the caller's log_u), its kLog2eD-scaled float32 (what the
+// column recompute adds) and the base-2 LSE (the next step's shift).
+struct FzRowOut {
+    double *lu64;
+    float *log_u;
+    float *lu2;
+    float *lse2_row;
+};
+
 // One row (batch-flat index r) of the fused step: its base-2 LSE, the log_u
-// update, then the column fold.  The LSE is summed against the row's LSE of
-// the previous step (rs) in one pass and accepted in the same window as the
-// column sums; otherwise, and on EXACT steps, it is the exact two-pass.
-// Returns the LDS slot parity for the next row.
+// update in float64, then the column fold.  The LSE is summed against the
+// row's LSE of the previous step (rs) in one pass and accepted in the same
+// window as the column sums; otherwise, and on EXACT steps, it is the exact
+// two-pass.  Returns the LDS slot parity for the next row.
 template <int W, int NV, bool EXACT>
-__device__ __forceinline__ int fz_row(const vf4 (&kk)[NV], float mu_r, float u_r, float rs,
-                                      int skip, const vf4 *lv_s, const vf4 *cs_s,
-                                      float2 (*rowpart)[W], int par, int w, int lane, int64_t r,
-                                      float *__restrict__ log_u, float *__restrict__ lse2_row,
-                                      float sum_lo, float sum_hi, float damp, int unbalanced,
+__device__ __forceinline__ int fz_row(const vf4 (&kk)[NV], double mu_r, double u_r, float rs,
+                                      const vf4 *lv_s, const vf4 *cs_s,
+                                      const vf4 (&wv)[NV], float2 (*rowpart)[W],
+                                      double (*rowsum)[W], int par, int w, int lane, int64_t r,
+                                      const FzRowOut &out, float sum_lo, float sum_hi,
+                                      double damp, int unbalanced,
                                       float (&cm)[EXACT ? 4 * NV : 1], float (&cs)[4 * NV]) {
     // u_r and rs were read with the row, before the row barrier after which
-    // wave 0 rewrites log_u[r] and lse2_row[r]
-    if (skip)
-        return par;  // lse = -inf: log_u keeps its value, and K is -inf on the row
-    Lse tot{0.f, 0.f};
+    // wave 0 rewrites the row's potential and shift
+    double l2 = 0.0;
     bool have = false;
     if constexpr (!EXACT) {
+        // lane sums in float32, the wave's and the row's sums in float64
+        // (wave_sum_all_d)
         float s = 0.f;
 #pragma unroll
         for (int k = 0; k < NV; ++k) {
-            const vf4 lv = lv_s[(k * W + w) * 64 + lane];
-            s += __builtin_amdgcn_exp2f(fmaf(kk[k].x, kLog2e, lv.x) - rs);
-            s += __builtin_amdgcn_exp2f(fmaf(kk[k].y, kLog2e, lv.y) - rs);
-            s += __builtin_amdgcn_exp2f(fmaf(kk[k].z, kLog2e, lv.z) - rs);
-            s += __builtin_amdgcn_exp2f(fmaf(kk[k].w, kLog2e, lv.w) - rs);
+            const vf4 y = kk[k] + lv_s[(k * W + w) * 64 + lane];
+            s = fmaf(__builtin_amdgcn_exp2f(y.x - rs), wv[k].x, s);
+            s = fmaf(__builtin_amdgcn_exp2f(y.y - rs), wv[k].y, s);
+            s = fmaf(__builtin_amdgcn_exp2f(y.z - rs), wv[k].z, s);
+            s = fmaf(__builtin_amdgcn_exp2f(y.w - rs), wv[k].w, s);
         }
-        s = wave_sum_all(s);
+        double s64 = wave_sum_all_d((double)s);
         if constexpr (W > 1) {  // the W waves' sums, added in LDS in wave order
             if (lane == 0)
-                rowpart[par][w].x = s;
+                rowsum[par][w] = s64;
             __syncthreads();
-            s = rowpart[par][0].x;
+            s64 = rowsum[par][0];
 #pragma unroll
             for (int k = 1; k < W; ++k)
-                s += rowpart[par][k].x;
+                s64 += rowsum[par][k];
             par ^= 1;
         }
-        if (s >= sum_lo && s <= sum_hi) {  // block-uniform; false for NaN
-            tot = Lse{rs, s};
+        if (s64 >= (double)sum_lo && s64 <= (double)sum_hi) {  // block-uniform; false for NaN
+            l2 = log2_of_sum(s64) + (double)rs;
             have = true;
         }
     }
-    if (!have)
-        par = fz_row_exact<W, NV>(kk, lv_s, rowpart, par, w, lane, tot);
-    const float lse2 = lse2_log2(tot);
-    const float lu = update_potential(ln_of_lse2(lse2), mu_r, u_r, damp, unbalanced != 0);
-    if (w == 0 && lane == 0) {
-        log_u[r] = lu;
-        lse2_row[r] = lse2;
+    if (!have) {
+        Lse tot;
+        par = fz_row_exact<W, NV>(kk, lv_s, wv, rowpart, par, w, lane, tot);
+        l2 = log2_split(tot.s) + (double)lse_shift(tot.m);
     }
-    const float lu2 = lu * kLog2e;
+    // the update in float64: nothing of the potential is rounded to float32
+    // between steps; the column sums below weight each term by the rounding
+    // residual of lu2
+    const double lu = update_potential64(l2, mu_r, u_r, damp, unbalanced != 0);
+    const float lu2 = (float)(lu * kLog2eD);
+    const float wr = potential_weight(lu, lu2);
+    if (w == 0 && lane == 0) {
+        out.lu64[r] = lu;
+        out.log_u[r] = (float)lu;
+        out.lu2[r] = lu2;
+        out.lse2_row[r] = (float)l2;
+    }
     if constexpr (EXACT) {
 #pragma unroll
         for (int k = 0; k < NV; ++k) {
-            col_fold2(cm[4 * k + 0], cs[4 * k + 0], fmaf(kk[k].x, kLog2e, lu2));
-            col_fold2(cm[4 * k + 1], cs[4 * k + 1], fmaf(kk[k].y, kLog2e, lu2));
-            col_fold2(cm[4 * k + 2], cs[4 * k + 2], fmaf(kk[k].z, kLog2e, lu2));
-            col_fold2(cm[4 * k + 3], cs[4 * k + 3], fmaf(kk[k].w, kLog2e, lu2));
+            const vf4 y = kk[k] + lu2;
+            col_fold2(cm[4 * k + 0], cs[4 * k + 0], y.x);
+            col_fold2(cm[4 * k + 1], cs[4 * k + 1], y.y);
+            col_fold2(cm[4 * k + 2], cs[4 * k + 2], y.z);
+            col_fold2(cm[4 * k + 3], cs[4 * k + 3], y.w);
         }
     } else {
 #pragma unroll
         for (int k = 0; k < NV; ++k) {
-            const vf4 c = cs_s[(k * W + w) * 64 + lane];
-            cs[4 * k + 0] += __builtin_amdgcn_exp2f(fmaf(kk[k].x, kLog2e, lu2) - c.x);
-            cs[4 * k + 1] += __builtin_amdgcn_exp2f(fmaf(kk[k].y, kLog2e, lu2) - c.y);
-            cs[4 * k + 2] += __builtin_amdgcn_exp2f(fmaf(kk[k].z, kLog2e, lu2) - c.z);
-            cs[4 * k + 3] += __builtin_amdgcn_exp2f(fmaf(kk[k].w, kLog2e, lu2) - c.w);
+            const vf4 y = (kk[k] + lu2) - cs_s[(k * W + w) * 64 + lane];
+            cs[4 * k + 0] = fmaf(__builtin_amdgcn_exp2f(y.x), wr, cs[4 * k + 0]);
+            cs[4 * k + 1] = fmaf(__builtin_amdgcn_exp2f(y.y), wr, cs[4 * k + 1]);
+            cs[4 * k + 2] = fmaf(__builtin_amdgcn_exp2f(y.z), wr, cs[4 * k + 2]);
+            cs[4 * k + 3] = fmaf(__builtin_amdgcn_exp2f(y.w), wr, cs[4 * k + 3]);
         }
     }
     return par;
@@ -1027,21 +1148,24 @@ __device__ __forceinline__ int fz_row(const vf4 (&kk)[NV], float mu_r, float u_r
 // last row.  NB: row buffers per wave.  colpart receives one float per column
 // (the sum against the shift c_j, which every chunk shares), or with EXACT the
 // exact running (max, sum) pair of col_fold2 (the first step, and the first
-// after an epsilon change, have no usable shift).  Requires M % 4 == 0,
-// M <= 256*W*NV, 16-byte aligned K and log_v.
+// after an epsilon change, have no usable shift).  K holds the base-2 log
+// kernel -C'*log2(e)/e and lv2 the kLog2eD-scaled log_v.  Requires M % 4 == 0,
+// M <= 256*W*NV, 16-byte aligned K and lv2.
 template <int W, int RW, int NV, int NB, bool EXACT, bool NT>
 __global__ void __launch_bounds__(W * RW * 64)
-sk_fused_step(const float *__restrict__ K, const float *__restrict__ log_v,
-              const float *__restrict__ lse2_col, float *__restrict__ lse2_row,
-              const float *__restrict__ log_mu, const uint8_t *__restrict__ inf_row,
-              float *__restrict__ log_u, float2 *__restrict__ colpart, int64_t N, int64_t M,
-              int n_chunk, int rows_per_chunk, int interleave, float sum_lo, float sum_hi,
-              float damp, int unbalanced) {
+sk_fused_step(const float *__restrict__ K, const float *__restrict__ lv2,
+              const float *__restrict__ lvw, const float *__restrict__ lse2_col,
+              float *__restrict__ lse2_row,
+              const double *__restrict__ mu64, double *__restrict__ lu64, float *__restrict__ log_u, float *__restrict__ lu2,
+              float2 *__restrict__ colpart, int64_t N, int64_t M, int n_chunk,
+              int rows_per_chunk, int interleave, float sum_lo, float sum_hi, double damp,
+              int unbalanced) {
     static_assert(W == 1 || RW == 1, "a row is split over waves only with one row group");
     constexpr int MV = W * 64 * NV;  // float4 per row at most
     __shared__ vf4 lv_s[MV];         // log_v * log2(e) of the batch, -inf past M
     __shared__ vf4 cs_s[MV];         // column shifts c_j (base 2)
     __shared__ float2 rowpart[2][W];
+    __shared__ double rowsum[2][W];
     const int chunk = blockIdx.x;
     const int64_t b = blockIdx.y;
     // wave-uniform (readfirstlane): row addresses and loop bounds stay scalar
@@ -1066,6 +1190,15 @@ sk_fused_step(const float *__restrict__ K, const float *__restrict__ log_v,
         qok[k] = q < m4;
         qb[k] = 16u * (uint32_t)(qok[k] ? q : (int)m4 - 1);
     }
+    // the lane's columns' weights (potential_weight of log_v): lane-private,
+    // so held in registers for the whole pass
+    vf4 wv[NV];
+    {
+        const vf4 *w4 = reinterpret_cast<const vf4 *>(lvw + b * M);
+#pragma unroll
+        for (int k = 0; k < NV; ++k)
+            wv[k] = qok[k] ? w4[(k * W + w) * 64 + lane] : vf4{1.f, 1.f, 1.f, 1.f};
+    }
     float cs[4 * NV], cm[EXACT ? 4 * NV : 1];
 #pragma unroll
     for (int k = 0; k < 4 * NV; ++k)
@@ -1075,30 +1208,37 @@ sk_fused_step(const float *__restrict__ K, const float *__restrict__ log_v,
         cm[k] = kFltMaxNeg;
     const vf4 *Kb4 = reinterpret_cast<const vf4 *>(K + b * N * M);
     const int64_t rb = b * N;
+    const FzRowOut out{lu64, log_u, lu2, lse2_row};
     int par = 0;
     int64_t i = first;
     // NB row buffers: a wave keeps NB - 1 rows' loads in flight while it
     // reduces one (NB = 1: the next row's loads go out once a row is folded)
     vf4 kr[NB][NV];
-    float rmu[NB], ru[NB], rls[NB];
-    int rskip[NB];
+    double rmu[NB], ru[NB];
+    float rls[NB];
 #define TM_FZ_LOAD(P_, I_)                                                                    \
-    fz_load<NV, NT>(kr[P_], rmu[P_], ru[P_], rls[P_], rskip[P_], Kb4 + (I_) * m4, qb,        \
-                    rb + (I_), log_mu, log_u, lse2_row, inf_row)
+    fz_load<NV, NT>(kr[P_], rmu[P_], ru[P_], rls[P_], Kb4 + (I_) * m4, qb, rb + (I_), mu64, \
+                    lu64, lse2_row)
+    // the wave's last row; prefetches past it load it again, so that every
+    // path through the loop issues the same loads and the wait for a row's
+    // data can leave the rows prefetched after it in flight (a conditional
+    // prefetch makes the compiler wait for every outstanding load instead)
+    const int64_t last = i < end ? first + ((end - 1 - first) / step) * step : first;
     if constexpr (NB == 1) {
         if (i < end)
             TM_FZ_LOAD(0, i);
     } else {
+        if (i < end) {
 #pragma unroll
-        for (int p = 0; p < NB - 1; ++p)
-            if (i + p * step < end)
-                TM_FZ_LOAD(p, i + p * step);
+            for (int p = 0; p < NB - 1; ++p)
+                TM_FZ_LOAD(p, i + p * step <= last ? i + p * step : last);
+        }
     }
-    const float4 *lv4 = reinterpret_cast<const float4 *>(log_v + b * M);
+    const float4 *lv4 = reinterpret_cast<const float4 *>(lv2 + b * M);
     const float4 *cs4 = reinterpret_cast<const float4 *>(lse2_col + b * M);
     for (int q = threadIdx.x; q < MV; q += W * RW * 64) {
         const float4 v = q < m4 ? lv4[q] : make_float4(-f_inf(), -f_inf(), -f_inf(), -f_inf());
-        lv_s[q] = vf4{v.x * kLog2e, v.y * kLog2e, v.z * kLog2e, v.w * kLog2e};
+        lv_s[q] = vf4{v.x, v.y, v.z, v.w};
         const float4 c = q < m4 ? cs4[q] : make_float4(0.f, 0.f, 0.f, 0.f);
         cs_s[q] = vf4{c.x, c.y, c.z, c.w};
     }
@@ -1106,9 +1246,9 @@ sk_fused_step(const float *__restrict__ K, const float *__restrict__ log_v,
 
     if constexpr (NB == 1) {
         for (; i < end; i += step) {
-            par = fz_row<W, NV, EXACT>(kr[0], rmu[0], ru[0], rls[0], rskip[0], lv_s, cs_s,
-                                       rowpart, par, w, lane, rb + i, log_u, lse2_row, sum_lo,
-                                       sum_hi, damp, unbalanced, cm, cs);
+            par = fz_row<W, NV, EXACT>(kr[0], rmu[0], ru[0], rls[0], lv_s, cs_s, wv,
+                                       rowpart, rowsum, par, w, lane, rb + i, out, sum_lo, sum_hi,
+                                       damp, unbalanced, cm, cs);
             if (i + step < end)
                 TM_FZ_LOAD(0, i + step);
         }
@@ -1116,16 +1256,14 @@ sk_fused_step(const float *__restrict__ K, const float *__restrict__ log_v,
         while (i < end) {
 #pragma unroll
             for (int p = 0; p < NB; ++p) {
-                if (i < end) {
-                    const int64_t ia = i + (int64_t)(NB - 1) * step;
-                    if (ia < end)
-                        TM_FZ_LOAD((p + NB - 1) % NB, ia);
-                    par = fz_row<W, NV, EXACT>(kr[p], rmu[p], ru[p], rls[p], rskip[p], lv_s,
-                                               cs_s, rowpart, par, w, lane, rb + i, log_u,
-                                               lse2_row, sum_lo, sum_hi, damp, unbalanced, cm,
-                                               cs);
-                    i += step;
-                }
+                const int64_t ia = i + (int64_t)(NB - 1) * step;
+                TM_FZ_LOAD((p + NB - 1) % NB, ia <= last ? ia : last);
+                par = fz_row<W, NV, EXACT>(kr[p], rmu[p], ru[p], rls[p], lv_s, cs_s, wv, rowpart,
+                                           rowsum, par, w, lane, rb + i, out,
+                                           sum_lo, sum_hi, damp, unbalanced, cm, cs);
+                i += step;
+                if (i >= end)
+                    break;
             }
         }
     }
@@ -1200,21 +1338,33 @@ sk_fused_step(const float *__restrict__ K, const float *__restrict__ log_v,
     }
 }
 
+// Outputs of the merge's column update (column t): the float64 potential,
+// its float32 copy (the caller's log_v), its kLog2eD-scaled float32 (the next
+// pass's lv2) and the base-2 LSE (the next step's shift).
+struct MergeOut {
+    double *lv64;
+    float *log_v;
+    float *lv2;
+    float *lvw;  // potential_weight of the column's lv2
+    float *lse2_col;
+};
+
 // grid (ceil(M/64), B), MW waves (16 for many chunks, else 4): lanes are 64
 // consecutive columns (coalesced 512-byte reads of one chunk), wave w merges
-// the partials of chunks w, w+MW, ..., and the waves merge in LDS.  With
-// shifted partials (exact = 0) a column whose total lies outside
-// [sum_lo, sum_hi] = [2^-16, 2^16] (its shift was stale) is recomputed
-// exactly: the block then folds its 64 columns of every row of K with the
-// step's final log_u (wave w takes rows w, w+MW, ...).  Wave 0 updates log_v
-// and stores each column's base-2 LSE as the next step's shift.
+// the partials of chunks w, w+MW, ..., and the waves merge in LDS.  Shifted
+// partials (exact = 0) share the column's shift and are added in float64; a
+// column whose total lies outside [sum_lo, sum_hi] = [2^-16, 2^16] (its shift
+// was stale) is recomputed exactly: the block then folds its 64 columns of
+// every row of K with the step's final lu2 (wave w takes rows w, w+MW, ...).
+// Wave 0 updates the column's potential in float64 and stores its base-2 LSE
+// as the next step's shift.
 template <int kMergeWaves>
 __global__ void __launch_bounds__(kMergeWaves * 64)
 sk_col_merge_blk(const float2 *__restrict__ colpart, const float *__restrict__ K,
-                 const float *__restrict__ log_u, const float *__restrict__ log_nu,
-                 const uint8_t *__restrict__ inf_col, float *__restrict__ log_v,
-                 float *__restrict__ lse2_col, int64_t N, int64_t M, int n_chunk, int exact,
-                 float sum_lo, float sum_hi, float damp, int unbalanced) {
+                 const float *__restrict__ lu2, const double *__restrict__ nu64,
+                 const uint8_t *__restrict__ inf_col, MergeOut out, int64_t N, int64_t M,
+                 int n_chunk, int exact, float sum_lo, float sum_hi, double damp,
+                 int unbalanced) {
     const int64_t b = blockIdx.y;
     const int w = (int)(threadIdx.x >> 6);
     const int lane = lane_id();
@@ -1223,11 +1373,16 @@ sk_col_merge_blk(const float2 *__restrict__ colpart, const float *__restrict__ K
     const int64_t t = b * M + jj;
     // the column's own values are loaded before the partials, so that their
     // latency overlaps the partials' instead of following the LDS merge
-    const float nu_t = log_nu[t], v_t = log_v[t];
+    const double nu_t = nu64[t], v_t = out.lv64[t];
+    const float c_t = out.lse2_col[t];
     const bool live = j < M && !inf_col[t];
-    Lse acc{-f_inf(), 0.f};
+    __shared__ float2 part[kMergeWaves][64];
+    __shared__ double part64[kMergeWaves][64];
     int c = w;
+    double l2;
+    bool ok = true;
     if (exact) {  // (max, sum) pairs
+        Lse acc{-f_inf(), 0.f};
         for (; c + 3 * kMergeWaves < n_chunk; c += 4 * kMergeWaves) {
             float2 p[4];
 #pragma unroll
@@ -1241,36 +1396,39 @@ sk_col_merge_blk(const float2 *__restrict__ colpart, const float *__restrict__ K
             const float2 p = colpart[(b * n_chunk + c) * M + jj];
             acc = lse2_merge(acc, Lse{p.x, p.y});
         }
-    } else {  // sums against the column's shift: plain adds
+        part[w][lane] = make_float2(acc.m, acc.s);
+        __syncthreads();
+#pragma unroll
+        for (int k = 0; k < kMergeWaves; ++k)
+            if (k != w)
+                acc = lse2_merge(acc, Lse{part[k][lane].x, part[k][lane].y});
+        l2 = log2_split(acc.s) + (double)lse_shift(acc.m);
+    } else {  // sums against the column's shift: plain adds, in float64
         const float *sum = reinterpret_cast<const float *>(colpart);
-        float t = 0.f;
+        double tsum = 0.0;
         for (; c + 3 * kMergeWaves < n_chunk; c += 4 * kMergeWaves) {
             float p[4];
 #pragma unroll
             for (int u = 0; u < 4; ++u)
                 p[u] = sum[(b * n_chunk + c + u * kMergeWaves) * M + jj];
-            t += (p[0] + p[1]) + (p[2] + p[3]);
+            tsum += ((double)p[0] + (double)p[1]) + ((double)p[2] + (double)p[3]);
         }
         for (; c < n_chunk; c += kMergeWaves)
-            t += sum[(b * n_chunk + c) * M + jj];
-        acc = Lse{lse2_col[b * M + jj], t};
-    }
-    __shared__ float2 part[kMergeWaves][64];
-    part[w][lane] = make_float2(acc.m, acc.s);
-    __syncthreads();
+            tsum += (double)sum[(b * n_chunk + c) * M + jj];
+        part64[w][lane] = tsum;
+        __syncthreads();
+        tsum = part64[0][lane];
 #pragma unroll
-    for (int k = 0; k < kMergeWaves; ++k)
-        if (k != w)
-            acc = lse2_merge(acc, Lse{part[k][lane].x, part[k][lane].y});
-    // exact partials are (max, sum) pairs, whose merge needs no check
-    const bool ok = exact || (acc.s >= sum_lo && acc.s <= sum_hi);  // false for NaN
-    float lse2 = lse2_log2(acc);
+        for (int k = 1; k < kMergeWaves; ++k)
+            tsum += part64[k][lane];
+        ok = tsum >= (double)sum_lo && tsum <= (double)sum_hi;  // false for NaN
+        l2 = ok ? log2_of_sum(tsum) + (double)c_t : 0.0;
+    }
     if (__syncthreads_or(live && !ok)) {
         float m = kFltMaxNeg, s = 0.f;
         const float *col = K + b * N * M + jj;
         for (int64_t i = w; i < N; i += kMergeWaves)
-            col_fold2(m, s, fmaf(col[i * M], kLog2e, log_u[b * N + i] * kLog2e));
-        __syncthreads();  // part[] is read above by every wave
+            col_fold2(m, s, col[i * M] + lu2[b * N + i]);
         part[w][lane] = make_float2(m, s);
         __syncthreads();
         Lse ex = fold_partial(part[0][lane].x, part[0][lane].y);
@@ -1278,12 +1436,17 @@ sk_col_merge_blk(const float2 *__restrict__ colpart, const float *__restrict__ K
         for (int k = 1; k < kMergeWaves; ++k)
             ex = lse2_merge(ex, fold_partial(part[k][lane].x, part[k][lane].y));
         if (!ok)
-            lse2 = lse2_log2(ex);
+            l2 = log2_split(ex.s) + (double)lse_shift(ex.m);
     }
     if (w != 0 || !live)
         return;
-    lse2_col[t] = lse2;
-    log_v[t] = update_potential(ln_of_lse2(lse2), nu_t, v_t, damp, unbalanced != 0);
+    const double lv = update_potential64(l2, nu_t, v_t, damp, unbalanced != 0);
+    const float lv2 = (float)(lv * kLog2eD);
+    out.lse2_col[t] = (float)l2;
+    out.lv64[t] = lv;
+    out.log_v[t] = (float)lv;
+    out.lv2[t] = lv2;
+    out.lvw[t] = potential_weight(lv, lv2);
 }
 
 // ---- final plan -------------------------------------------------------------------
@@ -1330,6 +1493,55 @@ sk_plan(const float *__restrict__ K, const float *__restrict__ log_u,
     }
 }
 
+// The fused step's plan: log_plan[b,i,j] = lu64[b,i] + Kref[b,i,j] + lv64[b,j]
+// in float64, rounded once, with Kref = -C'/e_final the reference's float32
+// K (IEEE division; C' = +inf where the keep mask is false).  Float4 steps
+// when `vec` (M % 4 == 0; C, plan 16-byte and keep 4-byte aligned).
+template <bool MASK>
+__global__ void __launch_bounds__(kMapBlock)
+sk_plan64(const float *__restrict__ C, const uint8_t *__restrict__ keep,
+          const double *__restrict__ lu64, const double *__restrict__ lv64,
+          float *__restrict__ plan, int64_t B, int64_t N, int64_t M, float e, int vec) {
+    const int64_t stride = (int64_t)gridDim.x * kMapBlock;
+    if (vec) {
+        const int64_t m4 = M / 4;
+        const int64_t n4 = B * N * m4;
+        const float4 *c4 = reinterpret_cast<const float4 *>(C);
+        const uint32_t *kp4 = reinterpret_cast<const uint32_t *>(keep);
+        float4 *p4 = reinterpret_cast<float4 *>(plan);
+        for (int64_t k = (int64_t)blockIdx.x * kMapBlock + threadIdx.x; k < n4; k += stride) {
+            const int64_t row = k / m4;
+            const int64_t q = k - row * m4;
+            const int64_t b = row / N;
+            const double u = lu64[row];
+            const double *v = lv64 + b * M + 4 * q;
+            float4 c = c4[k];
+            if (MASK) {
+                const uint32_t kp = kp4[k];
+                c.x = (kp & 0xffu) ? c.x : f_inf();
+                c.y = (kp & 0xff00u) ? c.y : f_inf();
+                c.z = (kp & 0xff0000u) ? c.z : f_inf();
+                c.w = (kp & 0xff000000u) ? c.w : f_inf();
+            }
+            float4 o;
+            o.x = (float)((u + (double)(-c.x / e)) + v[0]);
+            o.y = (float)((u + (double)(-c.y / e)) + v[1]);
+            o.z = (float)((u + (double)(-c.z / e)) + v[2]);
+            o.w = (float)((u + (double)(-c.w / e)) + v[3]);
+            p4[k] = o;
+        }
+        return;
+    }
+    const int64_t n = B * N * M;
+    for (int64_t k = (int64_t)blockIdx.x * kMapBlock + threadIdx.x; k < n; k += stride) {
+        const int64_t row = k / M;
+        const int64_t j = k - row * M;
+        const int64_t b = row / N;
+        const float c = (MASK && keep[k] == 0) ? f_inf() : C[k];
+        plan[k] = (float)((lu64[row] + (double)(-c / e)) + lv64[b * M + j]);
+    }
+}
+
 int grid_for(int64_t n, int block, int cap) {
     int64_t g = (n + block - 1) / block;
     if (g < 1)
@@ -1363,25 +1575,63 @@ bool shape_supported(const SinkhornLayout &L) {
            L.B * L.N <= 0x7fffffff;
 }
 
+// K for one epsilon: the reference's -C'/e (two-sweep step), or with `base2`
+// the fused step's -C'*log2(e)/e.
 int launch_log_kernel(const float *cost, const uint8_t *keep, float *K, int64_t nK, float e,
-                      hipStream_t stream) {
+                      bool base2, hipStream_t stream) {
+    const double s2 = base2 ? -kLog2eD / (double)e : 0.0;
     const int vec = ((uintptr_t)cost % 16) == 0 && ((uintptr_t)K % 16) == 0 &&
                     ((uintptr_t)keep % 4) == 0;
     const dim3 grid(grid_for(nK / 4 + 1, kMapBlock, 8192));
     if (keep != nullptr)
         TM_LAUNCH(sk_log_kernel<true>, grid, dim3(kMapBlock), 0, stream, cost, keep, K, nK, e,
-                  vec);
+                  s2, vec);
     else
         TM_LAUNCH(sk_log_kernel<false>, grid, dim3(kMapBlock), 0, stream, cost, keep, K, nK, e,
-                  vec);
+                  s2, vec);
     return TM_OK;
 }
 
-int launch_fused_step(const SinkhornLayout &L, bool exact, const float *K, float *log_v,
-                      float *lse2_col, float *lse2_row, const float *log_mu,
-                      const uint8_t *inf_row, float *log_u, const float *log_nu,
-                      const uint8_t *inf_col, float2 *colpart, float damp, int ub,
-                      hipStream_t stream) {
+// The fused step's arrays of one batch group (batches from b0 on).
+struct FusedPtrs {
+    const float *K;
+    float *lv2, *lvw, *lse2_col, *lse2_row, *log_u, *lu2, *log_v;
+    const double *mu64, *nu64;
+    double *lu64, *lv64;
+    const uint8_t *inf_row, *inf_col;
+    float2 *colpart;
+};
+
+FusedPtrs fused_ptrs(const SinkhornLayout &L, char *ws, float *log_u, float *log_v, int64_t b0) {
+    const int64_t N = L.N, M = L.M;
+    FusedPtrs P;
+    P.K = reinterpret_cast<const float *>(ws + L.off_k) + b0 * N * M;
+    P.lv2 = reinterpret_cast<float *>(ws + L.off_lv2) + b0 * M;
+    P.lvw = reinterpret_cast<float *>(ws + L.off_lvw) + b0 * M;
+    P.lse2_col = reinterpret_cast<float *>(ws + L.off_lse2col) + b0 * M;
+    P.lse2_row = reinterpret_cast<float *>(ws + L.off_lse2row) + b0 * N;
+    P.lu2 = reinterpret_cast<float *>(ws + L.off_lu2) + b0 * N;
+    P.log_u = log_u + b0 * N;
+    P.log_v = log_v + b0 * M;
+    P.mu64 = reinterpret_cast<const double *>(ws + L.off_mu64) + b0 * N;
+    P.nu64 = reinterpret_cast<const double *>(ws + L.off_nu64) + b0 * M;
+    P.lu64 = reinterpret_cast<double *>(ws + L.off_lu64) + b0 * N;
+    P.lv64 = reinterpret_cast<double *>(ws + L.off_lv64) + b0 * M;
+    P.inf_row = reinterpret_cast<const uint8_t *>(ws + L.off_infrow) + b0 * N;
+    P.inf_col = reinterpret_cast<const uint8_t *>(ws + L.off_infcol) + b0 * M;
+    P.colpart = reinterpret_cast<float2 *>(ws + L.off_colpart) + b0 * (int64_t)L.fz_chunk * M;
+    return P;
+}
+
+// The fused step runs when the row length has a shape and K (the start of
+// the workspace) is 16-byte aligned; everything else it reads is in the
+// workspace at 256-byte offsets.
+bool fused_ok(const SinkhornLayout &L, const void *workspace) {
+    return L.fused != kFzNone && ((uintptr_t)workspace % 16) == 0 && L.fz_chunk <= 0x7fffffff;
+}
+
+int launch_fused_step(const SinkhornLayout &L, bool exact, const FusedPtrs &P, double damp,
+                      int ub, hipStream_t stream) {
     // TORCHMATCH_AMD_SINKHORN_SHIFT_WINDOW narrows the accepted |LSE - shift|
     // of rows and columns (base 2; default 16): "0" sends every row through
     // the exact two-pass and every column through the exact recompute, which
@@ -1396,9 +1646,10 @@ int launch_fused_step(const SinkhornLayout &L, bool exact, const float *K, float
     const bool nontemporal = (size_t)(L.B * L.N * L.M) * sizeof(float) > kNonTemporalBytes;
     const dim3 block(f.W * f.RW * 64);
 #define TM_FUSED1(W_, RW_, NV_, NB_, EX_, NT_)                                             \
-    TM_LAUNCH((sk_fused_step<W_, RW_, NV_, NB_, EX_, NT_>), grid, block, 0, stream, K, log_v, \
-              lse2_col, lse2_row, log_mu, inf_row, log_u, colpart, L.N, L.M, L.fz_chunk,     \
-              L.fz_rows, L.fz_interleave, sum_lo, sum_hi, damp, ub)
+    TM_LAUNCH((sk_fused_step<W_, RW_, NV_, NB_, EX_, NT_>), grid, block, 0, stream, P.K,      \
+              P.lv2, P.lvw, P.lse2_col, P.lse2_row, P.mu64, P.lu64, P.log_u, P.lu2,                 \
+              P.colpart, L.N, L.M, L.fz_chunk, L.fz_rows, L.fz_interleave, sum_lo, sum_hi,   \
+              damp, ub)
 #define TM_FUSED(W_, RW_, NV_, NB_)                                                         \
     do {                                                                                    \
         if (exact && nontemporal)                                                           \
@@ -1412,7 +1663,7 @@ int launch_fused_step(const SinkhornLayout &L, bool exact, const float *K, float
     } while (0)
     switch (L.fused) {
     case kFz1x4x4: TM_FUSED(1, 4, 4, 1); break;
-    case kFz1x4x8: TM_FUSED(1, 4, 8, 3); break;
+    case kFz1x4x8: TM_FUSED(1, 4, 8, 2); break;
     case kFz2x1x8: TM_FUSED(2, 1, 8, 1); break;
     case kFz4x1x8: TM_FUSED(4, 1, 8, 1); break;
     case kFz8x1x8: TM_FUSED(8, 1, 8, 2); break;
@@ -1424,14 +1675,15 @@ int launch_fused_step(const SinkhornLayout &L, bool exact, const float *K, float
 #undef TM_FUSED
 #undef TM_FUSED1
     const dim3 mgrid((unsigned)((L.M + 63) / 64), (unsigned)L.B);
+    const MergeOut mo{P.lv64, P.log_v, P.lv2, P.lvw, P.lse2_col};
     if (L.fz_chunk > 64)  // C5: 256 chunks, 10.2 us with 16 waves against 11.3 with 4
-        TM_LAUNCH(sk_col_merge_blk<16>, mgrid, dim3(16 * 64), 0, stream, colpart, K, log_u,
-                  log_nu, inf_col, log_v, lse2_col, L.N, L.M, L.fz_chunk, exact ? 1 : 0, sum_lo,
-                  sum_hi, damp, ub);
+        TM_LAUNCH(sk_col_merge_blk<16>, mgrid, dim3(16 * 64), 0, stream, P.colpart, P.K, P.lu2,
+                  P.nu64, P.inf_col, mo, L.N, L.M, L.fz_chunk, exact ? 1 : 0, sum_lo, sum_hi,
+                  damp, ub);
     else  // C4: 32 chunks, 5.0 us with 4 waves against 8.5 with 16
-        TM_LAUNCH(sk_col_merge_blk<4>, mgrid, dim3(4 * 64), 0, stream, colpart, K, log_u,
-                  log_nu, inf_col, log_v, lse2_col, L.N, L.M, L.fz_chunk, exact ? 1 : 0, sum_lo,
-                  sum_hi, damp, ub);
+        TM_LAUNCH(sk_col_merge_blk<4>, mgrid, dim3(4 * 64), 0, stream, P.colpart, P.K, P.lu2,
+                  P.nu64, P.inf_col, mo, L.N, L.M, L.fz_chunk, exact ? 1 : 0, sum_lo, sum_hi,
+                  damp, ub);
     return TM_OK;
 }
 
@@ -1537,12 +1789,16 @@ extern "C" int tm_sinkhorn_prepare_f32(const float *cost, const uint8_t *keep, c
     const int64_t n_flags = B * N > B * M ? B * N : B * M;
     TM_LAUNCH(sk_reset_flags, dim3(grid_for(n_flags, kMapBlock, 1 << 30)), dim3(kMapBlock), 0,
               stream, inf_row, B * N, inf_col, B * M, stats);
+    double *mu64 = L.fused ? reinterpret_cast<double *>(ws + L.off_mu64) : nullptr;
+    double *nu64 = L.fused ? reinterpret_cast<double *>(ws + L.off_nu64) : nullptr;
     TM_LAUNCH(sk_log_marginal, dim3(grid_for(B * N, kMapBlock, 1 << 30)), dim3(kMapBlock), 0,
-              stream, a, log_mu, B * N, stats, kFlagANeg);
+              stream, a, log_mu, mu64, B * N, stats, kFlagANeg);
     TM_LAUNCH(sk_log_marginal, dim3(grid_for(B * M, kMapBlock, 1 << 30)), dim3(kMapBlock), 0,
-              stream, b, log_nu, B * M, stats, kFlagBNeg);
+              stream, b, log_nu, nu64, B * M, stats, kFlagBNeg);
 
     const bool vec = (M % 4) == 0 && ((uintptr_t)cost % 16) == 0 && ((uintptr_t)keep % 4) == 0;
+    // the first step's K: base-2 when the iteration takes the fused step
+    const double s2 = (fused_ok(L, workspace) && k_eps > 0.f) ? -kLog2eD / (double)k_eps : 0.0;
     const int cw = vec ? 4 : 1;
     const dim3 grid((unsigned)((M + 64 * cw - 1) / (64 * cw)),
                     (unsigned)((row_groups + groups - 1) / groups), (unsigned)B);
@@ -1550,16 +1806,16 @@ extern "C" int tm_sinkhorn_prepare_f32(const float *cost, const uint8_t *keep, c
     const int g = (int)groups;
     if (vec && keep != nullptr)
         TM_LAUNCH((sk_prepare<true, true>), grid, block, 0, stream, cost, keep, K, inf_row,
-                  inf_col, stats, N, M, g, k_eps);
+                  inf_col, stats, N, M, g, k_eps, s2);
     else if (vec)
         TM_LAUNCH((sk_prepare<true, false>), grid, block, 0, stream, cost, keep, K, inf_row,
-                  inf_col, stats, N, M, g, k_eps);
+                  inf_col, stats, N, M, g, k_eps, s2);
     else if (keep != nullptr)
         TM_LAUNCH((sk_prepare<false, true>), grid, block, 0, stream, cost, keep, K, inf_row,
-                  inf_col, stats, N, M, g, k_eps);
+                  inf_col, stats, N, M, g, k_eps, s2);
     else
         TM_LAUNCH((sk_prepare<false, false>), grid, block, 0, stream, cost, keep, K, inf_row,
-                  inf_col, stats, N, M, g, k_eps);
+                  inf_col, stats, N, M, g, k_eps, s2);
     return TM_OK;
 }
 
@@ -1632,18 +1888,25 @@ extern "C" int tm_sinkhorn_iterate_f32(const float *cost, const uint8_t *keep, i
     const bool unbalanced = rho > 0.0;
     const int64_t nK = B * N * M;
     const bool vec = (M % 4) == 0 && ((uintptr_t)log_v % 16) == 0;
-    const bool fused = L.fused != kFzNone && vec && ((uintptr_t)K % 16) == 0 &&
-                       L.fz_chunk <= 0x7fffffff;
+    const bool fused = fused_ok(L, workspace);
 
     TM_LAUNCH(sk_fill, dim3(grid_for(B * N, kMapBlock, 1 << 30)), dim3(kMapBlock), 0, stream,
               log_u, B * N, 0.f);
     TM_LAUNCH(sk_fill, dim3(grid_for(B * M, kMapBlock, 1 << 30)), dim3(kMapBlock), 0, stream,
               log_v, B * M, 0.f);
-    float *lse2_col = reinterpret_cast<float *>(ws + L.off_lse2col);
-    float *lse2_row = reinterpret_cast<float *>(ws + L.off_lse2row);
-    if (fused)  // no column shift yet (the first step folds exactly)
-        TM_LAUNCH(sk_fill, dim3(grid_for(B * M, kMapBlock, 1 << 30)), dim3(kMapBlock), 0,
-                  stream, lse2_col, B * M, __builtin_nanf(""));
+    if (fused) {
+        // float64 potentials and their scaled float32 copies start at 0; no
+        // column shift yet (the first step folds exactly)
+        const FusedPtrs P = fused_ptrs(L, ws, log_u, log_v, 0);
+        const dim3 gn(grid_for(B * N, kMapBlock, 1 << 30)), gm(grid_for(B * M, kMapBlock, 1 << 30));
+        TM_LAUNCH(sk_fill64, gn, dim3(kMapBlock), 0, stream, P.lu64, B * N, 0.0);
+        TM_LAUNCH(sk_fill64, gm, dim3(kMapBlock), 0, stream, P.lv64, B * M, 0.0);
+        TM_LAUNCH(sk_fill, gn, dim3(kMapBlock), 0, stream, P.lu2, B * N, 0.f);
+        TM_LAUNCH(sk_fill, gm, dim3(kMapBlock), 0, stream, P.lv2, B * M, 0.f);
+        TM_LAUNCH(sk_fill, gm, dim3(kMapBlock), 0, stream, P.lvw, B * M, 1.f);
+        TM_LAUNCH(sk_fill, gm, dim3(kMapBlock), 0, stream, P.lse2_col, B * M,
+                  __builtin_nanf(""));
+    }
 
     const int64_t waves_per_batch = (N + kRowsPerWave - 1) / kRowsPerWave;
     const int64_t row_waves = B * waves_per_batch;
@@ -1665,7 +1928,7 @@ extern "C" int tm_sinkhorn_iterate_f32(const float *cost, const uint8_t *keep, i
             const float e = (float)eps_sched[s0];
             bool exact0 = s0 == 0;
             if (e != cur_eps) {
-                const int rc = launch_log_kernel(cost, keep, K, nK, e, stream);
+                const int rc = launch_log_kernel(cost, keep, K, nK, e, true, stream);
                 if (rc != TM_OK)
                     return rc;
                 cur_eps = e;
@@ -1685,16 +1948,14 @@ extern "C" int tm_sinkhorn_iterate_f32(const float *cost, const uint8_t *keep, i
             }
             int rc = TM_OK;
             for (int32_t s = s0; s < s1 && rc == TM_OK; ++s) {
-                const float damp = unbalanced ? (float)(1.0 / (1.0 + eps_sched[s] / rho)) : 1.f;
+                const double damp = unbalanced ? 1.0 / (1.0 + eps_sched[s] / rho) : 1.0;
                 for (int g = 0; g < G && rc == TM_OK; ++g) {
                     // group g: batches [b0, b1)
                     const int64_t b0 = g * L.B / G, b1 = (g + 1) * L.B / G;
                     SinkhornLayout Lg = L;
                     Lg.B = b1 - b0;
-                    rc = launch_fused_step(Lg, s == s0 && exact0, K + b0 * N * M, log_v + b0 * M,
-                                           lse2_col + b0 * M, lse2_row + b0 * N, log_mu + b0 * N,
-                                           inf_row + b0 * N, log_u + b0 * N, log_nu + b0 * M,
-                                           inf_col + b0 * M, colpart + b0 * L.fz_chunk * M, damp,
+                    rc = launch_fused_step(Lg, s == s0 && exact0,
+                                           fused_ptrs(L, ws, log_u, log_v, b0), damp,
                                            unbalanced ? 1 : 0, g == 0 ? stream : ss->s[g - 1]);
                 }
             }
@@ -1711,7 +1972,7 @@ extern "C" int tm_sinkhorn_iterate_f32(const float *cost, const uint8_t *keep, i
     for (int32_t s = 0; s < n_iter && !fused; ++s) {
         const float e = (float)eps_sched[s];
         if (e != cur_eps) {  // K holds -C / e for the step's epsilon
-            const int rc = launch_log_kernel(cost, keep, K, nK, e, stream);
+            const int rc = launch_log_kernel(cost, keep, K, nK, e, false, stream);
             if (rc != TM_OK)
                 return rc;
             cur_eps = e;
@@ -1753,7 +2014,19 @@ extern "C" int tm_sinkhorn_iterate_f32(const float *cost, const uint8_t *keep, i
                       0, stream, colpart, log_nu, inf_col, log_v, B, M, L.n_chunk, damp,
                       unbalanced ? 1 : 0);
     }
-    if (log_plan != nullptr) {
+    if (log_plan != nullptr && fused) {
+        const FusedPtrs P = fused_ptrs(L, ws, log_u, log_v, 0);
+        const float e_final = (float)eps_sched[n_iter - 1];
+        const int pvec = (M % 4) == 0 && ((uintptr_t)cost % 16) == 0 &&
+                         ((uintptr_t)keep % 4) == 0 && ((uintptr_t)log_plan % 16) == 0;
+        const dim3 pgrid(grid_for(pvec ? nK / 4 : nK, kMapBlock, 8192));
+        if (keep != nullptr)
+            TM_LAUNCH(sk_plan64<true>, pgrid, dim3(kMapBlock), 0, stream, cost, keep, P.lu64,
+                      P.lv64, log_plan, B, N, M, e_final, pvec);
+        else
+            TM_LAUNCH(sk_plan64<false>, pgrid, dim3(kMapBlock), 0, stream, cost, keep, P.lu64,
+                      P.lv64, log_plan, B, N, M, e_final, pvec);
+    } else if (log_plan != nullptr) {
         if (vec && ((uintptr_t)log_plan % 16) == 0)
             TM_LAUNCH(sk_plan4, dim3(grid_for(nK / 4, kMapBlock, 8192)), dim3(kMapBlock), 0,
                       stream, K, log_u, log_v, log_plan, B, N, M);

@@ -311,6 +311,37 @@ __device__ __forceinline__ float wave_sum_all(float x) {
     return a + o;
 }
 
+// float64 DPP move: the two 32-bit halves moved with the same control.
+template <int CTRL>
+__device__ __forceinline__ double dpp_full_d(double x) {
+    const uint64_t u = (uint64_t)__double_as_longlong(x);
+    const int lo = __builtin_amdgcn_mov_dpp((int)(uint32_t)u, CTRL, 0xF, 0xF, true);
+    const int hi = __builtin_amdgcn_mov_dpp((int)(uint32_t)(u >> 32), CTRL, 0xF, 0xF, true);
+    return __longlong_as_double((long long)(((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo));
+}
+
+// Sum over the whole wave in float64 (uniform result), the same butterfly as
+// wave_sum_all.  Adding 64 float32 lane sums in float32 loses the lanes that
+// fall below half an ulp of their partner, always downward: a sum whose
+// lanes span many orders of magnitude comes out biased low.
+__device__ __forceinline__ double wave_sum_all_d(double x) {
+    x += dpp_full_d<kDppQuadXor1>(x);
+    x += dpp_full_d<kDppQuadXor2>(x);
+    x += dpp_full_d<kDppRowHalfMirror>(x);
+    x += dpp_full_d<kDppRowMirror>(x);
+    const uint64_t u = (uint64_t)__double_as_longlong(x);
+    u32x2 lo = __builtin_amdgcn_permlane16_swap((uint32_t)u, (uint32_t)u, false, false);
+    u32x2 hi = __builtin_amdgcn_permlane16_swap((uint32_t)(u >> 32), (uint32_t)(u >> 32), false,
+                                                false);
+    x = __longlong_as_double((long long)(((uint64_t)hi[0] << 32) | lo[0])) +
+        __longlong_as_double((long long)(((uint64_t)hi[1] << 32) | lo[1]));
+    const uint64_t v = (uint64_t)__double_as_longlong(x);
+    lo = __builtin_amdgcn_permlane32_swap((uint32_t)v, (uint32_t)v, false, false);
+    hi = __builtin_amdgcn_permlane32_swap((uint32_t)(v >> 32), (uint32_t)(v >> 32), false, false);
+    return __longlong_as_double((long long)(((uint64_t)hi[0] << 32) | lo[0])) +
+           __longlong_as_double((long long)(((uint64_t)hi[1] << 32) | lo[1]));
+}
+
 __device__ __forceinline__ float wave_max_all(float x) {
     x = fmaxf(x, dpp_full_f<kDppQuadXor1>(x));
     x = fmaxf(x, dpp_full_f<kDppQuadXor2>(x));
