@@ -90,3 +90,17 @@ def test_f64_is_not_float32(device):
                                .double(), b=workloads.uniform_marginal(1, 64).double())[0]
     assert sk_parity.logp_err(p64, ref) <= TOL64
     assert (p64.cpu() - p32.double().cpu()).abs().max().item() > 1e-8
+
+
+def test_batch_above_grid_limit_f64(device):
+    """70,000 problems (more than one 65,535-block grid dimension holds): the
+    column kernel strides over (batch, strip) pairs."""
+    B, N, M = 70_000, 2, 3
+    cost = torch.rand(B, N, M, generator=torch.Generator().manual_seed(21), dtype=torch.float64)
+    a = torch.full((B, N), 1.0 / N, dtype=torch.float64)
+    b = torch.full((B, M), 1.0 / M, dtype=torch.float64)
+    ref = sk.log_sinkhorn_plan(cost, eps=0.1, n_iter=12, a=a, b=b)[0]
+    plan = torch.ops.transport.log_sinkhorn(cost.to(device), 0.1, 12, a.to(device), b.to(device))
+    ep = sk_parity.logp_err(plan, ref)
+    print(f"f64 B={B}: plan {ep:.2e}", flush=True)
+    assert ep <= TOL64

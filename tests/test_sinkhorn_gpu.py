@@ -304,3 +304,17 @@ def test_potentials_reconstruct_plan(device):
 def test_cpu_tensor_rejected():
     with pytest.raises(ValueError, match="ROCm"):
         solve(torch.rand(3, 3), reg=0.1, n_iter=5)
+
+
+@pytest.mark.parametrize(("N", "M"), [(3, 5), (4, 128)], ids=["two-sweep", "fused"])
+def test_batch_above_grid_limit(N, M, device):
+    """70,000 problems: the launches that put the batch on a grid dimension
+    (prepare, the fused step and its merge, the column sweep) run in slices."""
+    B = 70_000
+    cost = torch.rand(B, N, M, generator=torch.Generator().manual_seed(22))
+    a = workloads.uniform_marginal(B, N)
+    b = workloads.uniform_marginal(B, M)
+    r32 = sk.log_sinkhorn_plan(cost, eps=0.1, n_iter=8, a=a, b=b)
+    r64 = sk.log_sinkhorn_plan(cost, eps=0.1, n_iter=8, a=a, b=b, dtype=torch.float64)
+    plan = torch.ops.transport.log_sinkhorn(cost.to(device), 0.1, 8, a.to(device), b.to(device))
+    sk_parity.check(f"B={B} {(N, M)}", {"plan": plan}, {"plan": r32[0]}, {"plan": r64[0]})

@@ -566,8 +566,7 @@ sk_row_sweep(const float *__restrict__ K, const float *__restrict__ log_v,
     const int lane = lane_id();
     const int64_t m4 = M / 4;
     const float4 *lv4 = reinterpret_cast<const float4 *>(log_v + b * M);
-    constexpr int CH = 64 * kRowNV;  // float4 per chunk
-    {  // m4 <= CH here (longer rows take sk_row_sweep_split)
+    {  // m4 <= 64 * kRowNV here (longer rows take sk_row_sweep_split)
         float4 kk[kRowsPerWave][kRowNV];
 #pragma unroll
         for (int rr = 0; rr < kRowsPerWave; ++rr) {
@@ -1569,10 +1568,12 @@ namespace {
             return TM_ERR_LAUNCH;                                                         \
     } while (0)
 
-// Shape limits of the launch grids below.
+// Shape limits of the launch grids below.  Launches that put the batch on
+// a grid dimension run in slices of at most kBatchSlice problems (pointers
+// offset to the slice), so the batch size itself has no grid limit.
+constexpr int64_t kBatchSlice = 65535;
 bool shape_supported(const SinkhornLayout &L) {
-    return L.n_strip <= 0x7fffffff && L.n_chunk <= 65535 && L.B <= 65535 &&
-           L.B * L.N <= 0x7fffffff;
+    return L.n_strip <= 0x7fffffff && L.n_chunk <= 65535 && L.B * L.N <= 0x7fffffff;
 }
 
 // K for one epsilon: the reference's -C'/e (two-sweep step), or with `base2`
@@ -1589,6 +1590,36 @@ int launch_log_kernel(const float *cost, const uint8_t *keep, float *K, int64_t 
     else
         TM_LAUNCH(sk_log_kernel<false>, grid, dim3(kMapBlock), 0, stream, cost, keep, K, nK, e,
                   s2, vec);
+    return TM_OK;
+}
+
+// The two-sweep column sweep, batch slices on grid z.
+int launch_col_sweep(const SinkhornLayout &L, bool vec, const float *K, const float *log_u,
+                     const float *log_nu, const uint8_t *inf_col, float *log_v, float2 *colpart,
+                     float damp, int ub, hipStream_t stream) {
+    const int64_t N = L.N, M = L.M;
+    for (int64_t b0 = 0; b0 < L.B; b0 += kBatchSlice) {
+        const int64_t nb = L.B - b0 < kBatchSlice ? L.B - b0 : kBatchSlice;
+        const dim3 grid((unsigned)L.n_strip, (unsigned)L.n_chunk, (unsigned)nb);
+        const float *k = K + b0 * N * M;
+        const float *lu = log_u + b0 * N;
+        const float *ln = log_nu + b0 * M;
+        const uint8_t *ic = inf_col + b0 * M;
+        float *lv = log_v + b0 * M;
+        float2 *cp = colpart + b0 * L.n_chunk * M;
+#define TM_COL_SWEEP(V_, S_)                                                                  \
+    TM_LAUNCH((sk_col_sweep<V_, S_>), grid, dim3(kColThreads), 0, stream, k, lu, ln, ic, lv, cp, \
+              N, M, L.rows_per_chunk, L.n_chunk, damp, ub)
+        if (vec && L.strip == kColStripNarrow)
+            TM_COL_SWEEP(true, kColStripNarrow);
+        else if (vec)
+            TM_COL_SWEEP(true, kColStrip);
+        else if (L.strip == kColStripNarrow)
+            TM_COL_SWEEP(false, kColStripNarrow);
+        else
+            TM_COL_SWEEP(false, kColStrip);
+#undef TM_COL_SWEEP
+    }
     return TM_OK;
 }
 
@@ -1800,22 +1831,29 @@ extern "C" int tm_sinkhorn_prepare_f32(const float *cost, const uint8_t *keep, c
     // the first step's K: base-2 when the iteration takes the fused step
     const double s2 = (fused_ok(L, workspace) && k_eps > 0.f) ? -kLog2eD / (double)k_eps : 0.0;
     const int cw = vec ? 4 : 1;
-    const dim3 grid((unsigned)((M + 64 * cw - 1) / (64 * cw)),
-                    (unsigned)((row_groups + groups - 1) / groups), (unsigned)B);
     const dim3 block(kPrepWaves * 64);
     const int g = (int)groups;
-    if (vec && keep != nullptr)
-        TM_LAUNCH((sk_prepare<true, true>), grid, block, 0, stream, cost, keep, K, inf_row,
-                  inf_col, stats, N, M, g, k_eps, s2);
-    else if (vec)
-        TM_LAUNCH((sk_prepare<true, false>), grid, block, 0, stream, cost, keep, K, inf_row,
-                  inf_col, stats, N, M, g, k_eps, s2);
-    else if (keep != nullptr)
-        TM_LAUNCH((sk_prepare<false, true>), grid, block, 0, stream, cost, keep, K, inf_row,
-                  inf_col, stats, N, M, g, k_eps, s2);
-    else
-        TM_LAUNCH((sk_prepare<false, false>), grid, block, 0, stream, cost, keep, K, inf_row,
-                  inf_col, stats, N, M, g, k_eps, s2);
+    for (int64_t b0 = 0; b0 < B; b0 += kBatchSlice) {
+        const int64_t nb = B - b0 < kBatchSlice ? B - b0 : kBatchSlice;
+        const int64_t eo = b0 * N * M;
+        const float *c = cost + eo;
+        const uint8_t *kp = keep != nullptr ? keep + eo : nullptr;
+        uint8_t *ir = inf_row + b0 * N, *ic = inf_col + b0 * M;
+        const dim3 grid((unsigned)((M + 64 * cw - 1) / (64 * cw)),
+                        (unsigned)((row_groups + groups - 1) / groups), (unsigned)nb);
+        if (vec && keep != nullptr)
+            TM_LAUNCH((sk_prepare<true, true>), grid, block, 0, stream, c, kp, K + eo, ir, ic,
+                      stats, N, M, g, k_eps, s2);
+        else if (vec)
+            TM_LAUNCH((sk_prepare<true, false>), grid, block, 0, stream, c, kp, K + eo, ir, ic,
+                      stats, N, M, g, k_eps, s2);
+        else if (keep != nullptr)
+            TM_LAUNCH((sk_prepare<false, true>), grid, block, 0, stream, c, kp, K + eo, ir, ic,
+                      stats, N, M, g, k_eps, s2);
+        else
+            TM_LAUNCH((sk_prepare<false, false>), grid, block, 0, stream, c, kp, K + eo, ir, ic,
+                      stats, N, M, g, k_eps, s2);
+    }
     return TM_OK;
 }
 
@@ -1911,7 +1949,6 @@ extern "C" int tm_sinkhorn_iterate_f32(const float *cost, const uint8_t *keep, i
     const int64_t waves_per_batch = (N + kRowsPerWave - 1) / kRowsPerWave;
     const int64_t row_waves = B * waves_per_batch;
     const dim3 row_grid((unsigned)((row_waves + kRowWaves - 1) / kRowWaves));
-    const dim3 col_grid((unsigned)L.n_strip, (unsigned)L.n_chunk, (unsigned)B);
     float cur_eps = k_eps > 0.f ? k_eps : -1.f;  // the epsilon K currently holds
     if (fused) {
         // steps run in segments of one epsilon (K rebuilt on the caller's
@@ -1950,13 +1987,16 @@ extern "C" int tm_sinkhorn_iterate_f32(const float *cost, const uint8_t *keep, i
             for (int32_t s = s0; s < s1 && rc == TM_OK; ++s) {
                 const double damp = unbalanced ? 1.0 / (1.0 + eps_sched[s] / rho) : 1.0;
                 for (int g = 0; g < G && rc == TM_OK; ++g) {
-                    // group g: batches [b0, b1)
+                    // group g: batches [b0, b1), launched in slices
                     const int64_t b0 = g * L.B / G, b1 = (g + 1) * L.B / G;
-                    SinkhornLayout Lg = L;
-                    Lg.B = b1 - b0;
-                    rc = launch_fused_step(Lg, s == s0 && exact0,
-                                           fused_ptrs(L, ws, log_u, log_v, b0), damp,
-                                           unbalanced ? 1 : 0, g == 0 ? stream : ss->s[g - 1]);
+                    for (int64_t c0 = b0; c0 < b1 && rc == TM_OK; c0 += kBatchSlice) {
+                        SinkhornLayout Lg = L;
+                        Lg.B = b1 - c0 < kBatchSlice ? b1 - c0 : kBatchSlice;
+                        rc = launch_fused_step(Lg, s == s0 && exact0,
+                                               fused_ptrs(L, ws, log_u, log_v, c0), damp,
+                                               unbalanced ? 1 : 0,
+                                               g == 0 ? stream : ss->s[g - 1]);
+                    }
                 }
             }
             // join the side streams even after a failed launch
@@ -1988,26 +2028,18 @@ extern "C" int tm_sinkhorn_iterate_f32(const float *cost, const uint8_t *keep, i
             else
                 TM_LAUNCH((sk_row_sweep_split<8, 4>), split_grid, dim3(8 * 64), 0, stream, K,
                           log_v, log_mu, inf_row, log_u, N, M, damp, ub);
-            if (L.strip == kColStripNarrow)
-                TM_LAUNCH((sk_col_sweep<true, kColStripNarrow>), col_grid, dim3(kColThreads), 0,
-                          stream, K, log_u, log_nu, inf_col, log_v, colpart, N, M,
-                          L.rows_per_chunk, L.n_chunk, damp, unbalanced ? 1 : 0);
-            else
-                TM_LAUNCH((sk_col_sweep<true, kColStrip>), col_grid, dim3(kColThreads), 0,
-                          stream, K, log_u, log_nu, inf_col, log_v, colpart, N, M,
-                          L.rows_per_chunk, L.n_chunk, damp, unbalanced ? 1 : 0);
+            const int rc = launch_col_sweep(L, true, K, log_u, log_nu, inf_col, log_v, colpart,
+                                            damp, unbalanced ? 1 : 0, stream);
+            if (rc != TM_OK)
+                return rc;
         } else {
             TM_LAUNCH(sk_row_sweep_scalar, dim3(grid_for(B * N, 4, 1 << 30)), dim3(256), 0,
                       stream, K, log_v, log_mu, inf_row, log_u, B, N, M, damp,
                       unbalanced ? 1 : 0);
-            if (L.strip == kColStripNarrow)
-                TM_LAUNCH((sk_col_sweep<false, kColStripNarrow>), col_grid, dim3(kColThreads), 0,
-                          stream, K, log_u, log_nu, inf_col, log_v, colpart, N, M,
-                          L.rows_per_chunk, L.n_chunk, damp, unbalanced ? 1 : 0);
-            else
-                TM_LAUNCH((sk_col_sweep<false, kColStrip>), col_grid, dim3(kColThreads), 0,
-                          stream, K, log_u, log_nu, inf_col, log_v, colpart, N, M,
-                          L.rows_per_chunk, L.n_chunk, damp, unbalanced ? 1 : 0);
+            const int rc = launch_col_sweep(L, false, K, log_u, log_nu, inf_col, log_v,
+                                            colpart, damp, unbalanced ? 1 : 0, stream);
+            if (rc != TM_OK)
+                return rc;
         }
         if (L.n_chunk > 1)
             TM_LAUNCH(sk_col_merge, dim3(grid_for(B * M, kMapBlock, 1 << 30)), dim3(kMapBlock),
