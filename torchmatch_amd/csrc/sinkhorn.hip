@@ -15,23 +15,25 @@
 // The reference's -80 stand-in for all-+inf rows/columns only feeds lanes that
 // the reference then overwrites with -inf, so those sweeps are skipped here.
 //
-// HBM layout (row-major float32, resident for the whole call):
-//   K        (B, N, M)  log kernel, rewritten only when the schedule's epsilon
-//                       changes (once for a constant schedule)
-//   log_u/v  (B, N) / (B, M) the caller's outputs, updated in place every step
+// HBM layout (row-major, resident for the whole call):
+//   K        (B, N, M)  float32 log kernel, rewritten only when the schedule's
+//                       epsilon changes (once for a constant schedule): -C/e
+//                       for the two-sweep step, -C*log2(e)/e for the fused one
+//   log_u/v  (B, N) / (B, M) the caller's float32 outputs, written every step
 //   colpart  (B, n_chunk, M) column partials of row chunks: float sums (fused
 //                       step) or float2 (max, sum) pairs (exact fused step,
 //                       two-sweep column sweep with chunked rows)
-//   lse2_col (B, M)     each column's base-2 LSE of the previous fused step
-//   lse2_row (B, N)     each row's, the same
+//   fused step state: float64 potentials and log marginals, the potentials
+//                       scaled by log2(e) in float32 with their rounding
+//                       weights, each row's base-2 LSE of the previous step
 //
 // One step, in one of two forms:
 //   fused (sk_fused_step + sk_col_merge_blk; 128 <= M <= 16384, M % 4 == 0):
 //     K is read once.  Each row's LSE is reduced from registers, its log_u
-//     updated, and the same registers add the row into per-column sums
-//     against the previous step's column LSE; the merge adds the chunks'
-//     sums and recomputes exactly any column whose sum left the accepted
-//     window.  B*N*M*4 algorithmic bytes.
+//     updated in float64, and the row's terms, times one factor of the row,
+//     are added into per-column sums; the merge adds the chunks' sums and
+//     recomputes exactly any column whose total left the accepted window.
+//     B*N*M*4 algorithmic bytes.
 //   two-sweep (sk_row_sweep* + sk_col_sweep [+ sk_col_merge]): a row sweep
 //     and a column sweep each read K, 2 * B*N*M*4 bytes.
 //
@@ -158,8 +160,8 @@ struct SinkhornLayout {
     int fused;                   // FusedVariant of sk_fused_step, 0: two-sweep step
     int fz_chunk, fz_rows;       // its row chunks per batch and rows per chunk
     int fz_interleave;           // chunks take every n_chunk-th row (else a range)
-    size_t off_k, off_logmu, off_lognu, off_infrow, off_infcol, off_colpart, off_lse2col,
-        off_lse2row, off_stats, total;
+    size_t off_k, off_logmu, off_lognu, off_infrow, off_infcol, off_colpart, off_lse2row,
+        off_stats, total;
     // float64 state of the fused step: the potentials, the marginals' logs,
     // and the potentials scaled by kLog2e in float32 (what the element
     // loops add), B*N / B*M each
@@ -187,7 +189,7 @@ struct FusedShape {
     int W, RW, NV, blocks_per_cu;
 };
 constexpr FusedShape kFusedShapes[] = {
-    {0, 0, 0, 0}, {1, 4, 4, 5}, {1, 4, 8, 2}, {2, 1, 8, 4}, {4, 1, 8, 2}, {8, 1, 8, 1},
+    {0, 0, 0, 0}, {1, 4, 4, 4}, {1, 4, 8, 2}, {2, 1, 8, 4}, {4, 1, 8, 2}, {8, 1, 8, 1},
     {16, 1, 4, 1}, {1, 4, 1, 8}, {1, 4, 2, 8},
 };
 constexpr int kFusedMinRowsPerWave = 8;
@@ -271,9 +273,6 @@ SinkhornLayout make_layout(int64_t B, int64_t N, int64_t M) {
             parts = L.fz_chunk;
         off = align_up(off + sizeof(float2) * (size_t)B * (size_t)parts * (size_t)M, 256);
     }
-    L.off_lse2col = off;
-    if (L.fused)
-        off = align_up(off + sizeof(float) * (size_t)(B * M), 256);
     L.off_lse2row = off;
     if (L.fused)
         off = align_up(off + sizeof(float) * (size_t)(B * N), 256);
@@ -847,23 +846,19 @@ sk_col_merge(const float2 *__restrict__ colpart, const float *__restrict__ log_n
 // launched after the pass; the next step's row sweep needs that log_v, so the
 // merge cannot move into the pass.
 //
-// Both LSEs work in base 2 on the native v_exp_f32: y = t*log2(e) comes from
-// one fma of K with the potential scaled once (log_v per column in LDS, log_u
-// per row).
-//   row:    exact two-pass over the row in registers (max, then sum of
-//           2^(y - max)), as the reference's logsumexp;
-//   column: sum of 2^(y - c_j) with c_j the column's base-2 LSE of the previous
-//           step (lse2_col).  A shift is only a scale: the sum keeps its
-//           relative precision as long as it neither overflows nor underflows,
-//           and the merge accepts a column only when its total lies in
-//           [2^-16, 2^16] (so |LSE - c_j| <= 16 and log2 of the total adds at
-//           most 1e-6 of rounding); any other column is recomputed exactly
-//           from K by the merge.  Three VALU ops and one exp per value
-//           instead of the eight of an exact running max.  The first step,
-//           and the first after K changes, have no shift and take the exact
-//           running fold (EXACT instances).
-// v_exp_f32 issues at half the FMA rate; the pass needs about half of its
-// time in VALU issue and is bound by the rows in flight, not by arithmetic.
+// Both LSEs work in base 2 on the native v_exp_f32, with K already in base-2
+// units: y = K + p2 for the potential p2 scaled once (log_v per column in LDS,
+// log_u per row).
+//   row:    the sum of 2^(y - rs) against the row's LSE of the previous step
+//           (a shift is only a scale: the sum keeps its relative precision
+//           while it neither overflows nor underflows; accepted in [2^-16,
+//           2^16]), else the exact two-pass (max, then sum of 2^(y - max)),
+//           the reference's logsumexp;
+//   column: the same terms times one per-row factor (fz_row), so a value costs
+//           one add, one subtract, one exp and two fma in all.
+// The first step, and the first after K changes, fold the columns with an
+// exact running (max, sum) instead (EXACT instances).  v_exp_f32 issues at
+// half the FMA rate.
 
 constexpr float kFltMaxNeg = -3.402823466e38f;
 constexpr float kShiftWindow = 16.f;  // accepted |LSE - shift|, base 2
@@ -941,6 +936,18 @@ __device__ __forceinline__ double log2_of_sum(double s) {
     const float h = (float)s;
     const float r = (float)(s - (double)h);  // exact: |r| <= ulp(h) / 2
     return log2_split(h) + (double)(r * __builtin_amdgcn_rcpf(h) * kLog2e);
+}
+
+// 2^t of a float64 t as a float32, to about 1e-7 relative: 2^round(t)
+// exactly (ldexp) times the native 2^f of the float32 fraction f, |f| <= 1/2,
+// with f's own rounding r restored to first order (2^(f + r) = 2^f (1 + r ln 2)).
+__device__ __forceinline__ float pow2_of(double t) {
+    const double ti = fmin(fmax(rint(t), -300.0), 300.0);
+    const double fd = t - ti;
+    const float f = (float)fd;
+    const float r = (float)(fd - (double)f);
+    const float e = __builtin_amdgcn_exp2f(f);
+    return ldexpf(fmaf(e, r * kLn2, e), (int)ti);
 }
 
 // A potential p (float64) enters the float32 element loops as p2 = fl(p *
@@ -1051,33 +1058,53 @@ struct FzRowOut {
 };
 
 // One row (batch-flat index r) of the fused step: its base-2 LSE, the log_u
-// update in float64, then the column fold.  The LSE is summed against the
-// row's LSE of the previous step (rs) in one pass and accepted in the same
-// window as the column sums; otherwise, and on EXACT steps, it is the exact
-// two-pass.  Returns the LDS slot parity for the next row.
+// update in float64, then the row's share of the column sums.
+//
+// Row LSE: the terms e_j = 2^(K_ij + lv2_j - rs), weighted by the lv2
+// rounding weights, summed against the row's LSE of the previous step (rs)
+// in one pass and accepted when the sum lies in [sum_lo, sum_hi]; otherwise
+// the row is read again and takes the exact two-pass (fz_row_exact), and the
+// terms are formed again against its shift.
+//
+// Column sums (not EXACT): the column half-step needs 2^(K_ij + lu2_i - c)
+// for the new log_u of this row.  That term is e_j * A_i * 2^(-lv2_j - c)
+// with A_i = 2^(lu_i * log2 e + shift_i): the row's terms times one
+// per-row factor, the last factor per column only.  So the row adds
+// e_j * A_i to column j's sum (one fma per term, the terms already in
+// registers), and the merge takes LSE2_j = log2(T_j) - lv2_j of the total
+// T_j, the column's own factor folded in exactly.  A_i carries the float64
+// potential (pow2_of), so no rounding of lu2 enters the columns.
+//
+// EXACT steps (the first, and the first after an epsilon change) fold the
+// columns with a running (max, sum) instead (col_fold2), from y = K + lu2.
+// Returns the LDS slot parity for the next row.
 template <int W, int NV, bool EXACT>
-__device__ __forceinline__ int fz_row(const vf4 (&kk)[NV], double mu_r, double u_r, float rs,
-                                      const vf4 *lv_s, const vf4 *cs_s,
-                                      const vf4 (&wv)[NV], float2 (*rowpart)[W],
-                                      double (*rowsum)[W], int par, int w, int lane, int64_t r,
-                                      const FzRowOut &out, float sum_lo, float sum_hi,
-                                      double damp, int unbalanced,
+__device__ __forceinline__ int fz_row(vf4 (&kk)[NV], double mu_r, double u_r, float rs,
+                                      const vf4 *row4, const uint32_t (&qb)[NV],
+                                      const vf4 *lv_s, const vf4 (&wv)[NV],
+                                      float2 (*rowpart)[W], double (*rowsum)[W], int par, int w,
+                                      int lane, int64_t r, const FzRowOut &out, float sum_lo,
+                                      float sum_hi, double damp, int unbalanced,
                                       float (&cm)[EXACT ? 4 * NV : 1], float (&cs)[4 * NV]) {
     // u_r and rs were read with the row, before the row barrier after which
-    // wave 0 rewrites the row's potential and shift
+    // the row's potential and shift are rewritten
     double l2 = 0.0;
+    float shift = rs;
     bool have = false;
     if constexpr (!EXACT) {
-        // lane sums in float32, the wave's and the row's sums in float64
-        // (wave_sum_all_d)
+        // the terms replace the row's K in registers; lane sums in float32,
+        // the wave's and the row's sums in float64 (wave_sum_all_d)
         float s = 0.f;
 #pragma unroll
         for (int k = 0; k < NV; ++k) {
             const vf4 y = kk[k] + lv_s[(k * W + w) * 64 + lane];
-            s = fmaf(__builtin_amdgcn_exp2f(y.x - rs), wv[k].x, s);
-            s = fmaf(__builtin_amdgcn_exp2f(y.y - rs), wv[k].y, s);
-            s = fmaf(__builtin_amdgcn_exp2f(y.z - rs), wv[k].z, s);
-            s = fmaf(__builtin_amdgcn_exp2f(y.w - rs), wv[k].w, s);
+            const vf4 e = vf4{__builtin_amdgcn_exp2f(y.x - rs), __builtin_amdgcn_exp2f(y.y - rs),
+                              __builtin_amdgcn_exp2f(y.z - rs), __builtin_amdgcn_exp2f(y.w - rs)};
+            kk[k] = e;
+            s = fmaf(e.x, wv[k].x, s);
+            s = fmaf(e.y, wv[k].y, s);
+            s = fmaf(e.z, wv[k].z, s);
+            s = fmaf(e.w, wv[k].w, s);
         }
         double s64 = wave_sum_all_d((double)s);
         if constexpr (W > 1) {  // the W waves' sums, added in LDS in wave order
@@ -1093,19 +1120,32 @@ __device__ __forceinline__ int fz_row(const vf4 (&kk)[NV], double mu_r, double u
         if (s64 >= (double)sum_lo && s64 <= (double)sum_hi) {  // block-uniform; false for NaN
             l2 = log2_of_sum(s64) + (double)rs;
             have = true;
+        } else {
+            // the exact two-pass needs the row's K again (rare: a stale shift)
+            const char *base = reinterpret_cast<const char *>(row4);
+#pragma unroll
+            for (int k = 0; k < NV; ++k)
+                kk[k] = *reinterpret_cast<const vf4 *>(base + qb[k]);
         }
     }
     if (!have) {
         Lse tot;
         par = fz_row_exact<W, NV>(kk, lv_s, wv, rowpart, par, w, lane, tot);
-        l2 = log2_split(tot.s) + (double)lse_shift(tot.m);
+        shift = lse_shift(tot.m);
+        l2 = log2_split(tot.s) + (double)shift;
+        if constexpr (!EXACT) {
+#pragma unroll
+            for (int k = 0; k < NV; ++k) {
+                const vf4 y = kk[k] + lv_s[(k * W + w) * 64 + lane];
+                kk[k] = vf4{__builtin_amdgcn_exp2f(y.x - shift), __builtin_amdgcn_exp2f(y.y - shift),
+                            __builtin_amdgcn_exp2f(y.z - shift), __builtin_amdgcn_exp2f(y.w - shift)};
+            }
+        }
     }
     // the update in float64: nothing of the potential is rounded to float32
-    // between steps; the column sums below weight each term by the rounding
-    // residual of lu2
+    // between steps
     const double lu = update_potential64(l2, mu_r, u_r, damp, unbalanced != 0);
     const float lu2 = (float)(lu * kLog2eD);
-    const float wr = potential_weight(lu, lu2);
     if (w == 0 && lane == 0) {
         out.lu64[r] = lu;
         out.log_u[r] = (float)lu;
@@ -1122,13 +1162,13 @@ __device__ __forceinline__ int fz_row(const vf4 (&kk)[NV], double mu_r, double u
             col_fold2(cm[4 * k + 3], cs[4 * k + 3], y.w);
         }
     } else {
+        const float a = pow2_of(lu * kLog2eD + (double)shift);
 #pragma unroll
         for (int k = 0; k < NV; ++k) {
-            const vf4 y = (kk[k] + lu2) - cs_s[(k * W + w) * 64 + lane];
-            cs[4 * k + 0] = fmaf(__builtin_amdgcn_exp2f(y.x), wr, cs[4 * k + 0]);
-            cs[4 * k + 1] = fmaf(__builtin_amdgcn_exp2f(y.y), wr, cs[4 * k + 1]);
-            cs[4 * k + 2] = fmaf(__builtin_amdgcn_exp2f(y.z), wr, cs[4 * k + 2]);
-            cs[4 * k + 3] = fmaf(__builtin_amdgcn_exp2f(y.w), wr, cs[4 * k + 3]);
+            cs[4 * k + 0] = fmaf(kk[k].x, a, cs[4 * k + 0]);
+            cs[4 * k + 1] = fmaf(kk[k].y, a, cs[4 * k + 1]);
+            cs[4 * k + 2] = fmaf(kk[k].z, a, cs[4 * k + 2]);
+            cs[4 * k + 3] = fmaf(kk[k].w, a, cs[4 * k + 3]);
         }
     }
     return par;
@@ -1145,16 +1185,15 @@ __device__ __forceinline__ int fz_row(const vf4 (&kk)[NV], double mu_r, double u
 // RW = 1 then, so every wave of the block sees the same rows and the same
 // barriers).  With RW > 1 the row groups' column sums add up in LDS after the
 // last row.  NB: row buffers per wave.  colpart receives one float per column
-// (the sum against the shift c_j, which every chunk shares), or with EXACT the
+// (the chunk's share of T_j = sum_i e_ij * A_i, fz_row), or with EXACT the
 // exact running (max, sum) pair of col_fold2 (the first step, and the first
-// after an epsilon change, have no usable shift).  K holds the base-2 log
+// after an epsilon change, have no usable row shift).  K holds the base-2 log
 // kernel -C'*log2(e)/e and lv2 the kLog2eD-scaled log_v.  Requires M % 4 == 0,
 // M <= 256*W*NV, 16-byte aligned K and lv2.
 template <int W, int RW, int NV, int NB, bool EXACT, bool NT>
 __global__ void __launch_bounds__(W * RW * 64)
 sk_fused_step(const float *__restrict__ K, const float *__restrict__ lv2,
-              const float *__restrict__ lvw, const float *__restrict__ lse2_col,
-              float *__restrict__ lse2_row,
+              const float *__restrict__ lvw, float *__restrict__ lse2_row,
               const double *__restrict__ mu64, double *__restrict__ lu64, float *__restrict__ log_u, float *__restrict__ lu2,
               float2 *__restrict__ colpart, int64_t N, int64_t M, int n_chunk,
               int rows_per_chunk, int interleave, float sum_lo, float sum_hi, double damp,
@@ -1162,7 +1201,6 @@ sk_fused_step(const float *__restrict__ K, const float *__restrict__ lv2,
     static_assert(W == 1 || RW == 1, "a row is split over waves only with one row group");
     constexpr int MV = W * 64 * NV;  // float4 per row at most
     __shared__ vf4 lv_s[MV];         // log_v * log2(e) of the batch, -inf past M
-    __shared__ vf4 cs_s[MV];         // column shifts c_j (base 2)
     __shared__ float2 rowpart[2][W];
     __shared__ double rowsum[2][W];
     const int chunk = blockIdx.x;
@@ -1234,18 +1272,15 @@ sk_fused_step(const float *__restrict__ K, const float *__restrict__ lv2,
         }
     }
     const float4 *lv4 = reinterpret_cast<const float4 *>(lv2 + b * M);
-    const float4 *cs4 = reinterpret_cast<const float4 *>(lse2_col + b * M);
     for (int q = threadIdx.x; q < MV; q += W * RW * 64) {
         const float4 v = q < m4 ? lv4[q] : make_float4(-f_inf(), -f_inf(), -f_inf(), -f_inf());
         lv_s[q] = vf4{v.x, v.y, v.z, v.w};
-        const float4 c = q < m4 ? cs4[q] : make_float4(0.f, 0.f, 0.f, 0.f);
-        cs_s[q] = vf4{c.x, c.y, c.z, c.w};
     }
     __syncthreads();
 
     if constexpr (NB == 1) {
         for (; i < end; i += step) {
-            par = fz_row<W, NV, EXACT>(kr[0], rmu[0], ru[0], rls[0], lv_s, cs_s, wv,
+            par = fz_row<W, NV, EXACT>(kr[0], rmu[0], ru[0], rls[0], Kb4 + i * m4, qb, lv_s, wv,
                                        rowpart, rowsum, par, w, lane, rb + i, out, sum_lo, sum_hi,
                                        damp, unbalanced, cm, cs);
             if (i + step < end)
@@ -1257,8 +1292,8 @@ sk_fused_step(const float *__restrict__ K, const float *__restrict__ lv2,
             for (int p = 0; p < NB; ++p) {
                 const int64_t ia = i + (int64_t)(NB - 1) * step;
                 TM_FZ_LOAD((p + NB - 1) % NB, ia <= last ? ia : last);
-                par = fz_row<W, NV, EXACT>(kr[p], rmu[p], ru[p], rls[p], lv_s, cs_s, wv, rowpart,
-                                           rowsum, par, w, lane, rb + i, out,
+                par = fz_row<W, NV, EXACT>(kr[p], rmu[p], ru[p], rls[p], Kb4 + i * m4, qb, lv_s,
+                                           wv, rowpart, rowsum, par, w, lane, rb + i, out,
                                            sum_lo, sum_hi, damp, unbalanced, cm, cs);
                 i += step;
                 if (i >= end)
@@ -1327,8 +1362,8 @@ sk_fused_step(const float *__restrict__ K, const float *__restrict__ lv2,
                 d4[0] = make_float4(p[0].m, p[0].s, p[1].m, p[1].s);
                 d4[1] = make_float4(p[2].m, p[2].s, p[3].m, p[3].s);
             } else {
-                // every chunk shares the column's shift: the sum alone (the
-                // float view of the same buffer, chunk-major)
+                // the chunk's share of T_j alone (the float view of the same
+                // buffer, chunk-major)
                 float *sum = reinterpret_cast<float *>(colpart) + (b * n_chunk + chunk) * M;
                 *reinterpret_cast<float4 *>(sum + qb[k] / 4) =
                     make_float4(cs[4 * k + 0], cs[4 * k + 1], cs[4 * k + 2], cs[4 * k + 3]);
@@ -1343,26 +1378,26 @@ sk_fused_step(const float *__restrict__ K, const float *__restrict__ lv2,
 struct MergeOut {
     double *lv64;
     float *log_v;
-    float *lv2;
+    float *lv2;  // read (the pass's lv2) before it is rewritten
     float *lvw;  // potential_weight of the column's lv2
-    float *lse2_col;
 };
 
 // grid (ceil(M/64), B), MW waves (16 for many chunks, else 4): lanes are 64
 // consecutive columns (coalesced 512-byte reads of one chunk), wave w merges
-// the partials of chunks w, w+MW, ..., and the waves merge in LDS.  Shifted
-// partials (exact = 0) share the column's shift and are added in float64; a
-// column whose total lies outside [sum_lo, sum_hi] = [2^-16, 2^16] (its shift
-// was stale) is recomputed exactly: the block then folds its 64 columns of
-// every row of K with the step's final lu2 (wave w takes rows w, w+MW, ...).
-// Wave 0 updates the column's potential in float64 and stores its base-2 LSE
-// as the next step's shift.
+// the partials of chunks w, w+MW, ..., and the waves merge in LDS.  Plain
+// partials (exact = 0) are the chunks' shares of T_j (fz_row), added in
+// float64; the column's base-2 LSE is log2(T_j) - lv2_j with the lv2 the pass
+// used.  A column whose T_j lies outside [col_lo, col_hi] = [2^-96, 2^96]
+// (its terms near float32 underflow or overflow) is recomputed exactly: the
+// block then folds its 64 columns of every row of K with the step's lu2
+// (wave w takes rows w, w+MW, ...).  Wave 0 updates the column's potential
+// in float64.
 template <int kMergeWaves>
 __global__ void __launch_bounds__(kMergeWaves * 64)
 sk_col_merge_blk(const float2 *__restrict__ colpart, const float *__restrict__ K,
                  const float *__restrict__ lu2, const double *__restrict__ nu64,
                  const uint8_t *__restrict__ inf_col, MergeOut out, int64_t N, int64_t M,
-                 int n_chunk, int exact, float sum_lo, float sum_hi, double damp,
+                 int n_chunk, int exact, double col_lo, double col_hi, double damp,
                  int unbalanced) {
     const int64_t b = blockIdx.y;
     const int w = (int)(threadIdx.x >> 6);
@@ -1373,7 +1408,7 @@ sk_col_merge_blk(const float2 *__restrict__ colpart, const float *__restrict__ K
     // the column's own values are loaded before the partials, so that their
     // latency overlaps the partials' instead of following the LDS merge
     const double nu_t = nu64[t], v_t = out.lv64[t];
-    const float c_t = out.lse2_col[t];
+    const float lv2_t = out.lv2[t];
     const bool live = j < M && !inf_col[t];
     __shared__ float2 part[kMergeWaves][64];
     __shared__ double part64[kMergeWaves][64];
@@ -1402,7 +1437,7 @@ sk_col_merge_blk(const float2 *__restrict__ colpart, const float *__restrict__ K
             if (k != w)
                 acc = lse2_merge(acc, Lse{part[k][lane].x, part[k][lane].y});
         l2 = log2_split(acc.s) + (double)lse_shift(acc.m);
-    } else {  // sums against the column's shift: plain adds, in float64
+    } else {  // shares of T_j: plain adds, in float64
         const float *sum = reinterpret_cast<const float *>(colpart);
         double tsum = 0.0;
         for (; c + 3 * kMergeWaves < n_chunk; c += 4 * kMergeWaves) {
@@ -1420,8 +1455,8 @@ sk_col_merge_blk(const float2 *__restrict__ colpart, const float *__restrict__ K
 #pragma unroll
         for (int k = 1; k < kMergeWaves; ++k)
             tsum += part64[k][lane];
-        ok = tsum >= (double)sum_lo && tsum <= (double)sum_hi;  // false for NaN
-        l2 = ok ? log2_of_sum(tsum) + (double)c_t : 0.0;
+        ok = tsum >= col_lo && tsum <= col_hi;  // false for NaN
+        l2 = ok ? log2_of_sum(tsum) - (double)lv2_t : 0.0;
     }
     if (__syncthreads_or(live && !ok)) {
         float m = kFltMaxNeg, s = 0.f;
@@ -1441,7 +1476,6 @@ sk_col_merge_blk(const float2 *__restrict__ colpart, const float *__restrict__ K
         return;
     const double lv = update_potential64(l2, nu_t, v_t, damp, unbalanced != 0);
     const float lv2 = (float)(lv * kLog2eD);
-    out.lse2_col[t] = (float)l2;
     out.lv64[t] = lv;
     out.log_v[t] = (float)lv;
     out.lv2[t] = lv2;
@@ -1626,7 +1660,7 @@ int launch_col_sweep(const SinkhornLayout &L, bool vec, const float *K, const fl
 // The fused step's arrays of one batch group (batches from b0 on).
 struct FusedPtrs {
     const float *K;
-    float *lv2, *lvw, *lse2_col, *lse2_row, *log_u, *lu2, *log_v;
+    float *lv2, *lvw, *lse2_row, *log_u, *lu2, *log_v;
     const double *mu64, *nu64;
     double *lu64, *lv64;
     const uint8_t *inf_row, *inf_col;
@@ -1639,7 +1673,6 @@ FusedPtrs fused_ptrs(const SinkhornLayout &L, char *ws, float *log_u, float *log
     P.K = reinterpret_cast<const float *>(ws + L.off_k) + b0 * N * M;
     P.lv2 = reinterpret_cast<float *>(ws + L.off_lv2) + b0 * M;
     P.lvw = reinterpret_cast<float *>(ws + L.off_lvw) + b0 * M;
-    P.lse2_col = reinterpret_cast<float *>(ws + L.off_lse2col) + b0 * M;
     P.lse2_row = reinterpret_cast<float *>(ws + L.off_lse2row) + b0 * N;
     P.lu2 = reinterpret_cast<float *>(ws + L.off_lu2) + b0 * N;
     P.log_u = log_u + b0 * N;
@@ -1678,7 +1711,7 @@ int launch_fused_step(const SinkhornLayout &L, bool exact, const FusedPtrs &P, d
     const dim3 block(f.W * f.RW * 64);
 #define TM_FUSED1(W_, RW_, NV_, NB_, EX_, NT_)                                             \
     TM_LAUNCH((sk_fused_step<W_, RW_, NV_, NB_, EX_, NT_>), grid, block, 0, stream, P.K,      \
-              P.lv2, P.lvw, P.lse2_col, P.lse2_row, P.mu64, P.lu64, P.log_u, P.lu2,                 \
+              P.lv2, P.lvw, P.lse2_row, P.mu64, P.lu64, P.log_u, P.lu2,                             \
               P.colpart, L.N, L.M, L.fz_chunk, L.fz_rows, L.fz_interleave, sum_lo, sum_hi,   \
               damp, ub)
 #define TM_FUSED(W_, RW_, NV_, NB_)                                                         \
@@ -1706,14 +1739,16 @@ int launch_fused_step(const SinkhornLayout &L, bool exact, const FusedPtrs &P, d
 #undef TM_FUSED
 #undef TM_FUSED1
     const dim3 mgrid((unsigned)((L.M + 63) / 64), (unsigned)L.B);
-    const MergeOut mo{P.lv64, P.log_v, P.lv2, P.lvw, P.lse2_col};
+    const MergeOut mo{P.lv64, P.log_v, P.lv2, P.lvw};
+    // the column totals T_j are on the scale of the column marginals
+    const double col_lo = win > 0.f ? 0x1p-96 : 1.0, col_hi = win > 0.f ? 0x1p96 : 0.0;
     if (L.fz_chunk > 64)  // C5: 256 chunks, 10.2 us with 16 waves against 11.3 with 4
         TM_LAUNCH(sk_col_merge_blk<16>, mgrid, dim3(16 * 64), 0, stream, P.colpart, P.K, P.lu2,
-                  P.nu64, P.inf_col, mo, L.N, L.M, L.fz_chunk, exact ? 1 : 0, sum_lo, sum_hi,
+                  P.nu64, P.inf_col, mo, L.N, L.M, L.fz_chunk, exact ? 1 : 0, col_lo, col_hi,
                   damp, ub);
     else  // C4: 32 chunks, 5.0 us with 4 waves against 8.5 with 16
         TM_LAUNCH(sk_col_merge_blk<4>, mgrid, dim3(4 * 64), 0, stream, P.colpart, P.K, P.lu2,
-                  P.nu64, P.inf_col, mo, L.N, L.M, L.fz_chunk, exact ? 1 : 0, sum_lo, sum_hi,
+                  P.nu64, P.inf_col, mo, L.N, L.M, L.fz_chunk, exact ? 1 : 0, col_lo, col_hi,
                   damp, ub);
     return TM_OK;
 }
@@ -1942,8 +1977,6 @@ extern "C" int tm_sinkhorn_iterate_f32(const float *cost, const uint8_t *keep, i
         TM_LAUNCH(sk_fill, gn, dim3(kMapBlock), 0, stream, P.lu2, B * N, 0.f);
         TM_LAUNCH(sk_fill, gm, dim3(kMapBlock), 0, stream, P.lv2, B * M, 0.f);
         TM_LAUNCH(sk_fill, gm, dim3(kMapBlock), 0, stream, P.lvw, B * M, 1.f);
-        TM_LAUNCH(sk_fill, gm, dim3(kMapBlock), 0, stream, P.lse2_col, B * M,
-                  __builtin_nanf(""));
     }
 
     const int64_t waves_per_batch = (N + kRowsPerWave - 1) / kRowsPerWave;
