@@ -75,14 +75,16 @@ JV_C3_CRITICAL_STEPS = 2750
 MEASURED_TRAFFIC = {
     # the fused solve launch on C2 (the op's only launch on this batch)
     "jv_c2": int((8349.5 * 2 + 584.0) * 1024),
+    # the K = 768 solve launch on C3 (its tile rows mostly from L2 / MALL)
+    "jv_c3": int((4940.0 * 2 + 256.0) * 1024),
     # sk_fused_step + sk_col_merge_blk per C4 iteration: two batch groups of 8,
     # each one pass + one merge (K once, column sums twice)
-    "sinkhorn_c4": int(2 * ((66330.9 + 1172.5) * 2 + 2176.0 + 128.0) * 1024),
+    "sinkhorn_c4": int(2 * ((66386.0 + 1236.0) * 2 + 2368.4 + 320.0) * 1024),
     # the same per iteration of the B = 64 control (two groups of 32; K read
     # with non-temporal loads)
-    "sinkhorn_b64": int(2 * ((264874.5 + 1508.5) * 2 + 2560.0 + 512.0) * 1024),
+    "sinkhorn_b64": int(2 * ((267595.7 + 1764.0) * 2 + 3328.0 + 1280.0) * 1024),
     # the same pair per C5 iteration (one group)
-    "sinkhorn_c5": int(((525955.8 + 8359.5) * 2 + 17412.8 + 128.0) * 1024),
+    "sinkhorn_c5": int(((533815.9 + 8405.5) * 2 + 18453.8 + 320.0) * 1024),
 }
 
 
@@ -392,7 +394,8 @@ def bench_jv_c3(device, reps: int = 3) -> dict:
            "cost_sha256": workloads.sha256(cost_cpu),
            "roofline": {"bound": "hbm", "binding": False, "achieved": round(gbs, 3),
                         "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                        "frac": round(gbs / HBM_PEAK_GBS, 6), "traffic": None,
+                        "frac": round(gbs / HBM_PEAK_GBS, 6),
+                        "traffic": MEASURED_TRAFFIC["jv_c3"],
                         "note": "one wave per problem walks a dependency chain over an "
                                 "L2 / Infinity-Cache resident tile; HBM is not binding"}}
     # The binding resource, as for C2: the slowest problem's sequential steps
