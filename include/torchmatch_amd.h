@@ -292,7 +292,7 @@ int tm_sinkhorn_f32(const float *cost, const float *a, const float *b, int64_t B
  *   cost, a, b, log_plan, log_u, log_v  device float64 tensors of the shapes
  *   and meanings of tm_sinkhorn_f32; log_plan may be NULL
  *   workspace  device, >= tm_sinkhorn_f64_workspace_bytes(B, N, M)
- * B <= 65535. */
+ * Any B: every launch strides its grid over the batch. */
 size_t tm_sinkhorn_f64_workspace_bytes(int64_t B, int64_t N, int64_t M);
 int tm_sinkhorn_f64(const double *cost, const double *a, const double *b, int64_t B,
                     int64_t N, int64_t M, const double *eps_sched, int32_t n_iter, double rho,

@@ -174,11 +174,12 @@ __host__ __device__ inline size_t align_up(size_t x, size_t a) { return (x + a -
 
 // sk_fused_step instantiations: (W waves per row, RW row groups, NV float4
 // per lane), chosen by row length; resident blocks per CU from their VGPR and
-// LDS use (69 / 197 / 100 / 100 / 140 / 85 VGPRs; 16 / 32 / 33 / 66 / 131 /
-// 131 KiB of LDS; the short-row shapes are far below both limits).  Rows
-// longer than 8192 columns take 16 waves of 1024 columns (C5: 193 us per
-// iteration against 215 for 8 waves of 2048; with the rows' sums added in
-// LDS instead of merged as (max, sum) pairs, the smaller shape is faster).
+// LDS use (hipcc's resource report for the non-EXACT instances: 1x4x4 104
+// VGPRs, 1x4x8 199, 2x1x8 and 4x1x8 190, 8x1x8 226, 16x1x4 122; LDS 12 / 24 /
+// 16 / 32 / 64 / 65 KiB; the short-row shapes 47 and 67 VGPRs).  Rows
+// longer than 8192 columns take 16 waves of 1024 columns, one block per CU
+// (four waves per SIMD at 122 VGPRs; 8 waves of 2048 columns measured
+// slower).
 enum FusedVariant {
     kFzNone = 0, kFz1x4x4, kFz1x4x8, kFz2x1x8, kFz4x1x8, kFz8x1x8, kFz16x1x4, kFz1x4x1, kFz1x4x2
 };
