@@ -1058,6 +1058,30 @@ struct FzRowOut {
     float *lse2_row;
 };
 
+// The potential update and the column sums of a one-wave row (fz_row with
+// W = 1, not EXACT) from its terms e_j = 2^(K_ij + lv2_j - shift).
+template <int NV>
+__device__ __forceinline__ void fz_row_tail_w1(const vf4 (&e)[NV], double l2, float shift,
+                                               double mu_r, double u_r, int lane, int64_t r,
+                                               const FzRowOut &out, double damp, int unbalanced,
+                                               float (&cs)[4 * NV]) {
+    const double lu = update_potential64(l2, mu_r, u_r, damp, unbalanced != 0);
+    if (lane == 0) {
+        out.lu64[r] = lu;
+        out.log_u[r] = (float)lu;
+        out.lu2[r] = (float)(lu * kLog2eD);
+        out.lse2_row[r] = (float)l2;
+    }
+    const float a = pow2_of(lu * kLog2eD + (double)shift);
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+        cs[4 * k + 0] = fmaf(e[k].x, a, cs[4 * k + 0]);
+        cs[4 * k + 1] = fmaf(e[k].y, a, cs[4 * k + 1]);
+        cs[4 * k + 2] = fmaf(e[k].z, a, cs[4 * k + 2]);
+        cs[4 * k + 3] = fmaf(e[k].w, a, cs[4 * k + 3]);
+    }
+}
+
 // One row (batch-flat index r) of the fused step: its base-2 LSE, the log_u
 // update in float64, then the row's share of the column sums.
 //
@@ -1108,6 +1132,38 @@ __device__ __forceinline__ int fz_row(vf4 (&kk)[NV], double mu_r, double u_r, fl
             s = fmaf(e.w, wv[k].w, s);
         }
         double s64 = wave_sum_all_d((double)s);
+        if constexpr (W == 1) {
+            // A one-wave row gives the rare exact fallback a tail and row
+            // registers of its own.  When the fallback reloaded the row into
+            // the registers of the common path, the compiler had the common
+            // path wait for that (conditional) reload, and with it for the
+            // next row's loads already in flight, on every row (C4: 38.3 ->
+            // 37.4 us per iteration without that wait).  Rows split over
+            // waves keep the form below: rewritten like this, the 16-wave
+            // shape measured 2-3% slower.
+            if (s64 >= (double)sum_lo && s64 <= (double)sum_hi) {  // false for NaN
+                fz_row_tail_w1<NV>(kk, log2_of_sum(s64) + (double)rs, rs, mu_r, u_r, lane, r, out,
+                                   damp, unbalanced, cs);
+                return par;
+            }
+            vf4 kx[NV];
+            const char *base = reinterpret_cast<const char *>(row4);
+#pragma unroll
+            for (int k = 0; k < NV; ++k)
+                kx[k] = *reinterpret_cast<const vf4 *>(base + qb[k]);
+            Lse tot;
+            par = fz_row_exact<W, NV>(kx, lv_s, wv, rowpart, par, w, lane, tot);
+            const float sh = lse_shift(tot.m);
+#pragma unroll
+            for (int k = 0; k < NV; ++k) {
+                const vf4 y = kx[k] + lv_s[(k * W + w) * 64 + lane];
+                kx[k] = vf4{__builtin_amdgcn_exp2f(y.x - sh), __builtin_amdgcn_exp2f(y.y - sh),
+                            __builtin_amdgcn_exp2f(y.z - sh), __builtin_amdgcn_exp2f(y.w - sh)};
+            }
+            fz_row_tail_w1<NV>(kx, log2_split(tot.s) + (double)sh, sh, mu_r, u_r, lane, r, out,
+                               damp, unbalanced, cs);
+            return par;
+        }
         if constexpr (W > 1) {  // the W waves' sums, added in LDS in wave order
             if (lane == 0)
                 rowsum[par][w] = s64;
