@@ -1036,17 +1036,14 @@ __device__ __forceinline__ bool certified_solve(const int K, WaveLds &L, const C
     // predecessor row and its cost column in registers (col.get(i) = c[i][j],
     // an indexed VGPR move).  The key of a distance is its raw bits: d >= 0
     // up to rounding, and a misorder among rounding-size negatives only picks
-    // another column of the same distance.  Lane r also holds
-    // u_r = c[r][x_r] - v[x_r] (fixed during a search), so the step's offset
-    // h = c[i][j*] - v[j*] - level (the scanned column j* is row i's own)
-    // comes from one read of lane i, alongside the row's gather.
+    // another column of the same distance.  Lane j also holds uy_j = u of the
+    // row y_j that owns column j, u_i = c[i][x_i] - v[x_i] = c[y_j][j] - v[j]
+    // (fixed during a search), so the step's offset h = u_i - level of the
+    // scanned column's row is read from the scanned lane itself, alongside
+    // that row's index, not from a lane the row index selects.
     int pred = 0;
-    float u = 0.f;
-    auto refresh_u = [&]() {
-        const int xs = x < 0 ? lane : x;
-        const float vx = __int_as_float(__builtin_amdgcn_ds_bpermute(xs * 4, __float_as_int(v)));
-        u = L.c[lane * kTile + xs] - vx;
-    };
+    float uy = 0.f;
+    auto refresh_u = [&]() { uy = (live && y >= 0 ? L.c[y * kTile + lane] : 0.f) - v; };
     refresh_u();
     // free rows from the highest index down: on C2-like batches (16 seeds of
     // 1024 problems, CPU count) the slowest problem's search takes 356 steps
@@ -1062,10 +1059,11 @@ __device__ __forceinline__ bool certified_solve(const int K, WaveLds &L, const C
         // the loop ends within K steps.  The step loop is placed at a fixed
         // offset from a 64-byte instruction-cache line (the padding runs once
         // per search): its speed otherwise moves by several percent with the
-        // size of the code before it.  One word past the line was the
-        // fastest of the offsets 0-7 measured on the C2 batches (1.5 us per
-        // launch against four words; re-measure when the loop changes).
-        asm volatile(".p2align 6\n\ts_nop 0" ::: "memory");
+        // size of the code before it.  Three words past the line was the
+        // fastest of the offsets 0-7 measured on the C2 batches (seed 0: 60.4
+        // us per launch, against 65.3 at two words and 63.5 at none;
+        // re-measure when the loop changes).
+        asm volatile(".p2align 6\n\ts_nop 0\n\ts_nop 0\n\ts_nop 0" ::: "memory");
         while (true) {
             const int kmin = wave_min_key_s(key);
             if (kmin == kKeyNone)
@@ -1073,6 +1071,7 @@ __device__ __forceinline__ bool certified_solve(const int K, WaveLds &L, const C
             const int js = first_lane(ballot(key == kmin));
             level = __int_as_float(kmin);  // an open column's key is its distance's bits
             const int is = readlane_i(y, js);
+            const float us = readlane_f(uy, js);
             if (is < 0) {
                 jf = js;  // unassigned column: the path ends
                 break;
@@ -1080,12 +1079,17 @@ __device__ __forceinline__ bool certified_solve(const int K, WaveLds &L, const C
             // relax through row `is`: r = c[i][j] - v[j] - (u_i - level), as
             // scan_dense's c[i][j] - v[j] - h, associated so that each step
             // of the sum takes one scalar
-            const float r = ((col.get(is) - v) - readlane_f(u, is)) + level;
-            const bool upd = (key != kKeyNone) & (r < d);
+            const float r = ((col.get(is) - v) - us) + level;
+            // an open lane's key is its distance's bits, and a scanned or
+            // dead lane's key, kKeyNone, is a NaN pattern, against which
+            // r < key is false: one compare, no separate test of the key
+            const bool upd = r < __int_as_float(key);
             d = upd ? r : d;
             pred = upd ? is : pred;
             const int nk = upd ? __float_as_int(r) : key;
-            key = lane == js ? kKeyNone : nk;
+            // the scanned lane retires through a scalar mask (made as soon
+            // as js is known), so this last select takes no vector compare
+            key = __builtin_amdgcn_inverse_ballot_w64(~(1ull << js)) ? nk : kKeyNone;
         }
         if (jf < 0)
             return false;
