@@ -33,7 +33,7 @@ namespace {
 
 constexpr int kMaxLargeK = 1024;
 constexpr int kMaxChunks = kMaxLargeK / 64;
-constexpr int kCacheSlots = 8;  // row-cache depth; one slot per lane of lanes 0..7
+constexpr int kCacheSlots = 16;  // row-cache depth; one slot per lane of lanes 0..15
 
 struct LargeLds {
     float v[kMaxLargeK];
@@ -53,10 +53,14 @@ struct LargeLds {
     // Duals only fall from the column reduction on, so every other reduced
     // cost of the row is still >= tau; when the second smallest cached value
     // (with the current duals) is < tau, the two cached minima are the row's
-    // two minima, first column on ties.  Filled with 8 columns for every row
-    // before the solve when the caller's workspace holds the prefill
-    // (jv_large_rowcache_kernel), and with 3 by the row scans.
-    alignas(16) int32_t cq[kMaxLargeK][kCacheSlots];  // 16-byte copies (copy_to_lds)
+    // two minima, first column on ties.  Filled with 16 columns for every
+    // row before the solve when the caller's workspace holds the prefill
+    // (jv_large_rowcache_kernel), and with 3 by the row scans.  Columns are
+    // 16-bit (K <= 1024), so the 16-slot cache of 1024 rows takes 96 KiB.
+    // On the C3 batch's slowest problem 16 prefilled slots leave 9 of its
+    // 2,496 row-reduction steps to scan their row, 8 left 80 (CPU model of
+    // the cache policy, which reproduces the kernel's counts).
+    alignas(16) int16_t cq[kMaxLargeK][kCacheSlots];  // 16-byte copies (copy_to_lds)
     alignas(16) float cg[kMaxLargeK][kCacheSlots];
     float ctau[kMaxLargeK];
 };
@@ -225,22 +229,14 @@ __device__ __forceinline__ float chunk_value(const f32x16 &v, int e, int l) {
     return readlane_f(v[e], l);
 }
 
-// Smallest key of lanes 0..7, in each of those lanes: quad butterflies, then
-// the 8-lane mirror (the groups of eight never mix).
-__device__ __forceinline__ int min8_key(int key) {
-    int a = key;
-    a = min(a, dpp_full<kDppQuadXor1>(a));
-    a = min(a, dpp_full<kDppQuadXor2>(a));
-    return min(a, dpp_full<kDppRowHalfMirror>(a));
-}
-
-// Smallest and second smallest key (as a multiset) of lanes 0..7, in each
-// of those lanes: three pair-merge butterfly stages.
-__device__ __forceinline__ void min2_8_key(int key, int &k1, int &k2) {
+// Smallest and second smallest key (as a multiset) of lanes 0..15, in each
+// of those lanes: four pair-merge butterfly stages inside the 16-lane row.
+__device__ __forceinline__ void min2_16_key(int key, int &k1, int &k2) {
     int a = key, b = kKeyNone;
     pair_merge(a, b, dpp_full<kDppQuadXor1>(a), dpp_full<kDppQuadXor1>(b));
     pair_merge(a, b, dpp_full<kDppQuadXor2>(a), dpp_full<kDppQuadXor2>(b));
     pair_merge(a, b, dpp_full<kDppRowHalfMirror>(a), dpp_full<kDppRowHalfMirror>(b));
+    pair_merge(a, b, dpp_full<kDppRowMirror>(a), dpp_full<kDppRowMirror>(b));
     k1 = a;
     k2 = b;
 }
@@ -251,7 +247,7 @@ __device__ __forceinline__ void min2_8_key(int key, int &k1, int &k2) {
 struct LargePrep {
     const float *v;
     const int32_t *y;
-    const int32_t *cq;
+    const int16_t *cq;
     const float *cg;
     const float *ctau;
 };
@@ -438,7 +434,7 @@ __device__ void scan_row(LargeLds &L, const CostView &C, int fi, int E, int K,
     const float g2 = chunk_value(cr, s2 >> 6, s2 & 63);
     // slots 0..2 by column, the rest empty
     if (lane < kCacheSlots) {
-        L.cq[fi][lane] = lane == 0 ? s0 : (lane == 1 ? s1 : (lane == 2 ? s2 : -1));
+        L.cq[fi][lane] = (int16_t)(lane == 0 ? s0 : (lane == 1 ? s1 : (lane == 2 ? s2 : -1)));
         L.cg[fi][lane] = lane == 0 ? g0 : (lane == 1 ? g1 : g2);
     }
     L.ctau[fi] = k4 == kKeyNone ? finf() : key_to_float(k4);  // every lane, the same word
@@ -550,7 +546,7 @@ template <int NC>
 __global__ void __launch_bounds__(256)
 jv_large_rowcache_kernel(const float *__restrict__ costs, int64_t B, int N, int M,
                          const JvStats *__restrict__ partial, int n_partial,
-                         const float *__restrict__ v_in, int32_t *__restrict__ cq_out,
+                         const float *__restrict__ v_in, int16_t *__restrict__ cq_out,
                          float *__restrict__ cg_out, float *__restrict__ tau_out) {
     const int K = N > M ? N : M;
     const int E = (K + 63) / 64;
@@ -636,7 +632,7 @@ jv_large_rowcache_kernel(const float *__restrict__ costs, int64_t B, int N, int 
         }
         if (lane < kCacheSlots) {
             const int slot = my_col >= 0 ? rank : lane;
-            cq_out[row * kCacheSlots + slot] = my_col;
+            cq_out[row * kCacheSlots + slot] = (int16_t)my_col;
             cg_out[row * kCacheSlots + slot] = my_cost;
         }
         if (lane == 0)
@@ -797,7 +793,7 @@ __device__ __forceinline__ bool large_solve(const int K, const int E, LargeLds &
         COMPACT ? compact_arr_guard(K) : 4u * (uint32_t)K * (uint32_t)K + 64u;
     if (P.v != nullptr) {
         // every real row's cache from the prefill (jv_large_rowcache_kernel)
-        copy_to_lds(&L.cq[0][0], P.cq, C.N * kCacheSlots);
+        copy_to_lds(&L.cq[0][0], P.cq, C.N * kCacheSlots / 2);  // dwords of 16-bit columns
         copy_to_lds(&L.cg[0][0], P.cg, C.N * kCacheSlots);
         float t[NC];
 #pragma unroll
@@ -854,7 +850,7 @@ __device__ __forceinline__ bool large_solve(const int K, const int E, LargeLds &
                     const float r = g - L.v[max(q, 0)];
                     const int key = (lane < kCacheSlots && q >= 0) ? fkey(r) : kKeyNone;
                     int p1, p2;
-                    min2_8_key(key, p1, p2);
+                    min2_16_key(key, p1, p2);
                     const int k1 = readlane_i(p1, 0), k2 = readlane_i(p2, 0);
                     const uint64_t m1 = ballot(key == k1);
                     const int l1 = first_lane(m1);
@@ -1225,7 +1221,7 @@ size_t align256(size_t n) { return (n + 255) / 256 * 256; }
 struct PrepBuffers {
     float *v;
     int32_t *y;
-    int32_t *cq;
+    int16_t *cq;
     float *cg;
     float *ctau;
 };
@@ -1238,8 +1234,8 @@ PrepBuffers prep_buffers(void *ws, int64_t B, int N, int M) {
     p += align256((size_t)(B * K) * 4);
     r.y = reinterpret_cast<int32_t *>(p);
     p += align256((size_t)(B * K) * 4);
-    r.cq = reinterpret_cast<int32_t *>(p);
-    p += align256((size_t)(B * N) * kCacheSlots * 4);
+    r.cq = reinterpret_cast<int16_t *>(p);
+    p += align256((size_t)(B * N) * kCacheSlots * 2);
     r.cg = reinterpret_cast<float *>(p);
     p += align256((size_t)(B * N) * kCacheSlots * 4);
     r.ctau = reinterpret_cast<float *>(p);
@@ -1301,8 +1297,8 @@ int launch_large(const float *costs, int64_t B, int N, int M, const JvStats *par
 
 size_t jv_large_prep_bytes(int64_t B, int N, int M) {
     const int64_t K = N > M ? N : M;
-    return 2 * align256((size_t)(B * K) * 4) + 2 * align256((size_t)(B * N) * kCacheSlots * 4) +
-           align256((size_t)(B * N) * 4);
+    return 2 * align256((size_t)(B * K) * 4) + align256((size_t)(B * N) * kCacheSlots * 2) +
+           align256((size_t)(B * N) * kCacheSlots * 4) + align256((size_t)(B * N) * 4);
 }
 
 int launch_jv_large(const float *costs, int64_t B, int N, int M, const JvStats *partial,
