@@ -34,6 +34,7 @@ namespace {
 constexpr int kMaxLargeK = 1024;
 constexpr int kMaxChunks = kMaxLargeK / 64;
 constexpr int kCacheSlots = 16;  // row-cache depth; one slot per lane of lanes 0..15
+constexpr int kKeyLarge = __builtin_bit_cast(int, kLarge);  // fkey(kLarge): kLarge > 0
 
 struct LargeLds {
     float v[kMaxLargeK];
@@ -821,18 +822,30 @@ __device__ __forceinline__ bool large_solve(const int K, const int E, LargeLds &
     for (int round = 0; n_free > 0 && round < 2; ++round) {
         uint32_t cur = 0, rr = 0;
         int still = 0;
+        // The row of the next step is known before this step ends: the row
+        // this step displaces when it lowers a dual (it goes back to the
+        // queue's head), else the queue entry after this row.  A step writes
+        // the queue only at positions < cur (the slot it consumed, or still
+        // <= that slot), so that entry is read at the step's start and its
+        // load overlaps the step.
+        int fi_next = uniform_i(L.fr[0]);
         while (cur < (uint32_t)n_free) {
             ++rr;
             if (rr > rr_limit)
                 return false;
             // LDS words every lane reads alike are made uniform explicitly, so
             // that the step's branches are scalar (no exec-mask bookkeeping)
-            const int fi = uniform_i(L.fr[cur]);
+            const int fi = fi_next;
             ++cur;
+            const int fq = L.fr[min(cur, (uint32_t)K - 1)];
             const bool pad_row = fi >= C.N;
             int j1 = -1, j2 = -1;
             float u1 = 0.f, u2 = 0.f;
             bool known = false;
+            // from the cache: v[j1], y[j1], y[j2] as gathered with the slots
+            bool cached = false;
+            float c_vj1 = 0.f;
+            int c_y1 = -1, c_y2 = -1;
             if (pad_row && pad_valid) {
                 j1 = pad_j1;
                 j2 = pad_j2;
@@ -840,33 +853,54 @@ __device__ __forceinline__ bool large_solve(const int K, const int E, LargeLds &
                 u2 = pad_u2;
                 known = true;
             } else if (!pad_row) {
-                const float tau = uniform_f(L.ctau[fi]);
-                if (tau > -finf()) {
-                    // lane s < kCacheSlots holds slot s (columns ascending
-                    // with the slot): the first lane at a key is the first
-                    // column at that key
-                    const int q = L.cq[fi][lane & (kCacheSlots - 1)];
-                    const float g = L.cg[fi][lane & (kCacheSlots - 1)];
-                    const float r = g - L.v[max(q, 0)];
-                    const int key = (lane < kCacheSlots && q >= 0) ? fkey(r) : kKeyNone;
-                    int p1, p2;
-                    min2_16_key(key, p1, p2);
-                    const int k1 = readlane_i(p1, 0), k2 = readlane_i(p2, 0);
-                    const uint64_t m1 = ballot(key == k1);
+                // No branch on tau: a row never filled has tau = -inf, which
+                // no t2 is below, so tau, the slots, then the slots' duals
+                // and owners load in two rounds without a wait between
+                // them.  Slot columns outside [0, K) (a row never filled,
+                // without the prefill) read column 0 and carry no key.
+                const float tau_l = L.ctau[fi];
+                const int qs = L.cq[fi][lane & (kCacheSlots - 1)];
+                const float g = L.cg[fi][lane & (kCacheSlots - 1)];
+                // all three issued before the first wait (the scheduler
+                // otherwise waits for the columns before issuing the rest)
+                __builtin_amdgcn_sched_barrier(0);
+                // tau as a key: fkey is monotone and tau was stored from a
+                // key, so t2 < tau <=> key(t2) < key(tau)
+                const int tb = uniform_i(__float_as_int(tau_l));
+                const int ktau = tb ^ ((tb >> 31) & 0x7fffffff);
+                const bool qok = lane < kCacheSlots && (unsigned)qs < (unsigned)K;
+                const int q = qok ? qs : 0;
+                const float vq = L.v[q];
+                const int yq = L.y[q];
+                const float r = g - vq;
+                // the owners are needed only by a cache hit, but their load
+                // is kept beside the duals' (the compiler would otherwise
+                // sink it into the hit's branch, a third round trip)
+                asm volatile("" ::"v"(yq));
+                // lane s < kCacheSlots holds slot s (columns ascending with
+                // the slot): the first lane at a key is the first column at
+                // that key
+                const int key = qok ? fkey(r) : kKeyNone;
+                int p1, p2;
+                min2_16_key(key, p1, p2);
+                const int k1 = readlane_i(p1, 0), k2 = readlane_i(p2, 0);
+                // The hit test on keys alone (k1 <= k2, and kKeyNone is above
+                // every key): u2 < tau, and u2 < LARGE so that the
+                // reference's (LARGE, -1) start slot cannot win.  The two
+                // ballots issue together.
+                const uint64_t m1 = ballot(key == k1), m2 = ballot(key == k2);
+                if (k2 < min(ktau, kKeyLarge)) {
                     const int l1 = first_lane(m1);
-                    if (k1 != kKeyNone && k2 != kKeyNone) {
-                        const int l2 = first_lane(ballot(key == k2) & ~(1ull << l1));
-                        const float t2 = readlane_f(r, l2);
-                        if (t2 < tau && t2 < kLarge) {
-                            // u2 < LARGE: the reference's (LARGE, -1) start
-                            // slot cannot win
-                            known = true;
-                            j1 = readlane_i(q, l1);
-                            j2 = readlane_i(q, l2);
-                            u1 = readlane_f(r, l1);
-                            u2 = t2;
-                        }
-                    }
+                    const int l2 = first_lane(m2 & ~(1ull << l1));
+                    known = true;
+                    cached = true;
+                    j1 = readlane_i(q, l1);
+                    j2 = readlane_i(q, l2);
+                    u1 = readlane_f(r, l1);
+                    u2 = readlane_f(r, l2);
+                    c_vj1 = readlane_f(vq, l1);
+                    c_y1 = readlane_i(yq, l1);
+                    c_y2 = readlane_i(yq, l2);
                 }
             }
             if (!known)
@@ -878,38 +912,42 @@ __device__ __forceinline__ bool large_solve(const int K, const int E, LargeLds &
                 pad_u2 = u2;
                 pad_valid = true;
             }
-            int jsel = j1;
-            int i0 = uniform_i(L.y[j1]);
-            const float vj1 = uniform_f(L.v[j1]);
+            // v[j1], y[j1], y[j2]: gathered with the slots, else read here
+            int y1, y2;
+            float vj1;
+            if (cached) {
+                y1 = c_y1;
+                y2 = c_y2;
+                vj1 = c_vj1;
+            } else {
+                y1 = uniform_i(L.y[j1]);
+                y2 = uniform_i(L.y[max(j2, 0)]);
+                vj1 = uniform_f(L.v[j1]);
+            }
             const float lowered = vj1 - (u2 - u1);
             const bool lowers = lowered < vj1;
             const bool cap = COMPACT || rr < cur * (uint32_t)K;
-            if (cap && !lowers && i0 >= 0 && j2 >= 0) {
-                jsel = j2;
-                i0 = uniform_i(L.y[j2]);
-            }
+            // dec: v[j1] falls and the displaced row goes back to the queue's
+            // head; sw: no fall, the row takes j2 when j1 is owned
+            const bool dec = cap && lowers;
+            const bool sw = cap && !lowers && y1 >= 0 && j2 >= 0;
+            const int jsel = sw ? j2 : j1;
+            const int i0 = sw ? y2 : y1;
+            const bool push = i0 >= 0;
+            const uint32_t slot = cur - 1;  // the queue slot this step consumed
+            fi_next = dec && push ? i0 : uniform_i(fq);
             lds_sync();
-            // every lane writes the same word (no exec-mask round trip)
-            if (cap) {
-                if (lowers) {
-                    L.v[j1] = lowered;
-                    pad_valid = false;
-                }
-                if (i0 >= 0) {
-                    if (lowers) {
-                        --cur;
-                        L.fr[cur] = i0;
-                    } else {
-                        L.fr[still] = i0;
-                        ++still;
-                    }
-                }
-            } else if (i0 >= 0) {
-                L.fr[still] = i0;
-                ++still;
-            }
+            // Every write unconditional, every lane writing the same word:
+            // v[j1] gets its own value back when it does not fall, and a row
+            // that displaces no one writes -1 into the consumed slot, which
+            // is dead (the next round's rows sit below it: still <= slot).
+            L.v[j1] = dec ? lowered : vj1;
+            L.fr[push && !dec ? (uint32_t)still : slot] = i0;
             L.x[fi] = jsel;
             L.y[jsel] = fi;
+            pad_valid = pad_valid && !dec;
+            cur = dec && push ? slot : cur;
+            still = push && !dec ? still + 1 : still;
             lds_sync();
         }
         n_free = still;
