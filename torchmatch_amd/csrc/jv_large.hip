@@ -819,6 +819,9 @@ __device__ __forceinline__ bool large_solve(const int K, const int E, LargeLds &
     // scan a row, and a row load in flight across the step's end made the
     // compiler wait for it at every step (2.64 against 2.27 ms per (64, 512,
     // 768) batch).
+    // lanes 0..kCacheSlots-1 hold the cache slots: a slot column is live
+    // when below this bound (K there, 0 in the other lanes)
+    const uint32_t slot_bound = lane < kCacheSlots ? (uint32_t)K : 0u;
     for (int round = 0; n_free > 0 && round < 2; ++round) {
         uint32_t cur = 0, rr = 0;
         int still = 0;
@@ -827,8 +830,51 @@ __device__ __forceinline__ bool large_solve(const int K, const int E, LargeLds &
         // queue's head), else the queue entry after this row.  A step writes
         // the queue only at positions < cur (the slot it consumed, or still
         // <= that slot), so that entry is read at the step's start and its
-        // load overlaps the step.
+        // load overlaps the step.  The next row's cache slots (tau, columns,
+        // costs) then load as soon as that row is known, before this step's
+        // writes (which touch no cache word: only a row's own scan refills
+        // its cache, and the next row is never this row).
         int fi_next = uniform_i(L.fr[0]);
+        float tau_n = L.ctau[fi_next];
+        int q_n = L.cq[fi_next][lane & (kCacheSlots - 1)];
+        float g_n = L.cg[fi_next][lane & (kCacheSlots - 1)];
+        // The end of a step (carr_dense's update, jonker_dense_flat.h:
+        // 210-232), given row fi's two minima j1 / j2 (j2 = -1: none), their
+        // owners y1 / y2, v[j1], lowered = v[j1] - (u2 - u1) and whether it
+        // is below v[j1].  x is not written here: it is rebuilt from y
+        // after the reduction (no step reads it).
+        auto finish = [&](int fi, int fq, int j1, int j2, int y1, int y2, float vj1, float lowered,
+                          bool lowers) __attribute__((always_inline)) {
+            const bool cap = COMPACT || rr < cur * (uint32_t)K;
+            // dec: v[j1] falls and the displaced row goes back to the queue's
+            // head; sw: no fall, the row takes j2 when j1 is owned
+            const bool dec = cap && lowers;
+            const bool sw = cap && !lowers && y1 >= 0 && j2 >= 0;
+            const int jsel = sw ? j2 : j1;
+            const int i0 = sw ? y2 : y1;
+            const bool push = i0 >= 0;
+            const uint32_t slot = cur - 1;  // the queue slot this step consumed
+            fi_next = dec && push ? i0 : uniform_i(fq);
+            {
+                // clamped: after the last step fq is read past the queue
+                const int rn = min(max(fi_next, 0), K - 1);
+                tau_n = L.ctau[rn];
+                q_n = L.cq[rn][lane & (kCacheSlots - 1)];
+                g_n = L.cg[rn][lane & (kCacheSlots - 1)];
+            }
+            lds_sync();
+            // Every write unconditional, every lane writing the same word:
+            // v[j1] gets its own value back when it does not fall, and a row
+            // that displaces no one writes -1 into the consumed slot, which
+            // is dead (the next round's rows sit below it: still <= slot).
+            L.v[j1] = dec ? lowered : vj1;
+            L.fr[push && !dec ? (uint32_t)still : slot] = i0;
+            L.y[jsel] = fi;
+            pad_valid = pad_valid && !dec;
+            cur = dec && push ? slot : cur;
+            still = push && !dec ? still + 1 : still;
+            lds_sync();
+        };
         while (cur < (uint32_t)n_free) {
             ++rr;
             if (rr > rr_limit)
@@ -838,41 +884,22 @@ __device__ __forceinline__ bool large_solve(const int K, const int E, LargeLds &
             const int fi = fi_next;
             ++cur;
             const int fq = L.fr[min(cur, (uint32_t)K - 1)];
-            const bool pad_row = fi >= C.N;
-            int j1 = -1, j2 = -1;
-            float u1 = 0.f, u2 = 0.f;
-            bool known = false;
-            // from the cache: v[j1], y[j1], y[j2] as gathered with the slots
-            bool cached = false;
-            float c_vj1 = 0.f;
-            int c_y1 = -1, c_y2 = -1;
-            if (pad_row && pad_valid) {
-                j1 = pad_j1;
-                j2 = pad_j2;
-                u1 = pad_u1;
-                u2 = pad_u2;
-                known = true;
-            } else if (!pad_row) {
+            if (fi < C.N) {
+                // The cached two minima, straight-line to the step's end.
                 // No branch on tau: a row never filled has tau = -inf, which
-                // no t2 is below, so tau, the slots, then the slots' duals
-                // and owners load in two rounds without a wait between
-                // them.  Slot columns outside [0, K) (a row never filled,
-                // without the prefill) read column 0 and carry no key.
-                const float tau_l = L.ctau[fi];
-                const int qs = L.cq[fi][lane & (kCacheSlots - 1)];
-                const float g = L.cg[fi][lane & (kCacheSlots - 1)];
-                // all three issued before the first wait (the scheduler
-                // otherwise waits for the columns before issuing the rest)
-                __builtin_amdgcn_sched_barrier(0);
-                // tau as a key: fkey is monotone and tau was stored from a
-                // key, so t2 < tau <=> key(t2) < key(tau)
-                const int tb = uniform_i(__float_as_int(tau_l));
-                const int ktau = tb ^ ((tb >> 31) & 0x7fffffff);
-                const bool qok = lane < kCacheSlots && (unsigned)qs < (unsigned)K;
-                const int q = qok ? qs : 0;
+                // no u2 is below.  Slot columns outside [0, K) (a row never
+                // filled, without the prefill) read column 0 and carry no
+                // key.  tau as a key: fkey is monotone and tau was stored
+                // from a key, so u2 < tau <=> key(u2) < key(tau); and u2 <
+                // LARGE, so that the reference's (LARGE, -1) start slot
+                // cannot win.
+                const int tb = uniform_i(__float_as_int(tau_n));
+                const int ktau = min(tb ^ ((tb >> 31) & 0x7fffffff), kKeyLarge);
+                const bool qok = (uint32_t)q_n < slot_bound;
+                const int q = qok ? q_n : 0;
                 const float vq = L.v[q];
                 const int yq = L.y[q];
-                const float r = g - vq;
+                const float r = g_n - vq;
                 // the owners are needed only by a cache hit, but their load
                 // is kept beside the duals' (the compiler would otherwise
                 // sink it into the hit's branch, a third round trip)
@@ -884,74 +911,64 @@ __device__ __forceinline__ bool large_solve(const int K, const int E, LargeLds &
                 int p1, p2;
                 min2_16_key(key, p1, p2);
                 const int k1 = readlane_i(p1, 0), k2 = readlane_i(p2, 0);
-                // The hit test on keys alone (k1 <= k2, and kKeyNone is above
-                // every key): u2 < tau, and u2 < LARGE so that the
-                // reference's (LARGE, -1) start slot cannot win.  The two
-                // ballots issue together.
+                // the two ballots issue together (k1 <= k2, and kKeyNone is
+                // above every key)
                 const uint64_t m1 = ballot(key == k1), m2 = ballot(key == k2);
-                if (k2 < min(ktau, kKeyLarge)) {
+                if (k2 < ktau) {
+                    // u1, u2 from the keys, beside the lane search: the
+                    // keys fold -0.0 into +0.0, which changes u2 - u1 only
+                    // when both are zeros, and then lowered is a zero that is
+                    // not below v[j1] and is not stored.  Every lane lowers
+                    // its own slot's dual; lane l1's is the step's.
+                    const float u1 = key_to_float(k1), u2 = key_to_float(k2);
+                    const float low = vq - (u2 - u1);
+                    const uint64_t mlow = ballot(low < vq);
+                    const int pk = (yq << 16) | q;  // q < K <= 1024, yq in [-1, K)
                     const int l1 = first_lane(m1);
                     const int l2 = first_lane(m2 & ~(1ull << l1));
-                    known = true;
-                    cached = true;
-                    j1 = readlane_i(q, l1);
-                    j2 = readlane_i(q, l2);
-                    u1 = readlane_f(r, l1);
-                    u2 = readlane_f(r, l2);
-                    c_vj1 = readlane_f(vq, l1);
-                    c_y1 = readlane_i(yq, l1);
-                    c_y2 = readlane_i(yq, l2);
+                    const int pk1 = readlane_i(pk, l1), pk2 = readlane_i(pk, l2);
+                    finish(fi, fq, pk1 & 0xffff, pk2 & 0xffff, pk1 >> 16, pk2 >> 16, readlane_f(vq, l1),
+                           readlane_f(low, l1), (mlow >> l1) & 1);
+                    continue;
                 }
             }
-            if (!known)
-                scan_row<NC>(L, C, fi, E, K, !pad_row, j1, j2, u1, u2);
-            if (pad_row && !pad_valid) {
-                pad_j1 = j1;
-                pad_j2 = j2;
-                pad_u1 = u1;
-                pad_u2 = u2;
-                pad_valid = true;
-            }
-            // v[j1], y[j1], y[j2]: gathered with the slots, else read here
-            int y1, y2;
-            float vj1;
-            if (cached) {
-                y1 = c_y1;
-                y2 = c_y2;
-                vj1 = c_vj1;
+            // a padded row (its two minima kept while no dual falls), or a
+            // cache miss: the row's scan
+            const bool pad_row = fi >= C.N;
+            int j1, j2;
+            float u1, u2;
+            if (pad_row && pad_valid) {
+                j1 = pad_j1;
+                j2 = pad_j2;
+                u1 = pad_u1;
+                u2 = pad_u2;
             } else {
-                y1 = uniform_i(L.y[j1]);
-                y2 = uniform_i(L.y[max(j2, 0)]);
-                vj1 = uniform_f(L.v[j1]);
+                scan_row<NC>(L, C, fi, E, K, !pad_row, j1, j2, u1, u2);
+                if (pad_row) {
+                    pad_j1 = j1;
+                    pad_j2 = j2;
+                    pad_u1 = u1;
+                    pad_u2 = u2;
+                    pad_valid = true;
+                }
             }
+            const float vj1 = uniform_f(L.v[j1]);
             const float lowered = vj1 - (u2 - u1);
-            const bool lowers = lowered < vj1;
-            const bool cap = COMPACT || rr < cur * (uint32_t)K;
-            // dec: v[j1] falls and the displaced row goes back to the queue's
-            // head; sw: no fall, the row takes j2 when j1 is owned
-            const bool dec = cap && lowers;
-            const bool sw = cap && !lowers && y1 >= 0 && j2 >= 0;
-            const int jsel = sw ? j2 : j1;
-            const int i0 = sw ? y2 : y1;
-            const bool push = i0 >= 0;
-            const uint32_t slot = cur - 1;  // the queue slot this step consumed
-            fi_next = dec && push ? i0 : uniform_i(fq);
-            lds_sync();
-            // Every write unconditional, every lane writing the same word:
-            // v[j1] gets its own value back when it does not fall, and a row
-            // that displaces no one writes -1 into the consumed slot, which
-            // is dead (the next round's rows sit below it: still <= slot).
-            L.v[j1] = dec ? lowered : vj1;
-            L.fr[push && !dec ? (uint32_t)still : slot] = i0;
-            L.x[fi] = jsel;
-            L.y[jsel] = fi;
-            pad_valid = pad_valid && !dec;
-            cur = dec && push ? slot : cur;
-            still = push && !dec ? still + 1 : still;
-            lds_sync();
+            finish(fi, fq, j1, j2, uniform_i(L.y[j1]), uniform_i(L.y[max(j2, 0)]), vj1, lowered,
+                   lowered < vj1);
         }
         n_free = still;
     }
+    // x from y (the row-reduction steps write y alone)
+    for (int i = lane; i < K; i += 64)
+        L.x[i] = -1;
+    lds_sync();
+    for (int j = lane; j < K; j += 64) {
+        const int i = L.y[j];
+        if (i >= 0)
+            L.x[i] = j;
+    }
+    lds_sync();
 
     // ---- augmentation (ca_dense / find_path_dense, jonker_dense_flat.h:75-122,237-258) ----
     // the next path's start row is loaded while this path is searched
