@@ -810,18 +810,15 @@ __device__ __forceinline__ bool large_solve(const int K, const int E, LargeLds &
             L.ctau[i] = -finf();
     }
     lds_sync();
-    // Rows >= N of the padded tile are all 0, so their reduced costs are -v:
-    // one two-minimum serves every such row until a dual changes.
-    int pad_j1 = -1, pad_j2 = -1;
-    float pad_u1 = 0.f, pad_u2 = 0.f;
-    bool pad_valid = false;
-    // No prefetch of the next step's row: with the prefilled caches few steps
-    // scan a row, and a row load in flight across the step's end made the
-    // compiler wait for it at every step (2.64 against 2.27 ms per (64, 512,
-    // 768) batch).
     // lanes 0..kCacheSlots-1 hold the cache slots: a slot column is live
     // when below this bound (K there, 0 in the other lanes)
     const uint32_t slot_bound = lane < kCacheSlots ? (uint32_t)K : 0u;
+    // Rows >= N of the padded tile are all 0, so their reduced costs are -v:
+    // one two-minimum serves every such row until a dual changes (their
+    // minima tie too often for the cache's strict tau test).
+    int pad_j1 = -1, pad_j2 = -1;
+    float pad_u1 = 0.f, pad_u2 = 0.f;
+    bool pad_valid = false;
     for (int round = 0; n_free > 0 && round < 2; ++round) {
         uint32_t cur = 0, rr = 0;
         int still = 0;
@@ -831,9 +828,9 @@ __device__ __forceinline__ bool large_solve(const int K, const int E, LargeLds &
         // the queue only at positions < cur (the slot it consumed, or still
         // <= that slot), so that entry is read at the step's start and its
         // load overlaps the step.  The next row's cache slots (tau, columns,
-        // costs) then load as soon as that row is known, before this step's
-        // writes (which touch no cache word: only a row's own scan refills
-        // its cache, and the next row is never this row).
+        // costs) then load as soon as that row is known: after this step's
+        // scan refills a cache row, before its other writes (which touch no
+        // cache word).
         int fi_next = uniform_i(L.fr[0]);
         float tau_n = L.ctau[fi_next];
         int q_n = L.cq[fi_next][lane & (kCacheSlots - 1)];
@@ -841,20 +838,27 @@ __device__ __forceinline__ bool large_solve(const int K, const int E, LargeLds &
         // The end of a step (carr_dense's update, jonker_dense_flat.h:
         // 210-232), given row fi's two minima j1 / j2 (j2 = -1: none), their
         // owners y1 / y2, v[j1], lowered = v[j1] - (u2 - u1) and whether it
-        // is below v[j1].  x is not written here: it is rebuilt from y
-        // after the reduction (no step reads it).
-        auto finish = [&](int fi, int fq, int j1, int j2, int y1, int y2, float vj1, float lowered,
-                          bool lowers) __attribute__((always_inline)) {
-            const bool cap = COMPACT || rr < cur * (uint32_t)K;
+        // is below v[j1] (lowers, 0 / 1).  Flags as 0 / 1 integers keep the
+        // logic on the scalar unit.  x is not written here: it is rebuilt
+        // from y after the reduction (no step reads it).
+        // (x >> 31) & 1 for "x < 0": a compare's flag would be kept as a
+        // lane mask, and turned into 0 / 1 on the vector unit.
+        auto neg = [](int x) { return (int)((uint32_t)x >> 31); };
+        auto finish = [&](int fi, int fqs, int j1, int j2, int y1, int y2, float vj1, float lowered,
+                          int lowers) __attribute__((always_inline)) {
+            // rr and cur * K stay below 2^31 (rr_limit)
+            const int cap = COMPACT ? 1 : neg((int)(rr - cur * (uint32_t)K));
             // dec: v[j1] falls and the displaced row goes back to the queue's
             // head; sw: no fall, the row takes j2 when j1 is owned
-            const bool dec = cap && lowers;
-            const bool sw = cap && !lowers && y1 >= 0 && j2 >= 0;
+            const int dec = cap & lowers;
+            const int sw = cap & (lowers ^ 1) & (neg(y1) ^ 1) & (neg(j2) ^ 1);
             const int jsel = sw ? j2 : j1;
             const int i0 = sw ? y2 : y1;
-            const bool push = i0 >= 0;
+            const int push = neg(i0) ^ 1;
+            const int back = dec & push;  // the displaced row is the next row
+            const int tail = push & (dec ^ 1);  // ... or it joins the next round
             const uint32_t slot = cur - 1;  // the queue slot this step consumed
-            fi_next = dec && push ? i0 : uniform_i(fq);
+            fi_next = back ? i0 : fqs;
             {
                 // clamped: after the last step fq is read past the queue
                 const int rn = min(max(fi_next, 0), K - 1);
@@ -867,12 +871,12 @@ __device__ __forceinline__ bool large_solve(const int K, const int E, LargeLds &
             // v[j1] gets its own value back when it does not fall, and a row
             // that displaces no one writes -1 into the consumed slot, which
             // is dead (the next round's rows sit below it: still <= slot).
-            L.v[j1] = dec ? lowered : vj1;
-            L.fr[push && !dec ? (uint32_t)still : slot] = i0;
+            L.v[j1] = __int_as_float(dec ? __float_as_int(lowered) : __float_as_int(vj1));
+            L.fr[tail ? (uint32_t)still : slot] = i0;
             L.y[jsel] = fi;
             pad_valid = pad_valid && !dec;
-            cur = dec && push ? slot : cur;
-            still = push && !dec ? still + 1 : still;
+            cur -= back;
+            still += tail;
             lds_sync();
         };
         while (cur < (uint32_t)n_free) {
@@ -911,29 +915,30 @@ __device__ __forceinline__ bool large_solve(const int K, const int E, LargeLds &
                 int p1, p2;
                 min2_16_key(key, p1, p2);
                 const int k1 = readlane_i(p1, 0), k2 = readlane_i(p2, 0);
+                const int fqs = uniform_i(fq);
                 // the two ballots issue together (k1 <= k2, and kKeyNone is
                 // above every key)
                 const uint64_t m1 = ballot(key == k1), m2 = ballot(key == k2);
                 if (k2 < ktau) {
-                    // u1, u2 from the keys, beside the lane search: the
-                    // keys fold -0.0 into +0.0, which changes u2 - u1 only
-                    // when both are zeros, and then lowered is a zero that is
-                    // not below v[j1] and is not stored.  Every lane lowers
-                    // its own slot's dual; lane l1's is the step's.
-                    const float u1 = key_to_float(k1), u2 = key_to_float(k2);
-                    const float low = vq - (u2 - u1);
+                    // u1, u2 from the keys (lanes 0..15 hold both), beside
+                    // the lane search: the keys fold -0.0 into +0.0, which
+                    // changes u2 - u1 only when both are zeros, and then
+                    // lowered is a zero that is not below v[j1] and is not
+                    // stored.  Every lane lowers its own slot's dual; lane
+                    // l1's is the step's.
+                    const float low = vq - (key_to_float(p2) - key_to_float(p1));
                     const uint64_t mlow = ballot(low < vq);
                     const int pk = (yq << 16) | q;  // q < K <= 1024, yq in [-1, K)
                     const int l1 = first_lane(m1);
                     const int l2 = first_lane(m2 & ~(1ull << l1));
                     const int pk1 = readlane_i(pk, l1), pk2 = readlane_i(pk, l2);
-                    finish(fi, fq, pk1 & 0xffff, pk2 & 0xffff, pk1 >> 16, pk2 >> 16, readlane_f(vq, l1),
-                           readlane_f(low, l1), (mlow >> l1) & 1);
+                    finish(fi, fqs, pk1 & 0xffff, pk2 & 0xffff, pk1 >> 16, pk2 >> 16, readlane_f(vq, l1),
+                           readlane_f(low, l1), (int)(mlow >> l1) & 1);
                     continue;
                 }
             }
-            // a padded row (its two minima kept while no dual falls), or a
-            // cache miss: the row's scan
+            // a padded row, or a cache miss: the row's scan (which refills
+            // a real row's cache)
             const bool pad_row = fi >= C.N;
             int j1, j2;
             float u1, u2;
@@ -954,8 +959,8 @@ __device__ __forceinline__ bool large_solve(const int K, const int E, LargeLds &
             }
             const float vj1 = uniform_f(L.v[j1]);
             const float lowered = vj1 - (u2 - u1);
-            finish(fi, fq, j1, j2, uniform_i(L.y[j1]), uniform_i(L.y[max(j2, 0)]), vj1, lowered,
-                   lowered < vj1);
+            finish(fi, uniform_i(fq), j1, j2, uniform_i(L.y[j1]), uniform_i(L.y[max(j2, 0)]), vj1,
+                   lowered, lowered < vj1 ? 1 : 0);
         }
         n_free = still;
     }
