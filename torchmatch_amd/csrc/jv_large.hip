@@ -976,18 +976,68 @@ __device__ __forceinline__ bool large_solve(const int K, const int E, LargeLds &
     lds_sync();
 
     // ---- augmentation (ca_dense / find_path_dense, jonker_dense_flat.h:75-122,237-258) ----
-    // the next path's start row is loaded while this path is searched
-    float nx[NC];
-    if (n_free > 0 && L.fr[0] < C.N)
-        load_row_raw<NC>(C, L.fr[0], nx);
+    // A run of padded start rows: their rows are all 0, so while no dual
+    // changes the first find_dense of each sees the same tied block (the
+    // columns at the largest v), and each path takes the next unassigned
+    // column of it.  The run's first path lists the block's unassigned
+    // columns in pick order (dense: descending, compact: ascending) in
+    // rbuf, unused by the paths; later padded paths take the next entry
+    // still unassigned (a real row's single-column path may have taken
+    // one).  A full search, which moves duals, ends the run.
+    int *const run_list = reinterpret_cast<int *>(L.rbuf);
+    int run_pos = 0, run_n = 0;
     for (int f = 0; f < n_free; ++f) {
         const int start = uniform_i(L.fr[f]);
+        if (start >= C.N && run_pos < run_n) {
+            int found = -1;
+            while (run_pos < run_n) {
+                const int j = uniform_i(run_list[run_pos++]);
+                if (uniform_i(L.y[j]) < 0) {
+                    found = j;
+                    break;
+                }
+            }
+            if (found >= 0) {
+                L.y[found] = start;  // every lane writes the same word
+                L.x[start] = found;
+                lds_sync();
+                continue;
+            }
+        }
+        // The first find_dense from the start row's cache, without its row:
+        // when the smallest cached reduced cost is below tau, it is the
+        // row's minimum and every column tied with it is cached (all others
+        // are >= tau: duals only fall, in the row reduction and in the
+        // path updates below alike).  Its tied block in column order is
+        // then the cached columns at that key (slots ascend with the
+        // column), and when one of them is unassigned the path is that
+        // single column, as below.
+        if (start < C.N) {
+            const float tau_l = L.ctau[start];
+            const int qs = L.cq[start][lane & (kCacheSlots - 1)];
+            const float g = L.cg[start][lane & (kCacheSlots - 1)];
+            __builtin_amdgcn_sched_barrier(0);
+            const int tb = uniform_i(__float_as_int(tau_l));
+            const int ktau = tb ^ ((tb >> 31) & 0x7fffffff);
+            const bool qok = (uint32_t)qs < slot_bound;
+            const int q = qok ? qs : 0;
+            const float vq = L.v[q];
+            const int yq = L.y[q];
+            const int key = qok ? fkey(g - vq) : kKeyNone;
+            const int mk = wave_min_key_s(key);
+            if (mk < ktau) {
+                const uint64_t open = ballot(key == mk && yq < 0);
+                if (open) {
+                    const int found = readlane_i(q, COMPACT ? first_lane(open) : last_lane(open));
+                    L.y[found] = start;  // every lane writes the same word
+                    L.x[start] = found;
+                    lds_sync();
+                    continue;
+                }
+            }
+        }
         float cr[NC];
-#pragma unroll
-        for (int e = 0; e < NC; ++e)
-            cr[e] = start < C.N ? fix_cost(C, nx[e], e * 64 + lane) : 0.f;
-        if (f + 1 < n_free && L.fr[f + 1] < C.N)
-            load_row_raw<NC>(C, L.fr[f + 1], nx);
+        load_row<NC>(C, start, cr);
         // The first find_dense, decided from the row in registers: cols[] is
         // the identity, so its tied block is, in column order, every column
         // whose d = c - v has the row's minimum key (the column of the last
@@ -1013,23 +1063,41 @@ __device__ __forceinline__ bool large_solve(const int K, const int E, LargeLds &
             }
             mk = wave_min_key_s(mk);
             int found = -1;
+            uint64_t open[NC];
 #pragma unroll
             for (int e = 0; e < NC; ++e) {
-                const uint64_t open = ballot((dk[e] == mk) & (yv[e] < 0));
+                open[e] = ballot((dk[e] == mk) & (yv[e] < 0));
                 if (COMPACT) {
-                    if (open && found < 0)
-                        found = e * 64 + first_lane(open);
-                } else if (open) {
-                    found = e * 64 + last_lane(open);
+                    if (open[e] && found < 0)
+                        found = e * 64 + first_lane(open[e]);
+                } else if (open[e]) {
+                    found = e * 64 + last_lane(open[e]);
                 }
             }
             if (found >= 0) {
+                if (start >= C.N) {
+                    // the run's list; its first entry is found
+                    int n = 0;
+#pragma unroll
+                    for (int t = 0; t < NC; ++t) {
+                        const int e = COMPACT ? t : NC - 1 - t;
+                        const uint64_t m = open[e];
+                        const uint64_t below = m & ((1ull << lane) - 1);
+                        const int rank = COMPACT ? __popcll(below) : __popcll(m) - 1 - __popcll(below);
+                        if ((m >> lane) & 1)
+                            run_list[n + rank] = e * 64 + lane;
+                        n += __popcll(m);
+                    }
+                    run_pos = 1;
+                    run_n = n;
+                }
                 L.y[found] = start;  // every lane writes the same word
                 L.x[start] = found;
                 lds_sync();
                 continue;
             }
         }
+        run_n = 0;  // the full search below moves duals
         float vv[NC];  // read outside the guard, all in flight together
 #pragma unroll
         for (int e = 0; e < NC; ++e)
