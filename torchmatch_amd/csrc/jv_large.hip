@@ -585,44 +585,64 @@ jv_large_rowcache_kernel(const float *__restrict__ costs, int64_t B, int N, int 
             cr[e] = c;
             kk[e] = (e < E && j < K) ? fkey(c - vv[e]) : kKeyNone;
         }
+        // Each lane keeps its three smallest (key, chunk) not yet taken, in
+        // (key, chunk) order (a later chunk is a larger column).  The row's
+        // next smallest (key, column) is then the head of some lane: the
+        // smallest key among the heads, and on a tie the smallest column
+        // among those heads (the first column at a key is its lane's head).
+        // A lane whose three run out while it still holds keys has them
+        // rebuilt (with every lane's: the same or longer prefixes).
+        int h1, h2, h3, e1, e2, e3;  // keys kKeyNone past the lane's last
+        uint32_t taken = 0;
+        int n_left = 0;
+#pragma unroll
+        for (int e = 0; e < NC; ++e)
+            n_left += kk[e] != kKeyNone ? 1 : 0;
+        auto build = [&]() {
+            h1 = h2 = h3 = kKeyNone;
+            e1 = e2 = e3 = 0;
+#pragma unroll
+            for (int e = 0; e < NC; ++e) {
+                const int k = (taken >> e) & 1 ? kKeyNone : kk[e];
+                const bool l1 = k < h1, l2 = k < h2, l3 = k < h3;
+                h3 = l2 ? h2 : (l3 ? k : h3);
+                e3 = l2 ? e2 : (l3 ? e : e3);
+                h2 = l1 ? h1 : (l2 ? k : h2);
+                e2 = l1 ? e1 : (l2 ? e : e2);
+                h1 = l1 ? k : h1;
+                e1 = l1 ? e : e1;
+            }
+        };
+        build();
         int my_col = -1;
         float my_cost = 0.f;
         int tau_key = kKeyNone;
         for (int t = 0; t <= kCacheSlots; ++t) {
-            int lm = kKeyNone;
-#pragma unroll
-            for (int e = 0; e < NC; ++e)
-                lm = min(lm, kk[e]);
-            const int k = wave_min_key_s(lm);
+            const int k = wave_min_key_s(h1);
             if (t == kCacheSlots || k == kKeyNone) {
                 tau_key = k;
                 break;
             }
-            // the first column at k: the first chunk holding k, its first
-            // lane (chunk index uniform, so the chunks after it branch past
-            // their compare)
-            int ef = -1, lf = 0;
-#pragma unroll
-            for (int e = 0; e < NC; ++e) {
-                if (ef < 0) {
-                    const uint64_t m = ballot(kk[e] == k);
-                    if (m) {
-                        ef = e;
-                        lf = first_lane(m);
-                    }
-                }
-            }
-            if (ef < 0)
-                break;  // not reached: k is a key of the row
-            const float c = chunk_value(cr, ef, lf);
+            const uint64_t m = ballot(h1 == k);
+            const int w = (m & (m - 1)) ? (wave_min_key_s(h1 == k ? e1 * 64 + lane : kKeyNone) & 63)
+                                        : first_lane(m);
+            const int ew = readlane_i(e1, w);
+            const float cost = chunk_value(cr, ew, w);
             if (lane == t) {
-                my_col = ef * 64 + lf;
-                my_cost = c;
+                my_col = ew * 64 + w;
+                my_cost = cost;
             }
-#pragma unroll
-            for (int e = 0; e < NC; ++e)
-                if (e == ef)
-                    kk[e] = lane == lf ? kKeyNone : kk[e];
+            if (lane == w) {
+                taken |= 1u << ew;
+                --n_left;
+                h1 = h2;
+                e1 = e2;
+                h2 = h3;
+                e2 = e3;
+                h3 = kKeyNone;
+            }
+            if (readlane_i(h1, w) == kKeyNone && readlane_i(n_left, w) > 0)
+                build();
         }
         // slot = rank of the column among the chosen ones
         int rank = 0;
