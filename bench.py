@@ -76,7 +76,7 @@ MEASURED_TRAFFIC = {
     # the fused solve launch on C2 (the op's only launch on this batch)
     "jv_c2": int((8349.5 * 2 + 584.0) * 1024),
     # the K = 768 solve launch on C3 (its tile rows mostly from L2 / MALL)
-    "jv_c3": int((4940.0 * 2 + 256.0) * 1024),
+    "jv_c3": int((2139.0 * 2 + 256.0) * 1024),
     # sk_fused_step + sk_col_merge_blk per C4 iteration: two batch groups of 8,
     # each one pass + one merge (K once, column sums twice)
     "sinkhorn_c4": int(2 * ((66386.0 + 1236.0) * 2 + 2368.4 + 320.0) * 1024),

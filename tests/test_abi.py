@@ -37,10 +37,11 @@ def test_workspace_queries():
     lib = _native.lib()
     assert lib.tm_jv_max_k() >= 64
     assert lib.tm_jv_workspace_bytes(1024, 64, 64) >= 256
-    # the prefill size: equal for K <= 64, larger for K > 64 (C3: ~2.6 MB)
+    # the prefill size: equal for K <= 64, larger for K > 64 (C3: ~3.7 MB,
+    # of which 3.1 MB are the 16-slot row caches: 6 bytes per slot)
     assert lib.tm_jv_workspace_bytes_prefill(1024, 64, 64) == lib.tm_jv_workspace_bytes(1024, 64, 64)
     c3 = lib.tm_jv_workspace_bytes_prefill(64, 512, 768)
-    assert lib.tm_jv_workspace_bytes(64, 512, 768) < c3 < 3 << 20
+    assert lib.tm_jv_workspace_bytes(64, 512, 768) + 64 * 512 * 16 * 6 < c3 < 4 << 20
     small = lib.tm_sinkhorn_workspace_bytes(2, 8, 8)
     big = lib.tm_sinkhorn_workspace_bytes(16, 2048, 2048)
     assert big > 16 * 2048 * 2048 * 4 > small
