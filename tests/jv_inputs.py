@@ -29,6 +29,9 @@ LARGE_SHAPES = [(65, 65), (100, 80), (80, 100), (128, 128), (200, 130), (300, 30
                 (700, 768), (768, 600), (1000, 1024)]
 PREFILL_SHAPES = [(65, 70), (130, 100), (100, 250), (300, 512), (512, 768), (768, 700),
                   (1024, 900)]
+# K in (1024, 2048]: the 32-chunk instantiation without the row cache
+KINDS_XL = ["uniform", "tied", "masked", "tied_masked"]
+XL_SHAPES = [(1025, 1025), (1100, 1300), (2048, 1500), (1800, 2048)]
 
 
 def random_batch(rng, kind: str, b: int, n: int, m: int) -> np.ndarray:
@@ -73,6 +76,12 @@ def prefill_batches(kind: str):
     rng = np.random.default_rng(zlib.crc32(("prefill" + kind).encode()))
     for n, m in PREFILL_SHAPES:
         yield n, m, random_batch(rng, kind, 4, n, m)
+
+
+def xl_batches(kind: str):
+    rng = np.random.default_rng(zlib.crc32(("xl" + kind).encode()))
+    for n, m in XL_SHAPES:
+        yield n, m, random_batch(rng, kind, 2, n, m)
 
 
 def compact_small_batches(kind: str, kmax: int = 64):

@@ -86,6 +86,19 @@ def test_large_k_match_oracle(kind, device):
         assert mism.size == 0, f"{kind} {c.shape}: {mism.size} problems differ"
 
 
+@pytest.mark.parametrize("kind", jv_inputs.KINDS_XL)
+def test_xl_k_match_oracle(kind, device):
+    """1024 < K <= 2048: the compact solver on the cache-less 32-chunk
+    instantiation."""
+    assert _max_k() >= 2048
+    for n, m, c in jv_inputs.xl_batches(kind):
+        print(f"compact xl {kind} {c.shape}", flush=True)
+        want = jv.jv_compact_batch(c)
+        got = run_op(c, device)
+        mism = np.argwhere((got != want).any(axis=1)).ravel()
+        assert mism.size == 0, f"{kind} {c.shape}: {mism.size} problems differ"
+
+
 def test_every_k_up_to_limit(device):
     rng = np.random.default_rng(31)
     for k in range(1, min(_max_k(), 64) + 1):

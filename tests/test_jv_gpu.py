@@ -79,6 +79,25 @@ def test_large_k_vs_oracle(kind, device):
         np.testing.assert_array_equal(got, want, err_msg=f"{kind} {c.shape}")
 
 
+@pytest.mark.parametrize("kind", jv_inputs.KINDS_XL)
+def test_xl_k_vs_oracle(kind, device):
+    """1024 < K <= 2048: the 32-chunk instantiation without the row cache
+    (every row-reduction step scans its row), through the op and through
+    the C ABI with the prefill-sized workspace (which K > 1024 leaves
+    unused)."""
+    assert _native.jv_max_k() >= 2048
+    lib = _native.lib()
+    for n, m, c in jv_inputs.xl_batches(kind):
+        want = jv.jv_dense_batch(c)
+        print(f"xl kind {kind} shape {c.shape}", flush=True)
+        got = run_op(torch.from_numpy(c), device)
+        np.testing.assert_array_equal(got, want, err_msg=f"{kind} {c.shape}")
+        ws = lib.tm_jv_workspace_bytes_prefill(*c.shape)
+        assert ws == lib.tm_jv_workspace_bytes(*c.shape)
+        got = _c_abi_solve(lib, lib.tm_jv_dense_batch_f32, c, ws, device)
+        np.testing.assert_array_equal(got, want, err_msg=f"C ABI {kind} {c.shape}")
+
+
 def _c_abi_solve(lib, entry, c: np.ndarray, ws_bytes: int, device) -> np.ndarray:
     b, n, m = c.shape
     dc = torch.from_numpy(c).to(device)
@@ -113,6 +132,26 @@ def test_large_k_prefill_and_plain_workspace(kind, device):
         for ws_bytes in (small, full):
             got = _c_abi_solve(lib, lib.tm_jv_compact_batch_f32, c, ws_bytes, device)
             np.testing.assert_array_equal(got, want_c, err_msg=f"compact {kind} {(n, m)}")
+
+
+def test_plain_workspace_after_xl_layout(device):
+    """Without the prefill the solve's row caches start empty: a regression
+    test for slots left unset, whose stale LDS words (here the 2048-column
+    layout's -1 owners and queue entries, NaN patterns as costs) once read
+    as cache hits.  The cache-less solves run first on as many workgroups
+    as the plain solves after them, so the latter inherit their LDS."""
+    lib = _native.lib()
+    rng = np.random.default_rng(77)
+    xl = rng.random((64, 1100, 1100), dtype=np.float32)
+    plain = rng.random((64, 70, 90), dtype=np.float32)
+    want = jv.jv_dense_batch(plain)
+    ws_small = lib.tm_jv_workspace_bytes(*plain.shape)
+    for rep in range(2):
+        print(f"xl then plain, round {rep}", flush=True)
+        _c_abi_solve(lib, lib.tm_jv_dense_batch_f32, xl, lib.tm_jv_workspace_bytes(*xl.shape),
+                     device)
+        got = _c_abi_solve(lib, lib.tm_jv_dense_batch_f32, plain, ws_small, device)
+        np.testing.assert_array_equal(got, want, err_msg=f"round {rep}")
 
 
 def test_large_k_error_contracts_both_workspaces(device):

@@ -1607,7 +1607,8 @@ namespace {
 // records), or 0 when the shape has none.
 size_t prefill_offset(int64_t B, int32_t N, int32_t M) {
     const int K = N > M ? N : M;
-    if (B <= 0 || N <= 0 || M <= 0 || K <= kTile || K > jv_large_max_k())
+    if (B <= 0 || N <= 0 || M <= 0 || K <= kTile || K > jv_large_max_k() ||
+        jv_large_prep_bytes(B, N, M) == 0)
         return 0;
     return (tm_jv_workspace_bytes(B, N, M) + 255) / 256 * 256;
 }

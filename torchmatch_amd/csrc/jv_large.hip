@@ -23,6 +23,8 @@
 #include <math.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "jv_batch.h"
 #include "jv_common.h"
 #include "jv_compact.h"
@@ -31,22 +33,29 @@
 namespace tmamd {
 namespace {
 
-constexpr int kMaxLargeK = 1024;
+constexpr int kMaxLargeK = 1024;   // with the row cache and the prefill
 constexpr int kMaxChunks = kMaxLargeK / 64;
+constexpr int kMaxXLK = 2048;      // beyond: no row cache (the state alone fills 80 KiB)
+constexpr int kXLChunks = kMaxXLK / 64;
 constexpr int kCacheSlots = 16;  // row-cache depth; one slot per lane of lanes 0..15
 constexpr int kKeyLarge = __builtin_bit_cast(int, kLarge);  // fkey(kLarge): kLarge > 0
 
-struct LargeLds {
-    float v[kMaxLargeK];
-    float d[kMaxLargeK];
-    float rbuf[kMaxLargeK];
-    int32_t y[kMaxLargeK];
-    int32_t x[kMaxLargeK];
-    int32_t fr[kMaxLargeK];
-    int32_t pred[kMaxLargeK];
-    int32_t cols[kMaxLargeK];
-    int32_t ev[kMaxLargeK];  // claims in the column reduction, swap events later
-    int32_t emap[kMaxLargeK];  // position -> index in the current tie run, else -1
+// The solve's LDS for K <= KMAX; SLOTS = 0: no row cache (its arrays are one
+// row long and never touched).
+template <int KMAX, int SLOTS>
+struct LargeLdsT {
+    static constexpr int kMax = KMAX;
+    static constexpr int kSlots = SLOTS;
+    float v[KMAX];
+    float d[KMAX];
+    float rbuf[KMAX];
+    int32_t y[KMAX];
+    int32_t x[KMAX];
+    int32_t fr[KMAX];
+    int32_t pred[KMAX];
+    int32_t cols[KMAX];
+    int32_t ev[KMAX];  // claims in the column reduction, swap events later
+    int32_t emap[KMAX];  // position -> index in the current tie run, else -1
     // Row cache of the augmenting row reduction: for row i, up to
     // kCacheSlots columns that were its smallest reduced costs when it was
     // filled (ascending column order, -1 = empty slot), their costs, and tau
@@ -61,10 +70,12 @@ struct LargeLds {
     // On the C3 batch's slowest problem 16 prefilled slots leave 9 of its
     // 2,496 row-reduction steps to scan their row, 8 left 80 (CPU model of
     // the cache policy, which reproduces the kernel's counts).
-    alignas(16) int16_t cq[kMaxLargeK][kCacheSlots];  // 16-byte copies (copy_to_lds)
-    alignas(16) float cg[kMaxLargeK][kCacheSlots];
-    float ctau[kMaxLargeK];
+    alignas(16) int16_t cq[SLOTS ? KMAX : 1][kCacheSlots];  // 16-byte copies (copy_to_lds)
+    alignas(16) float cg[SLOTS ? KMAX : 1][kCacheSlots];
+    float ctau[SLOTS ? KMAX : 1];
 };
+typedef LargeLdsT<kMaxLargeK, kCacheSlots> LargeLds;
+typedef LargeLdsT<kMaxXLK, 0> LargeLdsXL;  // 64 < K <= 2048 without the cache: 80 KiB
 
 // The virtually padded K x K tile: 0 outside (N, M), +inf -> sentinel.
 struct CostView {
@@ -126,12 +137,13 @@ __device__ __forceinline__ void lds_sync() {
 // when event i ran -- the original element there, unless h0 + i was an
 // earlier event's position pos_j (j < i), in which case it is what event j
 // received, and so on down the chain.  Leaves emap all -1.
-__device__ void apply_tie_run(LargeLds &L, int k0, int n, int h0) {
+template <class LDS>
+__device__ void apply_tie_run(LDS &L, int k0, int n, int h0) {
     const int lane = lane_id();
     for (int i = lane; i < n; i += 64)
         L.emap[L.ev[k0 + i] & 0x7fffffff] = i;
     lds_sync();
-    constexpr int kPer = kMaxLargeK / 64;
+    constexpr int kPer = LDS::kMax / 64;
     int a[kPer], b[kPer];
 #pragma unroll
     for (int t = 0; t < kPer; ++t) {
@@ -171,7 +183,8 @@ __device__ void apply_tie_run(LargeLds &L, int k0, int n, int h0) {
 // minimum (swap with lo, hi back to lo + 1), clear = a tie (swap with hi, then
 // hi + 1).  Each new minimum is one swap; each run of ties in between goes
 // through apply_tie_run.  Returns hi (uniform).
-__device__ int replay_find_events(LargeLds &L, int n_ev, int lo) {
+template <class LDS>
+__device__ int replay_find_events(LDS &L, int n_ev, int lo) {
     const int lane = lane_id();
     int hi = lo + 1;
     int k = 0;
@@ -209,7 +222,8 @@ __device__ int replay_find_events(LargeLds &L, int n_ev, int lo) {
 
 // Append the set bits of `mask` (positions base + lane) to L.ev in increasing
 // order, tagged with `tag`; returns the new count (uniform).
-__device__ __forceinline__ int append_events(LargeLds &L, int n_ev, uint64_t mask, int base,
+template <class LDS>
+__device__ __forceinline__ int append_events(LDS &L, int n_ev, uint64_t mask, int base,
                                              uint32_t tag_mask_rec, uint64_t rec_mask) {
     const int lane = lane_id();
     const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
@@ -224,9 +238,13 @@ __device__ __forceinline__ int append_events(LargeLds &L, int n_ev, uint64_t mas
 // A row's costs, chunk e of lane l at [e]; a vector value, so a read at a
 // wave-uniform chunk compiles to an indexed register move.
 typedef float f32x16 __attribute__((ext_vector_type(kMaxChunks)));
+typedef float f32x32 __attribute__((ext_vector_type(kXLChunks)));
+template <int NC> struct ChunkVec { typedef f32x16 type; };
+template <> struct ChunkVec<kXLChunks> { typedef f32x32 type; };
 
 // Lane l's value of chunk e (e, l uniform).
-__device__ __forceinline__ float chunk_value(const f32x16 &v, int e, int l) {
+template <class V>
+__device__ __forceinline__ float chunk_value(const V &v, int e, int l) {
     return readlane_f(v[e], l);
 }
 
@@ -297,11 +315,11 @@ __device__ __forceinline__ int first_column(const int (&kk)[NC], int k, int x1, 
 // cache of fi is refilled from the same scan.  Nothing goes through LDS: the
 // columns of the two (three) smallest come from wave minima over the column
 // indices, their costs from the owning lanes.
-template <int NC>
-__device__ void scan_row(LargeLds &L, const CostView &C, int fi, int E, int K,
+template <int NC, class LDS>
+__device__ void scan_row(LDS &L, const CostView &C, int fi, int E, int K,
                          bool refill, int &j1, int &j2, float &u1, float &u2) {
     const int lane = lane_id();
-    f32x16 cr;
+    typename ChunkVec<NC>::type cr;
     {
         float c[NC];
         load_row<NC>(C, fi, c);
@@ -402,6 +420,8 @@ __device__ void scan_row(LargeLds &L, const CostView &C, int fi, int E, int K,
         else
             j2 = -1;
     }
+    if constexpr (LDS::kSlots == 0)
+        return;
     if (!refill || j2 < 0)
         return;
     // refill: the third smallest (value, column) after j1, j2 and the fourth
@@ -667,8 +687,8 @@ jv_large_rowcache_kernel(const float *__restrict__ costs, int64_t B, int N, int 
 // augmenting row reduction, the first unassigned column of a minimum group
 // ending a path, the dual update (v + d) - min and FLT_MAX as the transfer's
 // starting minimum.
-template <bool COMPACT, int NC>
-__device__ __forceinline__ bool large_solve(const int K, const int E, LargeLds &L, const CostView &C,
+template <bool COMPACT, int NC, class LDS>
+__device__ __forceinline__ bool large_solve(const int K, const int E, LDS &L, const CostView &C,
                                             const LargePrep &P) {
     const int lane = lane_id();
 
@@ -812,7 +832,9 @@ __device__ __forceinline__ bool large_solve(const int K, const int E, LargeLds &
     // ---- augmenting row reduction (carr_dense, jonker_dense_flat.h:178-235) ----
     const uint32_t rr_limit =
         COMPACT ? compact_arr_guard(K) : 4u * (uint32_t)K * (uint32_t)K + 64u;
-    if (P.v != nullptr) {
+    constexpr bool kCache = LDS::kSlots > 0;  // K > kMaxLargeK: every step scans
+    if constexpr (!kCache) {
+    } else if (P.v != nullptr) {
         // every real row's cache from the prefill (jv_large_rowcache_kernel)
         copy_to_lds(&L.cq[0][0], P.cq, C.N * kCacheSlots / 2);  // dwords of 16-bit columns
         copy_to_lds(&L.cg[0][0], P.cg, C.N * kCacheSlots);
@@ -828,6 +850,12 @@ __device__ __forceinline__ bool large_solve(const int K, const int E, LargeLds &
     } else {
         for (int i = lane; i < K; i += 64)
             L.ctau[i] = -finf();
+        // Every slot empty (column -1): the hit tests below compare keys of
+        // the slots' costs, and a stale LDS word read as a cost could be a
+        // NaN whose key is below tau's even at tau = -inf.
+        int32_t *cq32 = reinterpret_cast<int32_t *>(&L.cq[0][0]);
+        for (int w = lane; w < C.N * (kCacheSlots / 2); w += 64)
+            cq32[w] = -1;
     }
     lds_sync();
     // lanes 0..kCacheSlots-1 hold the cache slots: a slot column is live
@@ -852,9 +880,13 @@ __device__ __forceinline__ bool large_solve(const int K, const int E, LargeLds &
         // scan refills a cache row, before its other writes (which touch no
         // cache word).
         int fi_next = uniform_i(L.fr[0]);
-        float tau_n = L.ctau[fi_next];
-        int q_n = L.cq[fi_next][lane & (kCacheSlots - 1)];
-        float g_n = L.cg[fi_next][lane & (kCacheSlots - 1)];
+        float tau_n = 0.f, g_n = 0.f;
+        int q_n = 0;
+        if constexpr (kCache) {
+            tau_n = L.ctau[fi_next];
+            q_n = L.cq[fi_next][lane & (kCacheSlots - 1)];
+            g_n = L.cg[fi_next][lane & (kCacheSlots - 1)];
+        }
         // The end of a step (carr_dense's update, jonker_dense_flat.h:
         // 210-232), given row fi's two minima j1 / j2 (j2 = -1: none), their
         // owners y1 / y2, v[j1], lowered = v[j1] - (u2 - u1) and whether it
@@ -879,7 +911,7 @@ __device__ __forceinline__ bool large_solve(const int K, const int E, LargeLds &
             const int tail = push & (dec ^ 1);  // ... or it joins the next round
             const uint32_t slot = cur - 1;  // the queue slot this step consumed
             fi_next = back ? i0 : fqs;
-            {
+            if constexpr (kCache) {
                 // clamped: after the last step fq is read past the queue
                 const int rn = min(max(fi_next, 0), K - 1);
                 tau_n = L.ctau[rn];
@@ -913,12 +945,11 @@ __device__ __forceinline__ bool large_solve(const int K, const int E, LargeLds &
             const int fi = fi_next;
             ++cur;
             const int fq = L.fr[min(cur, (uint32_t)K - 1)];
-            if (fi < C.N) {
+            if (kCache && fi < C.N) {
                 // The cached two minima, straight-line to the step's end.
-                // No branch on tau: a row never filled has tau = -inf, which
-                // no u2 is below.  Slot columns outside [0, K) (a row never
-                // filled, without the prefill) read column 0 and carry no
-                // key.  tau as a key: fkey is monotone and tau was stored
+                // No branch on tau: a row never filled has tau = -inf and
+                // every slot empty.  Slot columns outside [0, K) read column
+                // 0 and carry no key.  tau as a key: fkey is monotone and tau was stored
                 // from a key, so u2 < tau <=> key(u2) < key(tau); and u2 <
                 // LARGE, so that the reference's (LARGE, -1) start slot
                 // cannot win.
@@ -1037,7 +1068,7 @@ __device__ __forceinline__ bool large_solve(const int K, const int E, LargeLds &
         // then the cached columns at that key (slots ascend with the
         // column), and when one of them is unassigned the path is that
         // single column, as below.
-        if (start < C.N) {
+        if (kCache && start < C.N) {
             const float tau_l = L.ctau[start];
             const int qs = L.cq[start][lane & (kCacheSlots - 1)];
             const float g = L.cg[start][lane & (kCacheSlots - 1)];
@@ -1306,7 +1337,8 @@ __global__ void __launch_bounds__(64)
 jv_solve_large_kernel(const float *__restrict__ costs, int64_t B, int N, int M,
                       const JvStats *__restrict__ partial, int n_partial, LargePrep prep,
                       int64_t *__restrict__ out, uint32_t *__restrict__ status) {
-    __shared__ LargeLds L;
+    // past 16 chunks (K > 1024) the cache-less layout
+    __shared__ typename std::conditional<(NC > kMaxChunks), LargeLdsXL, LargeLds>::type L;
     const int lane = lane_id();
     const int K = N > M ? N : M;
     const int E = (K + 63) / 64;
@@ -1406,7 +1438,7 @@ int launch_large(const float *costs, int64_t B, int N, int M, const JvStats *par
     const int K = N > M ? N : M;
     const int E = (K + 63) / 64;
     LargePrep prep{nullptr, nullptr, nullptr, nullptr, nullptr};
-    if (prep_ws != nullptr) {
+    if (prep_ws != nullptr && K <= kMaxLargeK) {
         const PrepBuffers pb = prep_buffers(prep_ws, B, N, M);
         hipLaunchKernelGGL(jv_large_colmin_kernel,
                            dim3((unsigned)B, (unsigned)((K + kColminCols - 1) / kColminCols)),
@@ -1444,12 +1476,16 @@ int launch_large(const float *costs, int64_t B, int N, int M, const JvStats *par
         return go(jv_solve_large_kernel<COMPACT, 8>);
     if (E <= 12)
         return go(jv_solve_large_kernel<COMPACT, 12>);
-    return go(jv_solve_large_kernel<COMPACT, kMaxChunks>);
+    if (E <= kMaxChunks)
+        return go(jv_solve_large_kernel<COMPACT, kMaxChunks>);
+    return go(jv_solve_large_kernel<COMPACT, kXLChunks>);
 }
 } // namespace
 
 size_t jv_large_prep_bytes(int64_t B, int N, int M) {
     const int64_t K = N > M ? N : M;
+    if (K > kMaxLargeK)
+        return 0;  // no prefill past the cached layout
     return 2 * align256((size_t)(B * K) * 4) + align256((size_t)(B * N) * kCacheSlots * 2) +
            align256((size_t)(B * N) * kCacheSlots * 4) + align256((size_t)(B * N) * 4);
 }
@@ -1466,8 +1502,8 @@ int launch_jv_compact_large(const float *costs, int64_t B, int N, int M,
     return launch_large<true>(costs, B, N, M, partial, n_partial, prep_ws, out, status, stream);
 }
 
-int jv_large_max_k() { return kMaxLargeK; }
+int jv_large_max_k() { return kMaxXLK; }
 
-int jv_compact_max_k() { return kMaxLargeK; }
+int jv_compact_max_k() { return kMaxXLK; }
 
 } // namespace tmamd
