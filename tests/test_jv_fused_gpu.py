@@ -149,6 +149,28 @@ def test_sync_entry_matches_oracle(B, N, M, frac_inf, compact, device):
     assert replays <= B
 
 
+@pytest.mark.parametrize("compact", [False, True])
+def test_small_k_after_large_tiles(compact, device):
+    """Tiles with K < 64 are stored up to the next 16-row boundary (0 past
+    K), and the column build and the certificate stop there.  Regression
+    test for rows left unset: stale LDS words from the 64 x 64 tiles of large
+    costs solved just before, on as many workgroups, would enter the
+    certificate's cost scale (tau = 2^-20 max |c|) and send the square
+    problems to the exact replay: the same mappings, but counted."""
+    g = torch.Generator().manual_seed(31)
+    big = torch.rand(1024, 64, 64, generator=g) * 1e6
+    for n, m in [(5, 5), (17, 17), (20, 20), (33, 33), (47, 47), (30, 41)]:
+        cost = torch.rand(1024, n, m, generator=g)
+        print(f"large tiles, then {tuple(cost.shape)} compact={compact}", flush=True)
+        assert _sync(big, device, compact=compact)[0] == _native.TM_OK
+        code, replays, got = _sync(cost, device, compact=compact)
+        assert code == _native.TM_OK
+        want = (jv.jv_compact_batch if compact else jv.jv_dense_batch)(cost.numpy())
+        assert (got == want).all()
+        # uniform costs: near-ties within tau are rare (a few per 10^4 problems)
+        assert replays <= 8, f"{replays} replays on {tuple(cost.shape)}"
+
+
 def test_sync_replay_count_and_errors(device):
     # integer ties: every square problem fails the certificate and replays
     g = torch.Generator().manual_seed(5)

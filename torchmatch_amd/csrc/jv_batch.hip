@@ -1127,6 +1127,10 @@ __device__ __forceinline__ bool certified_solve(const int K, WaveLds &L, const C
     uint32_t row_lo = 0, row_hi = 0;  // lane i: near-tight columns of row i
 #pragma unroll
     for (int i = 0; i < kTile; ++i) {
+        // rows from K on read r = +inf; past the first 16-row boundary at or
+        // beyond K they are not visited (nor loaded into `col`)
+        if (i % 16 == 0 && i >= K)
+            break;
         const double r = ((double)col.get(i) - L.ubuf[i]) - vd;
         neg |= ballot(r < 0.0);
         const uint64_t tight = ballot(r <= td);
@@ -1240,7 +1244,10 @@ __device__ __forceinline__ void load_columns(const int K, const WaveLds &L, Col6
 #pragma unroll
     for (int i = 0; i < kTile; ++i) {
         const bool row = FULL || i < K;
-        const float val = row ? L.c[i * kTile + lane] : 0.f;
+        if (!FULL && i % 16 == 0 && i >= K)
+            break;  // rows from here on are never read from `col`
+        // rows K .. (the next multiple of 16) - 1 hold 0 in the tile
+        const float val = L.c[i * kTile + lane];
         col.set(i, val);
         amax = fmaxf(amax, fabsf(val));
         if (row && val < vmin) {
@@ -1380,22 +1387,39 @@ jv_solve_kernel(const float *__restrict__ costs, int64_t B, int N, int M,
         if (wide) {
             tile_stats_wide(q, mx, mn, flags);
         } else {
+            // Other shapes: the tile goes to the LDS as loaded (0 outside the
+            // N x M problem) in the same pass that folds the statistics, 16
+            // rows of loads in flight at a time (clamped addresses, so every
+            // load is unconditional), up to the first 16-row boundary at or
+            // past K (load_columns reads those rows).  A tile that holds +-inf
+            // or NaN leaves below without being used, so no value needs the
+            // sentinel here.
             float fmx = -finf(), fmn = finf();
             uint32_t f = 0;
-            for (int i = 0; i < N; ++i) {
-                if (lane < M) {
-                    const float x = src[(int64_t)i * M + lane];
-                    if (isnan(x)) {
-                        f |= kJvFlagNan;
-                    } else if (isinf(x)) {
-                        f |= (x < 0.f) ? kJvFlagNegInf : kJvFlagPosInf;
-                    } else {
-                        f |= kJvFlagAnyFinite;
-                        if (__float_as_uint(x) == 0x80000000u)
-                            f |= kJvFlagNegZero;
-                        fmx = fmaxf(fmx, x);
-                        fmn = fminf(fmn, x);
-                    }
+            const bool lane_in = lane < M;
+            const int64_t lane_off = lane_in ? lane : M - 1;
+            for (int i0 = 0; i0 < K; i0 += 16) {
+                float raw[16];
+#pragma unroll
+                for (int u = 0; u < 16; ++u) {
+                    const int i = i0 + u < N ? i0 + u : N - 1;
+                    raw[u] = src[(int64_t)i * M + lane_off];
+                }
+#pragma unroll
+                for (int u = 0; u < 16; ++u) {
+                    const int i = i0 + u;
+                    const bool real = lane_in && i < N;
+                    const float x = raw[u];
+                    const bool nan = real && isnan(x);
+                    const bool inf = real && isinf(x);
+                    const bool fin = real && !isnan(x) && !isinf(x);
+                    f |= nan ? kJvFlagNan : 0u;
+                    f |= inf ? ((x < 0.f) ? kJvFlagNegInf : kJvFlagPosInf) : 0u;
+                    f |= fin ? kJvFlagAnyFinite : 0u;
+                    f |= (fin && __float_as_uint(x) == 0x80000000u) ? kJvFlagNegZero : 0u;
+                    fmx = fin ? fmaxf(fmx, x) : fmx;
+                    fmn = fin ? fminf(fmn, x) : fmn;
+                    L.c[i * kTile + lane] = real ? x : 0.f;
                 }
             }
             mx = wave_max(fmx);
@@ -1461,7 +1485,10 @@ jv_solve_kernel(const float *__restrict__ costs, int64_t B, int N, int M,
     // for its minimum and first arg-min row (strict '<' from LARGE,
     // jonker_dense_flat.h:136-144)
     bool inf_here = false;  // this problem holds +inf (the sentinel is in the tile)
-    if (wide && MODE == kJvFusedSolve) {
+    if (MODE == kJvFusedSolve && !wide) {
+        // stored with the statistics above (a tile solved in this mode holds
+        // no +inf)
+    } else if (wide && MODE == kJvFusedSolve) {
         // a tile solved in this mode holds no +inf: stored as loaded
 #pragma unroll
         for (int k = 0; k < 16; ++k)
@@ -1482,8 +1509,11 @@ jv_solve_kernel(const float *__restrict__ costs, int64_t B, int N, int M,
             reinterpret_cast<float4 *>(L.c)[k * 64 + lane] = t;
         }
     } else {
+        // up to the first 16-row boundary at or past K (load_columns reads
+        // those rows; rows from K on hold 0)
+        const int k16 = (K + 15) & ~15;
 #pragma unroll 16
-        for (int i = 0; i < K; ++i) {
+        for (int i = 0; i < k16; ++i) {
             float val = 0.f;
             if (i < N && lane < M) {
                 val = src[(int64_t)i * M + lane];
