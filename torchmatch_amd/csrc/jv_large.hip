@@ -572,23 +572,39 @@ jv_large_rowcache_kernel(const float *__restrict__ costs, int64_t B, int N, int 
     const int K = N > M ? N : M;
     const int E = (K + 63) / 64;
     const int lane = lane_id();
+    // each wave's candidates of the threshold selection: keys, columns and
+    // costs at fixed offsets from one address
+    __shared__ uint32_t rc_cand[4][3][64];
     CostView C;
     C.N = N;
     C.M = M;
     C.sentinel = 1.f;
     bool have_sentinel = false;
     const int64_t rows = B * (int64_t)N;
-    for (int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); row < rows;
+    // the wave's index is uniform: row bases stay scalar and the loads take
+    // a scalar base with 32-bit lane offsets
+    const int wave = uniform_i((int)(threadIdx.x >> 6));
+    for (int64_t row = (int64_t)blockIdx.x * 4 + wave; row < rows;
          row += (int64_t)gridDim.x * 4) {
         const int64_t b = row / N;
         const int i = (int)(row - b * N);
         C.src = costs + b * (int64_t)N * M;
         const float *vb = v_in + b * K;
+        const char *rsrc = reinterpret_cast<const char *>(C.src + (int64_t)i * M);
+        const char *vsrc = reinterpret_cast<const char *>(vb);
+        // byte offsets from the scalar row bases, clamped into the row; the
+        // opaque copy of lane * 4 keeps the compiler from holding all of
+        // them (as 64-bit values) across the row loop
+        uint32_t lane4 = (uint32_t)lane * 4u;
+        asm volatile("" : "+v"(lane4));
+        const uint32_t lim_m = (uint32_t)(M - 1) * 4u, lim_k = (uint32_t)(K - 1) * 4u;
         float raw[NC], vv[NC];
-        load_row_raw<NC>(C, i, raw);
 #pragma unroll
         for (int e = 0; e < NC; ++e)
-            vv[e] = vb[min(e * 64 + lane, K - 1)];
+            raw[e] = *reinterpret_cast<const float *>(rsrc + min(lane4 + (uint32_t)e * 256u, lim_m));
+#pragma unroll
+        for (int e = 0; e < NC; ++e)
+            vv[e] = *reinterpret_cast<const float *>(vsrc + min(lane4 + (uint32_t)e * 256u, lim_k));
         // the statistics are folded while the row is in flight (the raw
         // costs need the sentinel only from here on)
         if (!have_sentinel) {
@@ -601,9 +617,88 @@ jv_large_rowcache_kernel(const float *__restrict__ costs, int64_t B, int N, int 
 #pragma unroll
         for (int e = 0; e < NC; ++e) {
             const int j = e * 64 + lane;
-            const float c = fix_cost(C, raw[e], j);
+            // fix_cost in bit operations (its selects became two nested
+            // branches per value here): +inf -> sentinel, columns >= M -> 0
+            const int rb = __float_as_int(raw[e]);
+            const int fin = -(int)((rb & 0x7f800000) != 0x7f800000);
+            const int cb = ((rb & fin) | (__float_as_int(C.sentinel) & ~fin)) & -(int)(j < M);
+            const float c = __int_as_float(cb);
             cr[e] = c;
-            kk[e] = (e < E && j < K) ? fkey(c - vv[e]) : kKeyNone;
+            // kKeyNone past the row: the key is formed unconditionally and
+            // raised by a max
+            kk[e] = max(fkey(c - vv[e]), (e < E && j < K) ? (int)0x80000000 : kKeyNone);
+        }
+        // Threshold selection.  T = the 17th smallest of the 64 lane minima
+        // (as a multiset), from a bitwise search on ballot counts: at least
+        // 17 keys are <= T, so the row's 17 smallest (key, column) pairs all
+        // are.  The candidates (key <= T; ~20 on the (64, 512, 768) batch)
+        // go to LDS in column order, and each takes its rank in (key,
+        // column) order from the others: ranks 0..15 are the slots (in
+        // column order already), rank 16 gives tau.  More than 64 candidates
+        // (wide ties) take the round-by-round selection below.
+        {
+            uint32_t lmin = 0xffffffffu;
+#pragma unroll
+            for (int e = 0; e < NC; ++e)
+                lmin = min(lmin, (uint32_t)kk[e] ^ 0x80000000u);
+            uint32_t T = 0;
+#pragma unroll
+            for (int bit = 31; bit >= 0; --bit) {
+                const uint32_t x = T | ((1u << bit) - 1u);
+                const uint64_t m = ballot(lmin <= x);
+                if (__builtin_popcount((uint32_t)m) + __builtin_popcount((uint32_t)(m >> 32)) <=
+                    kCacheSlots)
+                    T |= 1u << bit;
+            }
+            T = min(T, 0xfffffffeu);  // a missing key (0xffffffff) is never a candidate
+            uint32_t *sk = rc_cand[wave][0];
+            int *sc = reinterpret_cast<int *>(rc_cand[wave][1]);
+            float *sg = reinterpret_cast<float *>(rc_cand[wave][2]);
+            int total = 0;
+#pragma unroll
+            for (int e = 0; e < NC; ++e) {
+                const bool cand = ((uint32_t)kk[e] ^ 0x80000000u) <= T;
+                const uint64_t m = ballot(cand);
+                const int pos = total + lanes_below(m);
+                if (cand && pos < 64) {
+                    sk[pos] = (uint32_t)kk[e] ^ 0x80000000u;
+                    sc[pos] = e * 64 + lane;
+                    sg[pos] = cr[e];
+                }
+                total += __builtin_popcountll(m);
+            }
+            if (total <= 64) {
+                lds_sync();
+                const bool have = lane < total;
+                const uint32_t mu = have ? sk[lane] : 0xffffffffu;
+                const int mc = sc[lane];
+                const float mg = sg[lane];
+                lds_sync();  // read before the next row's candidates are written
+                int rank = 0;
+                for (int q = 0; q < total; ++q) {
+                    const uint32_t uq = (uint32_t)readlane_i((int)mu, q);
+                    rank += (uq < mu || (uq == mu && q < lane)) ? 1 : 0;
+                }
+                const bool sel = have && rank < kCacheSlots;
+                const uint64_t ms = ballot(sel);
+                const int nsel = __builtin_popcountll(ms);
+                if (sel) {
+                    const int slot = lanes_below(ms);
+                    cq_out[row * kCacheSlots + slot] = (int16_t)mc;
+                    cg_out[row * kCacheSlots + slot] = mg;
+                } else if (lane >= nsel && lane < kCacheSlots) {
+                    cq_out[row * kCacheSlots + lane] = (int16_t)-1;
+                    cg_out[row * kCacheSlots + lane] = 0.f;
+                }
+                const uint64_t mt = ballot(have && rank == kCacheSlots);
+                const float tau =
+                    mt == 0 ? finf()
+                            : key_to_float((int)((uint32_t)readlane_i((int)mu, first_lane(mt | (1ull << 63))) ^
+                                                 0x80000000u));
+                if (lane == 0)
+                    tau_out[row] = tau;
+                continue;
+            }
         }
         // Each lane keeps its three smallest (key, chunk) not yet taken, in
         // (key, chunk) order (a later chunk is a larger column).  The row's

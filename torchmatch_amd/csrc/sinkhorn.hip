@@ -1497,6 +1497,26 @@ sk_col_merge_blk(const float2 *__restrict__ colpart, const float *__restrict__ K
     } else {  // shares of T_j: plain adds, in float64
         const float *sum = reinterpret_cast<const float *>(colpart);
         double tsum = 0.0;
+        // sixteen loads in flight, then the same adds in the same order as
+        // the four-load loop below
+        for (; c + 15 * kMergeWaves < n_chunk; c += 16 * kMergeWaves) {
+            float p[16];
+#pragma unroll
+            for (int u = 0; u < 16; ++u)
+                p[u] = sum[(b * n_chunk + c + u * kMergeWaves) * M + jj];
+#pragma unroll
+            for (int q = 0; q < 16; q += 4)
+                tsum += ((double)p[q] + (double)p[q + 1]) + ((double)p[q + 2] + (double)p[q + 3]);
+        }
+        for (; c + 7 * kMergeWaves < n_chunk; c += 8 * kMergeWaves) {
+            float p[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+                p[u] = sum[(b * n_chunk + c + u * kMergeWaves) * M + jj];
+#pragma unroll
+            for (int q = 0; q < 8; q += 4)
+                tsum += ((double)p[q] + (double)p[q + 1]) + ((double)p[q + 2] + (double)p[q + 3]);
+        }
         for (; c + 3 * kMergeWaves < n_chunk; c += 4 * kMergeWaves) {
             float p[4];
 #pragma unroll

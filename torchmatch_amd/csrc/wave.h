@@ -131,6 +131,11 @@ __device__ __forceinline__ float wave_shift_up(float identity, float x) {
 }
 
 __device__ __forceinline__ int first_lane(uint64_t m) { return (int)__builtin_ctzll(m); }
+// Number of lanes below this one whose bit is set in m.
+__device__ __forceinline__ int lanes_below(uint64_t m) {
+    return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
+                                          __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+}
 __device__ __forceinline__ int last_lane(uint64_t m) { return 63 - (int)__builtin_clzll(m); }
 
 } // namespace tmamd
