@@ -15,7 +15,7 @@ import numpy as np
 
 KINDS_SMALL = ["uniform", "tied", "masked", "tied_masked", "negative", "huge"]
 KINDS_LARGE = ["uniform", "tied", "masked", "tied_masked", "negative"]
-KINDS_PREFILL = ["uniform", "tied", "masked", "tied_masked"]
+KINDS_PREFILL = ["uniform", "tied", "masked", "tied_masked", "negative_masked"]
 KINDS_COMPACT = ["uniform", "tied", "masked", "tied_masked", "negative", "huge", "big",
                  "signed_zero"]
 KINDS_COMPACT_LARGE = ["uniform", "tied", "masked", "tied_masked", "negative", "huge", "big"]
@@ -47,6 +47,11 @@ def random_batch(rng, kind: str, b: int, n: int, m: int) -> np.ndarray:
         c[rng.random((b, n, m)) < 0.3] = np.inf
     elif kind == "negative":
         c = (rng.random((b, n, m), dtype=np.float32) - 0.7) * 100.0
+    elif kind == "negative_masked":
+        # every finite cost <= -2, so the sentinel (max + 1) * (K + 1) lies
+        # below all of them and +inf cells become column minima
+        c = -(rng.random((b, n, m), dtype=np.float32) * 100.0 + 2.0)
+        c[rng.random((b, n, m)) < 0.3] = np.inf
     elif kind == "huge":  # beyond 1e15: lane-serial path
         c = rng.random((b, n, m), dtype=np.float32) * np.float32(3e16)
     elif kind == "big":  # 1e12 .. 1e15: serial for compact, wave path for dense
