@@ -1135,25 +1135,45 @@ __device__ __forceinline__ bool large_solve(const int K, const int E, LDS &L, co
     // rbuf, unused by the paths; later padded paths take the next entry
     // still unassigned (a real row's single-column path may have taken
     // one).  A full search, which moves duals, ends the run.
+    // Each padded start scans the list from run_pos and takes the first
+    // entry still unassigned, so a run of consecutive padded starts takes
+    // the list's unassigned entries in order: the k-th start of the run the
+    // k-th.  That is done 64 starts against 64 entries per round (ranks
+    // from a ballot); run_pos then stands where the sequential scans would
+    // leave it: after the last entry taken, or past the window when the
+    // starts outnumber its unassigned entries.  A start the list cannot
+    // serve (it ran out) or a real row takes the paths below.
     int *const run_list = reinterpret_cast<int *>(L.rbuf);
     int run_pos = 0, run_n = 0;
     for (int f = 0; f < n_free; ++f) {
-        const int start = uniform_i(L.fr[f]);
+        int start = uniform_i(L.fr[f]);
         if (start >= C.N && run_pos < run_n) {
-            int found = -1;
-            while (run_pos < run_n) {
-                const int j = uniform_i(run_list[run_pos++]);
-                if (uniform_i(L.y[j]) < 0) {
-                    found = j;
-                    break;
+            do {
+                const int fl = f + lane;
+                const int sl = L.fr[min(fl, K - 1)];
+                const uint64_t padm = ballot(fl < n_free && sl >= C.N);
+                const int R = ~padm == 0 ? 64 : (int)__builtin_ctzll(~padm);  // >= 1
+                const int pl = run_pos + lane;
+                const int el = run_list[min(pl, run_n - 1)];
+                const bool opn = pl < run_n && L.y[el] < 0;
+                const uint64_t om = ballot(opn);
+                const int A = min(R, (int)__builtin_popcountll(om));
+                const int k = lanes_below(om);  // rank of an open entry
+                const int sk = __shfl(sl, min(k, 63));  // its start row
+                if (opn && k < A) {
+                    L.y[el] = sk;
+                    L.x[sk] = el;
                 }
-            }
-            if (found >= 0) {
-                L.y[found] = start;  // every lane writes the same word
-                L.x[start] = found;
+                if (A == R)  // every start served: after the A-th open entry
+                    run_pos += first_lane(ballot(opn && k == A - 1)) + 1;
+                else  // the window's unassigned entries all taken, the rest skipped
+                    run_pos = min(run_pos + 64, run_n);
+                f += A;
                 lds_sync();
-                continue;
-            }
+            } while (f < n_free && run_pos < run_n && uniform_i(L.fr[f]) >= C.N);
+            if (f >= n_free)
+                break;
+            start = uniform_i(L.fr[f]);
         }
         // The first find_dense from the start row's cache, without its row:
         // when the smallest cached reduced cost is below tau, it is the
