@@ -83,6 +83,19 @@ def prefill_batches(kind: str):
         yield n, m, random_batch(rng, kind, 4, n, m)
 
 
+# N < M with padded-row runs from a few rows to several hundred
+KINDS_PADDED = ["uniform", "tied", "masked", "tied_masked", "negative_masked"]
+
+
+def padded_batches(kind: str):
+    rng = np.random.default_rng(zlib.crc32(("padded" + kind).encode()))
+    shapes = [(65, 1000), (70, 200), (129, 130), (200, 460)]
+    shapes += [(int(n), int(rng.integers(n + 1, min(1024, 3 * n) + 1)))
+               for n in rng.integers(40, 300, 6)]
+    for n, m in shapes:
+        yield n, m, random_batch(rng, kind, 4, n, m)
+
+
 def xl_batches(kind: str):
     rng = np.random.default_rng(zlib.crc32(("xl" + kind).encode()))
     for n, m in XL_SHAPES:

@@ -79,6 +79,28 @@ def test_large_k_vs_oracle(kind, device):
         np.testing.assert_array_equal(got, want, err_msg=f"{kind} {c.shape}")
 
 
+@pytest.mark.parametrize("kind", jv_inputs.KINDS_PADDED)
+def test_padded_row_runs_vs_oracle(kind, device):
+    """N < M: the padded rows (all 0) of the row reduction run in bulk while
+    no dual falls, and the augmentation's padded start rows take the tied
+    block's list 64 at a time.  Random shapes from a few padded rows to
+    runs of several hundred (more than one 64-entry window), dense with and
+    without the prefill workspace, and compact."""
+    lib = _native.lib()
+    for n, m, c in jv_inputs.padded_batches(kind):
+        print(f"padded runs {kind} shape {c.shape}", flush=True)
+        want = jv.jv_dense_batch(c)
+        got = run_op(torch.from_numpy(c), device)
+        np.testing.assert_array_equal(got, want, err_msg=f"{kind} {c.shape}")
+        small = lib.tm_jv_workspace_bytes(4, n, m)
+        got = _c_abi_solve(lib, lib.tm_jv_dense_batch_f32, c, small, device)
+        np.testing.assert_array_equal(got, want, err_msg=f"plain workspace {kind} {c.shape}")
+        got = _c_abi_solve(lib, lib.tm_jv_compact_batch_f32, c,
+                           lib.tm_jv_workspace_bytes_prefill(4, n, m), device)
+        np.testing.assert_array_equal(got, jv.jv_compact_batch(c),
+                                      err_msg=f"compact {kind} {c.shape}")
+
+
 @pytest.mark.parametrize("kind", jv_inputs.KINDS_XL)
 def test_xl_k_vs_oracle(kind, device):
     """1024 < K <= 2048: the 32-chunk instantiation without the row cache

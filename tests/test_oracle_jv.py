@@ -111,6 +111,17 @@ def test_oracle_matches_reference_build_on_prefill_gpu_inputs(kind):
 
 
 @pytest.mark.skipif(not jv.ref_available(), reason="reference build (oracle/_ref) absent")
+@pytest.mark.parametrize("kind", jv_inputs.KINDS_PADDED)
+def test_oracle_matches_reference_build_on_padded_gpu_inputs(kind):
+    """The batches of the GPU padded-row-run test, dense and compact."""
+    for n, m, c in jv_inputs.padded_batches(kind):
+        np.testing.assert_array_equal(jv.jv_dense_batch(c), jv.ref_jv_dense_batch(c),
+                                      err_msg=f"dense {kind} {c.shape}")
+        np.testing.assert_array_equal(jv.jv_compact_batch(c), jv.ref_jv_compact_batch(c),
+                                      err_msg=f"compact {kind} {c.shape}")
+
+
+@pytest.mark.skipif(not jv.ref_available(), reason="reference build (oracle/_ref) absent")
 @pytest.mark.parametrize("kind", jv_inputs.KINDS_XL)
 def test_oracle_matches_reference_build_on_xl_gpu_inputs(kind):
     """K = 1025 ... 2048 (the cache-less instantiation), rectangular both

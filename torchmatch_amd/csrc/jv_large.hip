@@ -1091,6 +1091,71 @@ __device__ __forceinline__ bool large_solve(const int K, const int E, LDS &L, co
             // a padded row, or a cache miss: the row's scan (which refills
             // a real row's cache)
             const bool pad_row = fi >= C.N;
+            if (pad_row && pad_valid && pad_j2 >= 0) {
+                // A run of padded rows while no dual falls.  Each of them
+                // has the same two minima (j1, j2) and lowers nothing, so
+                // step by step: the first takes j1 when j1 is free, every
+                // later one takes j2 and pushes j2's previous owner to the
+                // next round's list (still), and the next row is the next
+                // queue entry.  The run -- this row and the padded rows
+                // queued after it, within the step budget -- is done at
+                // once: the pushed rows are y[j2] (when owned) and the
+                // j2-takers but the last, copied 64 at a time, then the two
+                // owners.  The copy's target never passes its source by
+                // more than one entry (still <= the consumed slot), and each
+                // window is written only after the next one is read.
+                const float vj1 = uniform_f(L.v[pad_j1]);
+                const int cap = COMPACT ? 1 : neg((int)(rr - cur * (uint32_t)K));
+                if (cap && !(vj1 - (pad_u2 - pad_u1) < vj1)) {
+                    const uint32_t first = cur - 1;  // this row's slot
+                    const uint32_t budget = rr_limit - rr;  // further steps allowed
+                    uint32_t R = 1;
+                    for (uint32_t base = cur; R - 1 < budget; base += 64) {
+                        const uint32_t p = base + lane;
+                        const int r = L.fr[min(p, (uint32_t)K - 1)];
+                        const uint64_t pm = ballot(p < (uint32_t)n_free && r >= C.N);
+                        const uint32_t lead = ~pm == 0 ? 64u : (uint32_t)__builtin_ctzll(~pm);
+                        R += lead;
+                        if (lead < 64)
+                            break;
+                    }
+                    R = min(R, budget + 1);
+                    const int y1 = uniform_i(L.y[pad_j1]);
+                    const int y2 = uniform_i(L.y[pad_j2]);
+                    const uint32_t s0 = y1 < 0 ? 1u : 0u;  // the first row takes j1
+                    const int last = uniform_i(L.fr[first + R - 1]);
+                    if (R > s0) {
+                        const uint32_t src0 = first + s0, n_copy = R - 1 - s0;
+                        const uint32_t dst0 = (uint32_t)still + (y2 >= 0 ? 1u : 0u);
+                        int nxt = L.fr[min(src0 + lane, (uint32_t)K - 1)];
+                        for (uint32_t w = 0; w < n_copy; w += 64) {
+                            const int val = nxt;
+                            nxt = L.fr[min(src0 + w + 64 + lane, (uint32_t)K - 1)];
+                            lds_sync();
+                            if (w + lane < n_copy)
+                                L.fr[dst0 + w + lane] = val;
+                            lds_sync();
+                        }
+                        if (y2 >= 0)
+                            L.fr[still] = y2;  // every lane writes the same word
+                        L.y[pad_j2] = last;
+                        still += (int)n_copy + (y2 >= 0 ? 1 : 0);
+                    }
+                    if (s0)
+                        L.y[pad_j1] = fi;
+                    rr += R - 1;
+                    cur += R - 1;
+                    lds_sync();
+                    fi_next = uniform_i(L.fr[min(cur, (uint32_t)K - 1)]);
+                    if constexpr (kCache) {
+                        const int rn = min(max(fi_next, 0), K - 1);
+                        tau_n = L.ctau[rn];
+                        q_n = L.cq[rn][lane & (kCacheSlots - 1)];
+                        g_n = L.cg[rn][lane & (kCacheSlots - 1)];
+                    }
+                    continue;
+                }
+            }
             int j1, j2;
             float u1, u2;
             if (pad_row && pad_valid) {
