@@ -74,17 +74,17 @@ JV_C3_CRITICAL_STEPS = 2750
 # runs and commands are recorded in the profiles/ summaries.
 MEASURED_TRAFFIC = {
     # the fused solve launch on C2 (the op's only launch on this batch)
-    "jv_c2": int((8349.5 * 2 + 584.0) * 1024),
+    "jv_c2": int((8342.0 * 2 + 584.0) * 1024),
     # the K = 768 solve launch on C3 (its tile rows mostly from L2 / MALL)
-    "jv_c3": int((2139.0 * 2 + 256.0) * 1024),
+    "jv_c3": int((2151.0 * 2 + 256.0) * 1024),
     # sk_fused_step + sk_col_merge_blk per C4 iteration: two batch groups of 8,
     # each one pass + one merge (K once, column sums twice)
-    "sinkhorn_c4": int(2 * ((66386.0 + 1236.0) * 2 + 2368.4 + 320.0) * 1024),
+    "sinkhorn_c4": int(2 * ((66378.0 + 1243.0) * 2 + 2369.0 + 320.0) * 1024),
     # the same per iteration of the B = 64 control (two groups of 32; K read
     # with non-temporal loads)
-    "sinkhorn_b64": int(2 * ((267595.7 + 1764.0) * 2 + 3328.0 + 1280.0) * 1024),
+    "sinkhorn_b64": int(2 * ((267134.2 + 1771.0) * 2 + 3328.0 + 1280.0) * 1024),
     # the same pair per C5 iteration (one group)
-    "sinkhorn_c5": int(((533815.9 + 8405.5) * 2 + 18453.8 + 320.0) * 1024),
+    "sinkhorn_c5": int(((533816.2 + 8411.5) * 2 + 18454.0 + 320.0) * 1024),
 }
 
 
