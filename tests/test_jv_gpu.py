@@ -15,6 +15,7 @@ import json
 import subprocess
 import sys
 import textwrap
+import zlib
 from pathlib import Path
 
 import numpy as np
@@ -99,6 +100,18 @@ def test_padded_row_runs_vs_oracle(kind, device):
                            lib.tm_jv_workspace_bytes_prefill(4, n, m), device)
         np.testing.assert_array_equal(got, jv.jv_compact_batch(c),
                                       err_msg=f"compact {kind} {c.shape}")
+
+
+@pytest.mark.parametrize("shape", [(2100, 16, 16), (2050, 64, 64), (4, 100, 130)])
+def test_signed_zero_through_statistics_pass(shape, device):
+    """-0.0 (and +0.0 beside it) on the paths that take the statistics pass
+    (B > 2048 at K <= 64, and K > 64): the pass flags -0.0, which keeps the
+    K <= 64 kernel's displacement chains off, and the mapping stays the
+    reference's."""
+    rng = np.random.default_rng(zlib.crc32(repr(shape).encode()))
+    c = jv_inputs.random_batch(rng, "signed_zero", *shape)
+    print(f"signed zero {shape}", flush=True)
+    np.testing.assert_array_equal(run_op(torch.from_numpy(c), device), jv.jv_dense_batch(c))
 
 
 @pytest.mark.parametrize("kind", jv_inputs.KINDS_XL)

@@ -63,23 +63,25 @@ jv_stats_kernel(const float *__restrict__ costs, int64_t n, JvStats *__restrict_
         status[1] = 0;  // internal-error word, raised by jv_solve_kernel
         *replays = 0;   // problems the certified path handed to the exact replay
     }
-    float mx = -finf(), mn = finf();
-    uint32_t flags = 0;
+    // Branch-free per value: the finite range as order-preserving integer
+    // keys (no canonicalising float max / min; a -0.0 ranks just below
+    // +0.0), the rare classes as lane masks on the scalar unit.
+    constexpr int kKeyNegInf = (int)0x807fffff, kKeyPosInf = 0x7f800000;
+    int kmx = kKeyNegInf, kmn = kKeyPosInf;
+    uint64_t m_nan = 0, m_pinf = 0, m_ninf = 0, m_nz = 0;
     const int64_t stride = (int64_t)gridDim.x * kStatsBlock;
     const int64_t n4 = ((uintptr_t)costs % 16 == 0) ? n / 4 : 0;
     const float4 *c4 = reinterpret_cast<const float4 *>(costs);
     auto visit = [&](float x) {
-        if (isnan(x)) {
-            flags |= kJvFlagNan;
-        } else if (isinf(x)) {
-            flags |= (x < 0.f) ? kJvFlagNegInf : kJvFlagPosInf;
-        } else {
-            flags |= kJvFlagAnyFinite;
-            if (__float_as_uint(x) == 0x80000000u)
-                flags |= kJvFlagNegZero;
-            mx = fmaxf(mx, x);
-            mn = fminf(mn, x);
-        }
+        const uint32_t b = __float_as_uint(x);
+        const int k = (int)(b ^ ((uint32_t)((int)b >> 31) & 0x7fffffffu));
+        const bool fin = (b & 0x7f800000u) != 0x7f800000u;
+        kmx = max(kmx, fin ? k : kKeyNegInf);
+        kmn = min(kmn, fin ? k : kKeyPosInf);
+        m_nan |= ballot((b & 0x7fffffffu) > 0x7f800000u);
+        m_pinf |= ballot(b == 0x7f800000u);
+        m_ninf |= ballot(b == 0xff800000u);
+        m_nz |= ballot(b == 0x80000000u);
     };
     int64_t k0 = (int64_t)blockIdx.x * kStatsBlock + threadIdx.x;
     // four loads in flight per lane before any is folded (C2: each lane's
@@ -109,14 +111,15 @@ jv_stats_kernel(const float *__restrict__ costs, int64_t n, JvStats *__restrict_
          k += stride)
         visit(costs[k]);
 
+    // the keys back to floats (an involution on the bit patterns; no finite
+    // value leaves -inf / +inf, as before)
+    float mx = __int_as_float(kmx ^ ((kmx >> 31) & 0x7fffffff));
+    float mn = __int_as_float(kmn ^ ((kmn >> 31) & 0x7fffffff));
     mx = wave_max(mx);
     mn = wave_min(mn);
-    // OR of the flags across the wave
-    uint32_t f = 0;
-#pragma unroll
-    for (int bit = 0; bit < 5; ++bit)
-        if (ballot((flags >> bit) & 1u))
-            f |= 1u << bit;
+    uint32_t f = (m_nan ? kJvFlagNan : 0u) | (m_pinf ? kJvFlagPosInf : 0u) |
+                 (m_ninf ? kJvFlagNegInf : 0u) | (m_nz ? kJvFlagNegZero : 0u) |
+                 (mx != -finf() ? kJvFlagAnyFinite : 0u);
 
     __shared__ float s_mx[kStatsBlock / 64], s_mn[kStatsBlock / 64];
     __shared__ uint32_t s_f[kStatsBlock / 64];
