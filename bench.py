@@ -79,12 +79,12 @@ MEASURED_TRAFFIC = {
     "jv_c3": int((2151.0 * 2 + 256.0) * 1024),
     # sk_fused_step + sk_col_merge_blk per C4 iteration: two batch groups of 8,
     # each one pass + one merge (K once, column sums twice)
-    "sinkhorn_c4": int(2 * ((66378.0 + 1243.0) * 2 + 2369.0 + 320.0) * 1024),
+    "sinkhorn_c4": int(2 * ((66378.0 + 1243.0) * 2 + 2369.1 + 320.0) * 1024),
     # the same per iteration of the B = 64 control (two groups of 32; K read
     # with non-temporal loads)
-    "sinkhorn_b64": int(2 * ((267134.2 + 1771.0) * 2 + 3328.0 + 1280.0) * 1024),
+    "sinkhorn_b64": int(2 * ((267124.2 + 1771.0) * 2 + 3328.0 + 1280.0) * 1024),
     # the same pair per C5 iteration (one group)
-    "sinkhorn_c5": int(((533816.2 + 8411.5) * 2 + 18454.0 + 320.0) * 1024),
+    "sinkhorn_c5": int(((533822.9 + 8411.5) * 2 + 18453.4 + 320.0) * 1024),
 }
 
 
