@@ -102,6 +102,17 @@ def test_padded_row_runs_vs_oracle(kind, device):
                                       err_msg=f"compact {kind} {c.shape}")
 
 
+@pytest.mark.parametrize("seed", [1, 2, 3])
+def test_c3_shape_other_seeds_vs_oracle(seed, device):
+    """The C3 configuration (64, 512, 768), squared distances with 20 % +inf,
+    at seeds beside the golden batch's: 256 padded rows per problem, so the
+    row reduction's padded runs and the padded start rows' list run at full
+    size."""
+    c = workloads.jv_rect_masked(seed=seed)
+    print(f"C3 shape seed {seed}", flush=True)
+    np.testing.assert_array_equal(run_op(c, device), jv.jv_dense_batch(c.numpy()))
+
+
 @pytest.mark.parametrize("shape", [(2100, 16, 16), (2050, 64, 64), (4, 100, 130)])
 def test_signed_zero_through_statistics_pass(shape, device):
     """-0.0 (and +0.0 beside it) on the paths that take the statistics pass

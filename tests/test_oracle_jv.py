@@ -111,6 +111,14 @@ def test_oracle_matches_reference_build_on_prefill_gpu_inputs(kind):
 
 
 @pytest.mark.skipif(not jv.ref_available(), reason="reference build (oracle/_ref) absent")
+@pytest.mark.parametrize("seed", [1, 2, 3])
+def test_oracle_matches_reference_build_on_c3_seeds(seed):
+    """The C3-shape batches of the GPU test beside the golden one."""
+    c = workloads.jv_rect_masked(seed=seed).numpy()
+    np.testing.assert_array_equal(jv.jv_dense_batch(c), jv.ref_jv_dense_batch(c))
+
+
+@pytest.mark.skipif(not jv.ref_available(), reason="reference build (oracle/_ref) absent")
 @pytest.mark.parametrize("kind", jv_inputs.KINDS_PADDED)
 def test_oracle_matches_reference_build_on_padded_gpu_inputs(kind):
     """The batches of the GPU padded-row-run test, dense and compact."""
